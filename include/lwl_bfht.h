@@ -1,0 +1,137 @@
+/*
+ * lwl_bfht.h — C ABI of the MI355X (gfx950) BlockFHT library (liblwl_bfht.so).
+ *
+ * BlockFHT generates a long vector from a short latent: the latent (length n)
+ * is zero-padded to B = next_power_of_two(n), and block b of the output is
+ *
+ *     y_b = D_{b,L} H D_{b,L-1} H ... H D_{b,0} pad(latent)
+ *
+ * with H the Sylvester-ordered Walsh-Hadamard transform divided by sqrt(B) and
+ * D_{b,l} = diag(+-1) taken from one 32-bit hash word per 32 positions:
+ * sign(p) = bit (p & 31) of lowbias32(mix(seed, b, l, p >> 5)), set = +1.
+ * Output coordinate g lives in block g / B at position g % B.
+ *
+ * Every entry point is asynchronous on `stream` (a hipStream_t; pass the
+ * caller's current stream), never allocates device memory, never synchronizes
+ * the host, and is reentrant.  Device buffers are borrowed; scratch memory is
+ * passed in as `workspace` (256-byte aligned) of at least the size the
+ * matching *_workspace_size() query returns for the same arguments.
+ *
+ * Return value: LWL_OK (0) or a negative LWL_ERR_* code; lwl_last_error()
+ * returns the message of the calling thread's last failure.
+ *
+ * Element types: the latent, the generated output and their gradients share
+ * one dtype (LWL_DTYPE_*).  All arithmetic is float32 except in the explicitly
+ * fast-math paths documented per entry point.
+ */
+#ifndef LWL_BFHT_H
+#define LWL_BFHT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum lwl_dtype { LWL_DTYPE_F32 = 0, LWL_DTYPE_F16 = 1, LWL_DTYPE_BF16 = 2 };
+
+enum lwl_status {
+  LWL_OK = 0,
+  LWL_ERR_INVALID = -1,     /* bad argument value (the reference raises ValueError/RuntimeError) */
+  LWL_ERR_UNSUPPORTED = -2, /* valid request outside what the kernels implement */
+  LWL_ERR_WORKSPACE = -3,   /* workspace missing or smaller than the query returned */
+  LWL_ERR_HIP = -4          /* HIP runtime error while launching */
+};
+
+/* Largest block size (after padding) the library transforms: 2^23, as the
+ * reference's kGlobalMaxBlockSize (csrc/block_fht_ext_cuda.cu:15).  The
+ * reference's lower bound 2^5 (.cu:528) is lifted: any n >= 1 works. */
+#define LWL_BFHT_MAX_BLOCK_SIZE (1LL << 23)
+
+/* Message of the calling thread's last failure ("" if none). */
+const char* lwl_last_error(void);
+
+/* ABI revision of this header; bumped on any signature change. */
+int lwl_abi_version(void);
+
+/* ---------------------------------------------------------------- forward
+ * Replaces ext.forward (reference csrc/block_fht_ext.cpp:28-38 ->
+ * csrc/block_fht_ext_cuda.cu:516-566), called from
+ * latent_weight_lab/block_fht.py:170.
+ *
+ * Writes out[g - start] = y[g] for g in [start, stop), stop - start elements
+ * of `dtype`.  Checks (messages follow the reference): 0 <= start <= stop <=
+ * output_size ("invalid slice", .cu:524), layers in {1,2,3} (.cu:525),
+ * 1 <= latent_size and B <= 2^23 (.cu:528).
+ *
+ * dtype F32: float32 arithmetic.  dtype BF16/F16: loads/stores in the 16-bit
+ * type, float32 arithmetic.
+ */
+size_t lwl_bfht_forward_workspace_size(int64_t latent_size, int64_t output_size, int64_t start,
+                                       int64_t stop);
+int lwl_bfht_forward(const void* latent, int dtype, int64_t latent_size, int64_t output_size,
+                     int64_t layers, int64_t seed, int64_t start, int64_t stop, void* out,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Host-only argument check of lwl_bfht_forward (no GPU needed). */
+int lwl_bfht_check_forward(int dtype, int64_t latent_size, int64_t output_size, int64_t layers,
+                           int64_t start, int64_t stop);
+
+/* ---------------------------------------------------------------- backward
+ * Replaces ext.backward (reference csrc/block_fht_ext.cpp:40-51 ->
+ * csrc/block_fht_ext_cuda.cu:568-622), called from block_fht.py:184 and :223.
+ *
+ * Overwrites grad_latent[0 .. latent_size) with the adjoint of the forward
+ * slice applied to grad_out (stop - start elements):
+ *     grad_latent[p] = sum_b [D_{b,0} H D_{b,1} ... H D_{b,L} scatter_b(grad_out)][p].
+ * The sum over blocks runs in a fixed order (deterministic, unlike the
+ * reference's atomicAdd at .cu:221,493).  grad_out and grad_latent have `dtype`.
+ */
+size_t lwl_bfht_backward_workspace_size(int64_t latent_size, int64_t output_size, int64_t start,
+                                        int64_t stop);
+int lwl_bfht_backward(const void* grad_out, int dtype, int64_t latent_size, int64_t output_size,
+                      int64_t layers, int64_t seed, int64_t start, int64_t stop, void* grad_latent,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- fused linear
+ * Replaces ext.linear_forward (reference csrc/block_fht_ext.cpp:53-67 ->
+ * csrc/block_fht_ext_cuda.cu:624-681), called from block_fht.py:274.
+ *
+ * out[t, o] = weight_scale * sum_i input[t, i] * W[o, i], W[o, i] = y[o * in + i]
+ * with y generated from `latent` over size = in_features * out_features.
+ * input is row-major [tokens, in_features], out row-major [tokens, out_features],
+ * both `dtype`, as the latent.  W is generated on chip, block by block, and
+ * never written to memory.  Unlike the reference (.cu:639-642) any in_features
+ * <= B works (rows may straddle blocks; partial rows are summed in a fixed
+ * order through the workspace).  B <= 2^15.
+ *
+ * dtype BF16/F16: the generated weight is rounded to the I/O type and the
+ * contraction runs on MFMA with float32 accumulation.  dtype F32: float32
+ * MFMA, float32 accumulation.
+ */
+size_t lwl_bfht_linear_forward_workspace_size(int64_t tokens, int64_t in_features,
+                                              int64_t out_features, int64_t latent_size);
+int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, int64_t tokens,
+                            int64_t in_features, int64_t latent_size, int64_t out_features,
+                            int64_t layers, int64_t seed, double weight_scale, void* out,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Host-only argument check of lwl_bfht_linear_forward (no GPU needed). */
+int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features,
+                                  int64_t latent_size, int64_t out_features, int64_t layers);
+
+/* ---------------------------------------------------------------- sign words
+ * Parity probe for the device hash (reference device functions
+ * csrc/block_fht_ext_cuda.cu:27-43; Python twin block_fht.py:36-52):
+ * out[i] = sign_word(seed, block, layer, first_word + i), computed on the GPU
+ * by the same inlined code the transform kernels use.  out: nwords uint32.
+ */
+int lwl_bfht_sign_words(int64_t seed, int64_t block, int64_t layer, int64_t first_word,
+                        int64_t nwords, uint32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LWL_BFHT_H */

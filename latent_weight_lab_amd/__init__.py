@@ -1,0 +1,38 @@
+"""latent_weight_lab_amd — the BlockFHT path of latent-weight-lab on MI355X.
+
+Public names follow the reference package ``latent_weight_lab``
+(``latent_weight_lab/__init__.py:1-23``).  The generator, its backward and the
+fused linear run in hand-written gfx950 HIP kernels (``csrc/``) behind the C
+ABI declared in ``include/lwl_bfht.h``.
+"""
+from .block_fht import (
+    BlockFHT,
+    BlockFHTLinear,
+    block_fht_grad_latent,
+    block_fht_linear_forward,
+    block_fht_slice,
+    flush_block_fht_weight_cache,
+    lowbias32,
+    next_power_of_two,
+    prepare_block_fht_weight_cache,
+    restore_block_fht_weight_cache,
+    sign_word_for,
+    signs_for,
+    suspend_block_fht_weight_cache,
+)
+
+__all__ = [
+    "BlockFHT",
+    "BlockFHTLinear",
+    "block_fht_grad_latent",
+    "block_fht_linear_forward",
+    "block_fht_slice",
+    "flush_block_fht_weight_cache",
+    "lowbias32",
+    "next_power_of_two",
+    "prepare_block_fht_weight_cache",
+    "restore_block_fht_weight_cache",
+    "sign_word_for",
+    "signs_for",
+    "suspend_block_fht_weight_cache",
+]

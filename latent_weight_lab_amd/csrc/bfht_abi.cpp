@@ -1,0 +1,265 @@
+// C ABI of liblwl_bfht.so (declared in include/lwl_bfht.h).
+//
+// Host-side only: argument validation with the reference's messages, the
+// execution plan (which kernels, how many overlapped blocks, workspace
+// layout), and translation of HIP errors.  No device memory is allocated here.
+#include "../../include/lwl_bfht.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "bfht_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return LWL_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(LWL_ERR_HIP, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+int log2_pow2_ceil(int64_t v) {
+  int l = 0;
+  while (((int64_t)1 << l) < v) ++l;
+  return l;
+}
+
+uint32_t fold_seed(int64_t seed) {
+  const uint64_t s = (uint64_t)seed;
+  return (uint32_t)s ^ (uint32_t)(s >> 32);
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool valid_dtype(int d) { return d == LWL_DTYPE_F32 || d == LWL_DTYPE_F16 || d == LWL_DTYPE_BF16; }
+
+// Checks shared by forward and backward.  Messages follow the reference:
+// block_fht.py:13-14,92-93,609-610 and block_fht_ext_cuda.cu:524-529.
+int check_common(int dtype, int64_t latent_size, int64_t output_size, int64_t layers,
+                 int64_t start, int64_t stop) {
+  if (!valid_dtype(dtype))
+    return fail(LWL_ERR_UNSUPPORTED, "Block-FHT supports float32, float16 and bfloat16 (dtype code %d)",
+                dtype);
+  if (latent_size <= 0) return fail(LWL_ERR_INVALID, "latent size must be positive");
+  if (output_size <= 0) return fail(LWL_ERR_INVALID, "size must be positive");
+  if (layers < 1 || layers > 3) return fail(LWL_ERR_INVALID, "layers must be 1, 2, or 3");
+  if (!(0 <= start && start <= stop && stop <= output_size))
+    return fail(LWL_ERR_INVALID, "invalid slice [%lld, %lld) for size %lld", (long long)start,
+                (long long)stop, (long long)output_size);
+  if (latent_size > LWL_BFHT_MAX_BLOCK_SIZE)
+    return fail(LWL_ERR_UNSUPPORTED,
+                "Block-FHT supports power-of-two block sizes up to 2^23 after padding (latent size %lld)",
+                (long long)latent_size);
+  return LWL_OK;
+}
+
+lwl::BfhtArgs plan(int dtype, int64_t latent_size, int64_t layers, int64_t seed, int64_t start,
+                   int64_t stop) {
+  lwl::BfhtArgs a{};
+  a.dtype = dtype;
+  a.n = latent_size;
+  a.log_block = log2_pow2_ceil(latent_size);
+  const int64_t B = (int64_t)1 << a.log_block;
+  a.first_block = start / B;
+  a.nblocks = stop > start ? (stop + B - 1) / B - a.first_block : 0;
+  a.start = start;
+  a.stop = stop;
+  a.seed32 = fold_seed(seed);
+  a.layers = (int)layers;
+  return a;
+}
+
+size_t forward_ws(const lwl::BfhtArgs& a) {
+  if (a.log_block <= lwl::kWholeBlockMaxLog || a.nblocks == 0) return 0;
+  return align_up((size_t)a.nblocks * ((size_t)1 << a.log_block) * sizeof(float));
+}
+
+size_t backward_ws(const lwl::BfhtArgs& a) {
+  if (a.nblocks == 0) return 0;
+  if (a.log_block <= lwl::kWholeBlockMaxLog)
+    return a.nblocks == 1 ? 0 : align_up((size_t)a.nblocks * (size_t)a.n * sizeof(float));
+  return align_up((size_t)a.nblocks * ((size_t)1 << a.log_block) * sizeof(float));
+}
+
+// Fused linear checks; messages follow block_fht_ext_cuda.cu:631-644 and
+// block_fht.py:259-260.
+int check_linear(int dtype, int64_t tokens, int64_t in_features, int64_t latent_size,
+                 int64_t out_features, int64_t layers) {
+  if (!valid_dtype(dtype))
+    return fail(LWL_ERR_UNSUPPORTED,
+                "fused linear forward supports float32, float16, and bfloat16 (dtype code %d)", dtype);
+  if (tokens < 0) return fail(LWL_ERR_INVALID, "tokens must be non-negative");
+  if (in_features <= 0) return fail(LWL_ERR_INVALID, "in_features must be positive");
+  if (out_features <= 0) return fail(LWL_ERR_INVALID, "out_features must be positive");
+  if (layers < 1 || layers > 3) return fail(LWL_ERR_INVALID, "layers must be 1, 2, or 3");
+  if (latent_size <= 0) return fail(LWL_ERR_INVALID, "latent size must be positive");
+  const int lb = log2_pow2_ceil(latent_size);
+  if (lb > lwl::kWholeBlockMaxLog)
+    return fail(LWL_ERR_UNSUPPORTED,
+                "fused linear forward supports block sizes up to 2^15 (latent size %lld)",
+                (long long)latent_size);
+  if (in_features > ((int64_t)1 << lb))
+    return fail(LWL_ERR_UNSUPPORTED, "fused linear forward requires in_features <= block_size");
+  if (in_features > lwl::kLinearMaxInFeatures)
+    return fail(LWL_ERR_UNSUPPORTED, "fused linear forward supports in_features up to %d",
+                lwl::kLinearMaxInFeatures);
+  if (!lwl::kLinearKernelAvailable)
+    return fail(LWL_ERR_UNSUPPORTED, "fused linear kernel not available in this build");
+  return LWL_OK;
+}
+
+lwl::LinearArgs plan_linear(int dtype, int64_t tokens, int64_t in_features, int64_t latent_size,
+                            int64_t out_features, int64_t layers, int64_t seed,
+                            double weight_scale) {
+  lwl::LinearArgs a{};
+  a.dtype = dtype;
+  a.tokens = tokens;
+  a.in_features = in_features;
+  a.out_features = out_features;
+  a.n = latent_size;
+  a.log_block = log2_pow2_ceil(latent_size);
+  const int64_t B = (int64_t)1 << a.log_block;
+  a.nblocks_w = (in_features * out_features + B - 1) / B;
+  a.seed32 = fold_seed(seed);
+  a.layers = (int)layers;
+  a.weight_scale = (float)weight_scale;
+  a.token_splits = lwl::linear_token_splits(a);
+  return a;
+}
+
+size_t linear_ws(const lwl::LinearArgs& a) {
+  return align_up((size_t)a.nblocks_w * 2 * (size_t)a.tokens * sizeof(float));
+}
+
+int check_workspace(size_t need, const void* ws, size_t have) {
+  if (need == 0) return LWL_OK;
+  if (ws == nullptr || have < need)
+    return fail(LWL_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                ws ? have : (size_t)0);
+  if ((uintptr_t)ws % kAlign) return fail(LWL_ERR_WORKSPACE, "workspace must be %zu-byte aligned", kAlign);
+  return LWL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* lwl_last_error(void) { return g_last_error.c_str(); }
+
+int lwl_abi_version(void) { return 1; }
+
+int lwl_bfht_check_forward(int dtype, int64_t latent_size, int64_t output_size, int64_t layers,
+                           int64_t start, int64_t stop) {
+  const int rc = check_common(dtype, latent_size, output_size, layers, start, stop);
+  return rc ? rc : ok();
+}
+
+size_t lwl_bfht_forward_workspace_size(int64_t latent_size, int64_t output_size, int64_t start,
+                                       int64_t stop) {
+  if (check_common(LWL_DTYPE_F32, latent_size, output_size, 1, start, stop)) return 0;
+  return forward_ws(plan(LWL_DTYPE_F32, latent_size, 1, 0, start, stop));
+}
+
+int lwl_bfht_forward(const void* latent, int dtype, int64_t latent_size, int64_t output_size,
+                     int64_t layers, int64_t seed, int64_t start, int64_t stop, void* out,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_common(dtype, latent_size, output_size, layers, start, stop);
+  if (rc) return rc;
+  lwl::BfhtArgs a = plan(dtype, latent_size, layers, seed, start, stop);
+  if (a.nblocks == 0) return ok();
+  if (!latent || !out) return fail(LWL_ERR_INVALID, "latent and out must be non-null");
+  rc = check_workspace(forward_ws(a), workspace, workspace_bytes);
+  if (rc) return rc;
+  a.src = latent;
+  a.dst = out;
+  a.work = workspace;
+  return hip_status(lwl::launch_bfht(a, (hipStream_t)stream, true), "lwl_bfht_forward");
+}
+
+size_t lwl_bfht_backward_workspace_size(int64_t latent_size, int64_t output_size, int64_t start,
+                                        int64_t stop) {
+  if (check_common(LWL_DTYPE_F32, latent_size, output_size, 1, start, stop)) return 0;
+  return backward_ws(plan(LWL_DTYPE_F32, latent_size, 1, 0, start, stop));
+}
+
+int lwl_bfht_backward(const void* grad_out, int dtype, int64_t latent_size, int64_t output_size,
+                      int64_t layers, int64_t seed, int64_t start, int64_t stop, void* grad_latent,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_common(dtype, latent_size, output_size, layers, start, stop);
+  if (rc) return rc;
+  lwl::BfhtArgs a = plan(dtype, latent_size, layers, seed, start, stop);
+  if (!grad_latent || (a.nblocks > 0 && !grad_out))
+    return fail(LWL_ERR_INVALID, "grad_out and grad_latent must be non-null");
+  rc = check_workspace(backward_ws(a), workspace, workspace_bytes);
+  if (rc) return rc;
+  a.src = grad_out;
+  a.dst = grad_latent;
+  a.work = workspace;
+  return hip_status(lwl::launch_bfht(a, (hipStream_t)stream, false), "lwl_bfht_backward");
+}
+
+int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features,
+                                  int64_t latent_size, int64_t out_features, int64_t layers) {
+  const int rc = check_linear(dtype, tokens, in_features, latent_size, out_features, layers);
+  return rc ? rc : ok();
+}
+
+size_t lwl_bfht_linear_forward_workspace_size(int64_t tokens, int64_t in_features,
+                                              int64_t out_features, int64_t latent_size) {
+  if (check_linear(LWL_DTYPE_F32, tokens, in_features, latent_size, out_features, 1)) return 0;
+  return linear_ws(plan_linear(LWL_DTYPE_F32, tokens, in_features, latent_size, out_features, 1, 0,
+                               1.0));
+}
+
+int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, int64_t tokens,
+                            int64_t in_features, int64_t latent_size, int64_t out_features,
+                            int64_t layers, int64_t seed, double weight_scale, void* out,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_linear(dtype, tokens, in_features, latent_size, out_features, layers);
+  if (rc) return rc;
+  if (tokens == 0) return ok();
+  if (!input || !latent || !out)
+    return fail(LWL_ERR_INVALID, "input, latent and out must be non-null");
+  lwl::LinearArgs a = plan_linear(dtype, tokens, in_features, latent_size, out_features, layers,
+                                  seed, weight_scale);
+  rc = check_workspace(linear_ws(a), workspace, workspace_bytes);
+  if (rc) return rc;
+  a.x = input;
+  a.latent = latent;
+  a.out = out;
+  a.partial = (float*)workspace;
+  return hip_status(lwl::launch_linear(a, (hipStream_t)stream), "lwl_bfht_linear_forward");
+}
+
+int lwl_bfht_sign_words(int64_t seed, int64_t block, int64_t layer, int64_t first_word,
+                        int64_t nwords, uint32_t* out, void* stream) {
+  if (nwords < 0 || first_word < 0 || (nwords > 0 && !out))
+    return fail(LWL_ERR_INVALID, "invalid sign-word request");
+  if (first_word + nwords > ((int64_t)1 << 32))
+    return fail(LWL_ERR_INVALID, "word index exceeds 32 bits");
+  return hip_status(lwl::launch_sign_words(fold_seed(seed), block, (int)layer, first_word, nwords,
+                                           out, (hipStream_t)stream),
+                    "lwl_bfht_sign_words");
+}
+
+}  // extern "C"

@@ -1,0 +1,133 @@
+// Device building blocks shared by the BlockFHT kernels (gfx950, wave64).
+//
+// Sign hash: lowbias32 avalanche over (seed, block, layer, word), one 32-bit
+// word per 32 positions; bit p&31 of word p>>5 set means +1
+// (reference latent_weight_lab/block_fht.py:36-81, csrc/block_fht_ext_cuda.cu:27-48).
+//
+// Register-resident FHT: a thread holds E = 2^LE elements in VGPRs.  A "bit
+// group" is a run of up to 5 index bits; for one group the thread holds the
+// 2^nb elements that differ only in those bits (times 2^(LE-nb) independent
+// columns), so the radix-2^nb butterflies of that group run entirely in
+// registers.  Groups are exchanged through LDS with one padding float per 32
+// (lds index p + p/32), which keeps every group access pattern below free of
+// bank conflicts for the 64 lanes of a wave.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lwl {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+
+constexpr int kTileLog = 15;  // 2^15 fp32 = 128 KiB: the largest block one workgroup holds in LDS
+constexpr int kMaxLog = 23;   // largest block size (after padding)
+
+__device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// seed32 ^ golden(block): constant per generated block.
+__device__ __forceinline__ uint32_t block_key(uint32_t seed32, int64_t block) {
+  return seed32 ^ (0x9e3779b9u * (uint32_t)(uint64_t)(block + 1));
+}
+__device__ __forceinline__ uint32_t layer_key(int layer) { return 0x85ebca6bu * (uint32_t)(layer + 1); }
+__device__ __forceinline__ uint32_t sign_word(uint32_t bkey, uint32_t lkey, uint32_t word) {
+  return lowbias32(bkey ^ lkey ^ (0xc2b2ae35u * (word + 1u)));
+}
+
+// x * (bit `bit` of `word` ? +1 : -1), as a sign-bit xor.
+__device__ __forceinline__ float signed_by(float x, uint32_t word, int bit) {
+  uint32_t flip = ((~word) >> bit) & 1u;
+  return __uint_as_float(__float_as_uint(x) ^ (flip << 31));
+}
+
+// Sign of block position p (hash per element; for passes whose layout does not
+// keep 32 consecutive positions in one thread).
+__device__ __forceinline__ float signed_at(float x, uint32_t bkey, uint32_t lkey, uint32_t p) {
+  return signed_by(x, sign_word(bkey, lkey, p >> 5), p & 31);
+}
+
+template <class T>
+__device__ __forceinline__ float to_f32(T v) {
+  return (float)v;
+}
+template <class T>
+__device__ __forceinline__ T from_f32(float v) {
+  return (T)v;
+}
+
+__device__ __forceinline__ int lds_index(int p) { return p + (p >> 5); }
+
+// Index of the element that thread t holds in register r for bit group
+// [lo, lo + nb) of an LB-bit index space, with 2^LE registers per thread.
+// Register bits below nb walk the group; the remaining register bits pick one
+// of 2^(LE-nb) columns placed above the thread index, so that for a fixed
+// register the lanes of a wave touch consecutive columns.
+template <int LB, int LE>
+__device__ __forceinline__ int group_pos(int t, int r, int lo, int nb) {
+  const int rlo = r & ((1 << nb) - 1);
+  const int c = ((r >> nb) << (LB - LE)) | t;
+  return ((c >> lo) << (lo + nb)) | (rlo << lo) | (c & ((1 << lo) - 1));
+}
+
+// Unnormalized radix-2 butterflies over register-index bits [0, nb).
+template <int E>
+__device__ __forceinline__ void butterflies(float (&v)[E], int nb) {
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    if (j < nb) {
+#pragma unroll
+      for (int r = 0; r < E; ++r) {
+        if (!(r & (1 << j)) && (r | (1 << j)) < E) {
+          const float a = v[r], b = v[r | (1 << j)];
+          v[r] = a + b;
+          v[r | (1 << j)] = a - b;
+        }
+      }
+    }
+  }
+}
+
+// Full unnormalized Walsh-Hadamard transform of an LB-bit block held as
+// v[E] per thread in the contiguous layout (thread t holds positions t*E + r),
+// using `lds` (lds_index-padded, one block) for the group exchanges.  Leaves v
+// in the same contiguous layout.  All threads of the workgroup must call it
+// (it contains barriers); `t` is the thread's index within its block.
+template <int LB, int LE>
+__device__ __forceinline__ void fht_unnormalized(float (&v)[1 << LE], float* lds, int t) {
+  constexpr int E = 1 << LE;
+  constexpr int NG = (LB + 4) / 5;
+  butterflies<E>(v, LE < 5 ? LE : 5);
+  if constexpr (NG > 1) {
+#pragma unroll
+    for (int g = 1; g < NG; ++g) {
+      const int plo = (g - 1) * 5;  // every group but the last has 5 bits
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < E; ++r) lds[lds_index(group_pos<LB, LE>(t, r, plo, 5))] = v[r];
+      __syncthreads();
+      const int lo = g * 5, nb = (g == NG - 1) ? LB - lo : 5;
+#pragma unroll
+      for (int r = 0; r < E; ++r) v[r] = lds[lds_index(group_pos<LB, LE>(t, r, lo, nb))];
+      butterflies<E>(v, nb);
+    }
+    {
+      const int lo = (NG - 1) * 5, nb = LB - lo;
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < E; ++r) lds[lds_index(group_pos<LB, LE>(t, r, lo, nb))] = v[r];
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < E; ++r) v[r] = lds[lds_index(t * E + r)];
+    }
+  }
+}
+
+}  // namespace lwl

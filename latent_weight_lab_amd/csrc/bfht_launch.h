@@ -1,0 +1,61 @@
+// Internal interface between the C ABI (bfht_abi.cpp) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <utility>
+
+namespace lwl {
+
+enum { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// Blocks up to 2^15 are transformed whole by one workgroup; larger ones go
+// through the float32 work buffer in tile passes.
+constexpr int kWholeBlockMaxLog = 15;
+
+// tile-pass prologues / epilogues
+enum { kSrcLatent = 0, kSrcGrad = 1, kSrcWorkSigned = 2, kSrcWork = 3 };
+enum { kDstWork = 0, kDstOut = 1, kDstPartial = 2 };
+
+struct BfhtArgs {
+  int dtype;
+  const void* src;     // forward: latent; backward: grad_out
+  void* dst;           // forward: out slice; backward: grad_latent
+  void* work;          // float32 scratch (see workspace sizes in bfht_abi.cpp)
+  int64_t n;           // latent size
+  int log_block;       // log2(B)
+  int64_t first_block; // first block overlapped by [start, stop)
+  int64_t nblocks;     // blocks overlapped
+  int64_t start, stop;
+  uint32_t seed32;
+  int layers;
+};
+
+hipError_t launch_bfht(const BfhtArgs& a, hipStream_t s, bool forward);
+hipError_t launch_sign_words(uint32_t seed32, int64_t block, int layer, int64_t first_word,
+                             int64_t nwords, uint32_t* out, hipStream_t s);
+
+struct LinearArgs {
+  int dtype;
+  const void* x;       // [tokens, in]
+  const void* latent;  // [n]
+  void* out;           // [tokens, out]
+  float* partial;      // [nblocks_w, 2, tokens] float32 straddling-row partials
+  int64_t tokens, in_features, out_features, n;
+  int log_block;
+  int64_t nblocks_w;   // ceil(in*out / B)
+  uint32_t seed32;
+  int layers;
+  float weight_scale;
+  int token_splits;
+};
+
+// Fused linear limits: the generated block (<= 2^15) and its row layout live
+// in LDS; in_features bounds the padded row length.
+constexpr int kLinearMaxInFeatures = 32768;
+extern const bool kLinearKernelAvailable;
+int linear_token_splits(const LinearArgs& a);
+hipError_t launch_linear(const LinearArgs& a, hipStream_t s);
+
+}  // namespace lwl

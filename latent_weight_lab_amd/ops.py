@@ -1,0 +1,111 @@
+"""Tensor-level calls into the HIP library.
+
+Each function validates devices/dtypes, allocates outputs and scratch through
+torch's caching allocator, and launches on the current stream of the
+tensors' device.  Nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native as N
+
+
+def _device_guard(device: torch.device):
+    return torch.cuda.device(device)
+
+
+def next_power_of_two(value: int) -> int:
+    """Reference ``block_fht.py:12-15``."""
+    if value <= 0:
+        raise ValueError("value must be positive")
+    return 1 << (int(value) - 1).bit_length()
+
+
+def forward(latent: torch.Tensor, size: int, layers: int, seed: int, start: int, stop: int) -> torch.Tensor:
+    """Generated coordinates ``[start, stop)`` (reference ext.forward,
+    ``csrc/block_fht_ext_cuda.cu:516-566``)."""
+    dev = N.require_cuda(latent)
+    latent = latent.contiguous()
+    code = N.dtype_code(latent.dtype)
+    L = N.lib()
+    n = latent.numel()
+    N.check(L.lwl_bfht_check_forward(code, n, size, layers, start, stop))
+    out = torch.empty(stop - start, dtype=latent.dtype, device=dev)
+    if stop == start:
+        return out
+    with _device_guard(dev):
+        ws_ptr, ws_size, ws = N.workspace(L.lwl_bfht_forward_workspace_size(n, size, start, stop), dev)
+        N.check(L.lwl_bfht_forward(latent.data_ptr(), code, n, size, layers, seed, start, stop,
+                                   out.data_ptr(), ws_ptr, ws_size, N.stream_ptr(dev)))
+    del ws
+    return out
+
+
+def backward(grad_out: torch.Tensor, latent_size: int, latent_dtype: torch.dtype, size: int, layers: int,
+             seed: int, start: int, stop: int) -> torch.Tensor:
+    """Latent gradient of the slice (reference ext.backward,
+    ``csrc/block_fht_ext_cuda.cu:568-622``), summed over blocks in a fixed order."""
+    dev = N.require_cuda(grad_out)
+    grad_out = grad_out.contiguous().to(dtype=latent_dtype)
+    if grad_out.numel() != stop - start:
+        raise N.BlockFHTArgumentError(
+            f"grad_out has {grad_out.numel()} elements, slice [{start}, {stop}) needs {stop - start}")
+    code = N.dtype_code(latent_dtype)
+    L = N.lib()
+    grad_latent = torch.empty(latent_size, dtype=latent_dtype, device=dev)
+    with _device_guard(dev):
+        ws_ptr, ws_size, ws = N.workspace(L.lwl_bfht_backward_workspace_size(latent_size, size, start, stop), dev)
+        N.check(L.lwl_bfht_backward(grad_out.data_ptr() if grad_out.numel() else 0, code, latent_size, size,
+                                    layers, seed, start, stop, grad_latent.data_ptr(), ws_ptr, ws_size,
+                                    N.stream_ptr(dev)))
+    del ws
+    return grad_latent
+
+
+def linear_supported(in_features: int, out_features: int, latent: torch.Tensor, x: torch.Tensor) -> bool:
+    """Whether the fused kernel takes this shape (else the caller materializes)."""
+    if not (x.is_cuda and latent.is_cuda and x.dtype == latent.dtype and x.dtype in N.DTYPE_CODES):
+        return False
+    return N.lib().lwl_bfht_check_linear_forward(N.dtype_code(x.dtype), max(1, x.numel() // max(1, in_features)),
+                                                 in_features, latent.numel(), out_features, 1) == N.LWL_OK
+
+
+def linear_forward(x2d: torch.Tensor, latent: torch.Tensor, out_features: int, layers: int, seed: int,
+                   weight_scale: float) -> torch.Tensor:
+    """Fused ``x @ (weight_scale * W)^T`` with W generated on chip (reference
+    ext.linear_forward, ``csrc/block_fht_ext_cuda.cu:624-681``)."""
+    dev = N.require_cuda(x2d, latent)
+    x2d = x2d.contiguous()
+    latent = latent.contiguous()
+    code = N.dtype_code(x2d.dtype)
+    if latent.dtype != x2d.dtype:
+        raise RuntimeError("block_fht_linear_forward: input and latent dtype must match")
+    tokens, in_features = x2d.shape
+    L = N.lib()
+    N.check(L.lwl_bfht_check_linear_forward(code, tokens, in_features, latent.numel(), out_features, layers))
+    out = torch.empty(tokens, out_features, dtype=x2d.dtype, device=dev)
+    if tokens == 0:
+        return out
+    with _device_guard(dev):
+        need = L.lwl_bfht_linear_forward_workspace_size(tokens, in_features, out_features, latent.numel())
+        ws_ptr, ws_size, ws = N.workspace(need, dev)
+        N.check(L.lwl_bfht_linear_forward(x2d.data_ptr(), latent.data_ptr(), code, tokens, in_features,
+                                          latent.numel(), out_features, layers, seed, float(weight_scale),
+                                          out.data_ptr(), ws_ptr, ws_size, N.stream_ptr(dev)))
+    del ws
+    return out
+
+
+def sign_words(seed: int, block: int, layer: int, nwords: int, first_word: int = 0,
+               device: torch.device | str = "cuda") -> torch.Tensor:
+    """Sign words computed by the device hash (int32 tensor holding the uint32 bits)."""
+    device = torch.device(device)
+    out = torch.empty(nwords, dtype=torch.int32, device=device)
+    with _device_guard(device):
+        N.check(N.lib().lwl_bfht_sign_words(seed, block, layer, first_word, nwords,
+                                            ctypes.cast(out.data_ptr(), ctypes.POINTER(ctypes.c_uint32)),
+                                            N.stream_ptr(device)))
+    return out

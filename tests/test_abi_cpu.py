@@ -1,0 +1,133 @@
+"""CPU-only checks of the C ABI: the library loads beside torch, exports every
+declared symbol, shares torch's HIP runtime, and validates arguments with the
+reference's messages — without launching anything."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+import torch  # noqa: F401  (must precede the library: it owns the HIP runtime)
+
+from latent_weight_lab_amd import _native as N
+from latent_weight_lab_amd import ops
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "lwl_bfht.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lwl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.lib()
+    names = declared_functions()
+    assert len(names) >= 11
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_library_shares_torch_hip_runtime():
+    N.lib()
+    maps = Path("/proc/self/maps").read_text()
+    hip_paths = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(hip_paths) == 1, hip_paths
+    assert "torch" in next(iter(hip_paths))
+
+
+def test_abi_version():
+    assert N.lib().lwl_abi_version() == 1
+
+
+@pytest.mark.parametrize(
+    "args, code, msg",
+    [
+        ((0, 1024, 108_618, 3, 1000, 2000), N.LWL_OK, ""),
+        ((2, 1, 5, 1, 0, 5), N.LWL_OK, ""),                     # B = 1 is accepted
+        ((0, 1024, 100, 3, 50, 200), N.LWL_ERR_INVALID, "invalid slice [50, 200) for size 100"),
+        ((0, 1024, 100, 3, 60, 50), N.LWL_ERR_INVALID, "invalid slice [60, 50) for size 100"),
+        ((0, 1024, 100, 3, -1, 5), N.LWL_ERR_INVALID, "invalid slice"),
+        ((0, 1024, 100, 0, 0, 5), N.LWL_ERR_INVALID, "layers must be 1, 2, or 3"),
+        ((0, 1024, 100, 4, 0, 5), N.LWL_ERR_INVALID, "layers must be 1, 2, or 3"),
+        ((0, 0, 100, 1, 0, 5), N.LWL_ERR_INVALID, "latent size must be positive"),
+        ((0, 10, 0, 1, 0, 0), N.LWL_ERR_INVALID, "size must be positive"),
+        ((0, (1 << 23) + 1, 1 << 24, 1, 0, 5), N.LWL_ERR_UNSUPPORTED, "2^23"),
+        ((7, 16, 100, 1, 0, 5), N.LWL_ERR_UNSUPPORTED, "float32, float16 and bfloat16"),
+    ],
+)
+def test_forward_validation(args, code, msg):
+    lib = N.lib()
+    assert lib.lwl_bfht_check_forward(*args) == code
+    assert msg in lib.lwl_last_error().decode()
+
+
+def test_invalid_argument_maps_to_value_and_runtime_error():
+    lib = N.lib()
+    rc = lib.lwl_bfht_check_forward(0, 16, 10, 1, 5, 11)
+    with pytest.raises(ValueError, match="invalid slice"):
+        N.check(rc)
+    rc = lib.lwl_bfht_check_forward(0, 16, 10, 1, 5, 11)
+    with pytest.raises(RuntimeError, match="invalid slice"):
+        N.check(rc)
+
+
+def test_forward_rejects_missing_workspace_without_launching():
+    lib = N.lib()
+    # B = 2^20 needs a work buffer; a null workspace must fail before any launch
+    rc = lib.lwl_bfht_forward(1, 0, 1 << 20, 1 << 21, 1, 0, 0, 10, 1, 0, 0, 0)
+    assert rc == N.LWL_ERR_WORKSPACE
+    assert "workspace" in lib.lwl_last_error().decode()
+
+
+def test_workspace_sizes():
+    lib = N.lib()
+    assert lib.lwl_bfht_forward_workspace_size(32768, 8 << 20, 0, 8 << 20) == 0
+    assert lib.lwl_bfht_forward_workspace_size(1 << 20, 1 << 26, 0, 1 << 26) == 64 * (1 << 20) * 4
+    # slice [12345, 1012345) of B=2^20 touches blocks 0..0
+    assert lib.lwl_bfht_forward_workspace_size(1 << 20, 1 << 26, 12345, 1_012_345) == (1 << 20) * 4
+    # backward small-B: one float32 partial per overlapped block (none for one block)
+    assert lib.lwl_bfht_backward_workspace_size(1024, 108_618, 1000, 2000) == 2 * 1024 * 4
+    assert lib.lwl_bfht_backward_workspace_size(1024, 108_618, 0, 1024) == 0
+    assert lib.lwl_bfht_backward_workspace_size(1 << 23, 1 << 26, 0, 1 << 26) == 8 * (1 << 23) * 4
+
+
+def test_cpu_tensors_fail_loudly():
+    from latent_weight_lab_amd import BlockFHT
+
+    bfht = BlockFHT(16, size=40, layers=1, seed=1)
+    with pytest.raises(RuntimeError, match="GPU"):
+        bfht()
+
+
+def test_module_metadata_and_validation():
+    from latent_weight_lab_amd import BlockFHT, BlockFHTLinear
+
+    # reference tests/test_block_fht.py:49-59
+    latent = torch.nn.Parameter(torch.randn(8))
+    assert BlockFHT(latent, size=40, layers=1, seed=5).latent is latent
+    assert BlockFHT(32, size=64, layers=1, seed=1).block_size == 32
+    assert BlockFHT((1 << 23) - 17, size=1 << 23, layers=1, seed=1).block_size == 1 << 23
+    with pytest.raises(ValueError):
+        BlockFHT(8, size=0)
+    with pytest.raises(ValueError):
+        BlockFHT(8, size=10, layers=4)
+    with pytest.raises(ValueError):
+        BlockFHT(torch.zeros(2, 2), size=10)
+    layer = BlockFHTLinear(768, 3072, latent_dim=32768, layers=3, seed=3)
+    assert layer.generator.block_size == 32768 and layer.generator.size == 768 * 3072
+
+
+def test_sign_word_api_matches_oracle():
+    from latent_weight_lab_amd import sign_word_for
+    from oracle import oracle as O
+
+    for args in [(999, 3, 2, 4), (-1, 0, 0, 0), (2**63 - 1, 2**32 - 1, 3, 262143), (-(2**63), 5, 1, 7)]:
+        assert sign_word_for(*args) == O.sign_word_for(*args)
+
+
+def test_next_power_of_two():
+    assert [ops.next_power_of_two(v) for v in (1, 2, 3, 1024, 1025, 20000)] == [1, 2, 4, 1024, 2048, 32768]
+    with pytest.raises(ValueError):
+        ops.next_power_of_two(0)

@@ -1,0 +1,211 @@
+"""GPU parity of the HIP generator against the CPU oracle.
+
+Bars: sign words bit-exact; float32 within 1e-5
+relative L2 of the float64 oracle; bfloat16/float16 within 1e-2 relative L2
+of the float32-exact result.  Full-size configs that the oracle cannot redo in
+seconds are checked through size-independent properties (orthogonality per
+block, adjointness, determinism) plus oracle slices.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import decode_array, gpu_available
+from latent_weight_lab_amd import BlockFHT, block_fht_grad_latent, block_fht_slice
+from latent_weight_lab_amd import ops
+from oracle import c_oracle
+from oracle import oracle as O
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 1e-2}
+
+
+def rel_l2(got, want):
+    return O.rel_l2(got, want)
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().double().cpu().numpy()
+
+
+def latent_for(n: int, seed: int, dtype=torch.float32) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(n, generator=g, dtype=torch.float32).to(dtype)
+
+
+# ---------------------------------------------------------------- sign words
+
+@pytest.mark.parametrize("seed,block,layer", [(7, 0, 0), (7, 255, 3), (-123456789, 2**31 + 3, 1),
+                                              (2**63 - 1, 2**32 - 1, 2), (-(2**63), 17, 0)])
+def test_sign_words_bit_exact(seed, block, layer):
+    nwords = 1 << 18  # a 2^23 block
+    got = ops.sign_words(seed, block, layer, nwords, device="cuda").cpu().numpy().view(np.uint32)
+    want = O.sign_words(seed, block, layer, nwords)
+    assert np.array_equal(got, want)
+
+
+def test_sign_words_match_golden(golden):
+    rows = golden["sign_words"]
+    for seed, block, layer, word, value in rows[::7]:
+        got = ops.sign_words(seed, block, layer, 1, first_word=word, device="cuda").cpu().numpy().view(np.uint32)
+        assert int(got[0]) == value
+
+
+# ---------------------------------------------------------------- golden fixtures
+
+def test_golden_slices_fp32(golden):
+    for case in golden["slices"]:
+        latent = torch.tensor(decode_array(case["latent"]), dtype=torch.float32, device="cuda", requires_grad=True)
+        args = (case["size"], case["layers"], case["seed"], case["start"], case["stop"])
+        y = block_fht_slice(latent, *args)
+        want = decode_array(case["out"])
+        if want.size == 0:
+            assert y.numel() == 0
+            continue
+        assert rel_l2(to_np(y), want) < 1e-5, case["name"]
+        y.square().sum().backward()
+        grad = to_np(latent.grad)
+        if "grad_sumsq" in case:
+            assert rel_l2(grad, decode_array(case["grad_sumsq"])) < 1e-5, case["name"]
+        else:
+            stride = case["grad_sumsq_stride"]
+            assert rel_l2(grad[::stride], decode_array(case["grad_sumsq_sampled"])) < 1e-5, case["name"]
+
+
+# ---------------------------------------------------------------- forward / backward sweeps
+
+CASES = [
+    # (n, size, layers, seed, start, stop)
+    (1, 5, 3, 11, 0, 5),                     # B = 1
+    (7, 31, 2, 123, 3, 17),                  # B = 8 (reference CPU test)
+    (17, 200, 1, -4, 0, 200),                # B = 32, ragged tail
+    (33, 1000, 3, 5, 63, 999),               # B = 64
+    (100, 2049, 2, 2**40 + 3, 1, 2049),      # B = 128
+    (300, 5000, 3, 9, 511, 4097),            # B = 512
+    (1024, 108_618, 3, 123, 0, 108_618),     # config 1 full
+    (1024, 108_618, 3, 123, 1000, 2000),     # config 1 slice
+    (2000, 9000, 1, 77, 2047, 8193),         # B = 2048
+    (4096, 8192, 1, 123, 17, 4099),          # reference smem-backend test shape
+    (5000, 40000, 2, 1, 8191, 30001),        # B = 8192
+    (16384, 50000, 3, 2, 0, 50000),          # B = 2^14
+    (20000, 65536, 1, 123, 111, 4096),       # reference global-backend test shape (B = 2^15)
+    (32768, 200_000, 3, 7, 12345, 198_765),  # B = 2^15, config-2 block size
+    (40000, 200_000, 2, 3, 1000, 150_000),   # B = 2^16: tile passes
+    ((1 << 17) - 5, 300_000, 3, -9, 70_000, 299_999),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", CASES, ids=[f"n{c[0]}_s{c[1]}_L{c[2]}" for c in CASES])
+def test_forward_backward_parity(case, dtype):
+    n, size, layers, seed, start, stop = case
+    lat = latent_for(n, n + layers, dtype)
+    lat64 = lat.double().numpy()
+    latent = lat.cuda().requires_grad_(True)
+    y = block_fht_slice(latent, size, layers, seed, start, stop)
+    assert y.dtype == dtype and y.shape == (stop - start,)
+    want = c_oracle.forward(lat64, size, layers, seed, start, stop)
+    assert rel_l2(to_np(y), want) < TOL[dtype]
+    g = torch.randn(stop - start, generator=torch.Generator().manual_seed(1)).to(dtype)
+    y.backward(g.cuda())
+    gwant = c_oracle.backward(g.double().numpy(), n, size, layers, seed, start, stop)
+    assert latent.grad.dtype == dtype
+    assert rel_l2(to_np(latent.grad), gwant) < TOL[dtype]
+
+
+def test_empty_slice_and_zero_gradient():
+    latent = latent_for(64, 1).cuda().requires_grad_(True)
+    y = block_fht_slice(latent, 1000, 2, 3, 500, 500)
+    assert y.shape == (0,)
+    g = block_fht_grad_latent(latent.detach(), torch.empty(0, device="cuda"), 1000, 2, 3, 500, 500)
+    assert torch.count_nonzero(g) == 0 and g.shape == (64,)
+
+
+def test_invalid_slice_raises_on_gpu():
+    latent = latent_for(64, 1).cuda()
+    with pytest.raises(ValueError, match="invalid slice"):
+        block_fht_slice(latent, 100, 1, 0, 50, 101)
+    with pytest.raises(RuntimeError, match="layers"):
+        block_fht_slice(latent, 100, 0, 0, 0, 10)
+
+
+# ---------------------------------------------------------------- BASELINE config 2
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_config2_full_parity(dtype):
+    """256 blocks of 2^15, layers 3, hash seed 7, latent ~N(0,1) from seed 1."""
+    torch.manual_seed(1)
+    lat = torch.randn(32768, dtype=torch.float32).to(dtype)
+    size = 8_388_608
+    latent = lat.cuda().requires_grad_(True)
+    y = block_fht_slice(latent, size, 3, 7, 0, size)
+    want = c_oracle.forward(lat.double().numpy(), size, 3, 7, 0, size)
+    assert rel_l2(to_np(y), want) < TOL[dtype]
+    g = torch.randn(size, generator=torch.Generator().manual_seed(5)).to(dtype)
+    y.backward(g.cuda())
+    gwant = c_oracle.backward(g.double().numpy(), 32768, size, 3, 7, 0, size)
+    assert rel_l2(to_np(latent.grad), gwant) < TOL[dtype]
+
+
+def test_config2_slice_and_determinism():
+    torch.manual_seed(1)
+    lat = torch.randn(32768, dtype=torch.float32)
+    start, stop = 12_345, 1_012_345
+    latent = lat.cuda()
+    y1 = ops.forward(latent, 8_388_608, 3, 7, start, stop)
+    y2 = ops.forward(latent, 8_388_608, 3, 7, start, stop)
+    assert torch.equal(y1, y2)
+    want = c_oracle.forward(lat.double().numpy(), 8_388_608, 3, 7, start, stop)
+    assert rel_l2(to_np(y1), want) < 1e-5
+    g = torch.randn(stop - start, generator=torch.Generator().manual_seed(2)).cuda()
+    b1 = ops.backward(g, 32768, torch.float32, 8_388_608, 3, 7, start, stop)
+    b2 = ops.backward(g, 32768, torch.float32, 8_388_608, 3, 7, start, stop)
+    assert torch.equal(b1, b2)  # fixed-order reduction
+
+
+# ---------------------------------------------------------------- BASELINE config 3 (multi-pass)
+
+@pytest.mark.parametrize("log_block", [20, 23])
+def test_config3_multipass(log_block):
+    """size 2^26, fp32, layers 3, hash seed 99, latent ~N(0,1) from seed 2."""
+    B = 1 << log_block
+    size = 1 << 26
+    torch.manual_seed(2)
+    lat = torch.randn(B, dtype=torch.float32)
+    latent = lat.cuda()
+    y = ops.forward(latent, size, 3, 99, 0, size)
+    # every block is an orthogonal image of the latent
+    norms = y.view(-1, B).double().norm(dim=1).cpu().numpy()
+    assert np.allclose(norms, float(lat.double().norm()), rtol=1e-5)
+    # oracle on a slice straddling blocks 1|2 and on the last block
+    for s0, s1 in [(2 * B - 777, 2 * B + 4321), (size - B, size)]:
+        want = c_oracle.forward(lat.double().numpy(), size, 3, 99, s0, s1)
+        assert rel_l2(to_np(y[s0:s1]), want) < 1e-5
+    # adjointness <T x, g> = <x, T^T g> over the full size (fp64 dot products)
+    g = torch.randn(size, generator=torch.Generator().manual_seed(3)).cuda()
+    gl = ops.backward(g, B, torch.float32, size, 3, 99, 0, size)
+    lhs = float(torch.dot(y.double(), g.double()))
+    rhs = float(torch.dot(latent.double(), gl.double()))
+    scale = float(y.double().norm() * g.double().norm())
+    assert abs(lhs - rhs) < 1e-6 * scale
+    # backward of one block vs the oracle
+    s0, s1 = 3 * B, 4 * B
+    gwant = c_oracle.backward(g[s0:s1].double().cpu().numpy(), B, size, 3, 99, s0, s1)
+    gb = ops.backward(g[s0:s1].contiguous(), B, torch.float32, size, 3, 99, s0, s1)
+    assert rel_l2(to_np(gb), gwant) < 1e-5
+
+
+def test_reference_2_23_smoke():
+    # reference tests/test_block_fht_cuda.py:34-40
+    bfht = BlockFHT((1 << 23) - 17, size=1 << 23, layers=1, seed=9).cuda()
+    out = bfht.slice(12345, 12345 + 1024)
+    out.square().mean().backward()
+    torch.cuda.synchronize()
+    assert out.shape == (1024,)
+    assert bfht.latent.grad is not None and torch.isfinite(bfht.latent.grad).all()
+    lat = bfht.latent.detach().double().cpu().numpy()
+    want = c_oracle.forward(lat, 1 << 23, 1, 9, 12345, 12345 + 1024)
+    assert rel_l2(to_np(out), want) < 1e-5
