@@ -1,0 +1,354 @@
+"""Benchmark of the BlockFHT hot path on one MI355X.
+
+Headline (BASELINE metric, config 2): full BlockFHT generation at
+block_size = 32768, layers = 3, hash seed 7, 256 blocks (8,388,608
+coordinates), bfloat16 latent/output, latent ~N(0,1) from torch seed 1.  One
+step = one call of the C ABI forward (``lwl_bfht_forward``) over the whole
+output, inputs resident in HBM.  The K timed steps are captured into one HIP
+graph and replayed once, bracketed by HIP events on the capture stream, so the
+timed region measures the GPU back to back (a Python launch costs more than
+the kernel).
+
+Printed: one JSON line with the contract keys, plus
+  roofline      algorithmic HBM bytes per launch / average launch duration;
+  cpu_baseline  the reference's CPU fallback algorithm (op-for-op torch port,
+                oracle/oracle.py) timed on this host on the same workload;
+  extra         the other configs' directions and dtypes (backward, float32,
+                slice, multi-pass 2^20 / 2^23, fused linear vs dense GEMM).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # dense
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-extra", action="store_true", help="headline only")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--only", default="", help="comma list of extra names to run (default: all)")
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------- helpers
+
+class Abi:
+    """Direct C-ABI calls on preallocated buffers (what a drop-in caller does)."""
+
+    def __init__(self):
+        import torch
+
+        from latent_weight_lab_amd import _native as N
+
+        self.torch = torch
+        self.N = N
+        self.lib = N.lib()
+
+    def stream(self):
+        return self.torch.cuda.current_stream().cuda_stream
+
+    def forward(self, latent, out, size, layers, seed, start, stop, ws=None):
+        N = self.N
+        wp, wn = (ws.data_ptr(), ws.numel()) if ws is not None else (0, 0)
+        rc = self.lib.lwl_bfht_forward(latent.data_ptr(), N.dtype_code(latent.dtype), latent.numel(), size,
+                                       layers, seed, start, stop, out.data_ptr(), wp, wn, self.stream())
+        N.check(rc)
+
+    def backward(self, grad, grad_latent, size, layers, seed, start, stop, ws=None):
+        N = self.N
+        wp, wn = (ws.data_ptr(), ws.numel()) if ws is not None else (0, 0)
+        rc = self.lib.lwl_bfht_backward(grad.data_ptr(), N.dtype_code(grad.dtype), grad_latent.numel(), size,
+                                        layers, seed, start, stop, grad_latent.data_ptr(), wp, wn, self.stream())
+        N.check(rc)
+
+    def fwd_ws(self, n, size, start, stop, device):
+        nbytes = self.lib.lwl_bfht_forward_workspace_size(n, size, start, stop)
+        return self.torch.empty(nbytes, dtype=self.torch.uint8, device=device) if nbytes else None
+
+    def bwd_ws(self, n, size, start, stop, device):
+        nbytes = self.lib.lwl_bfht_backward_workspace_size(n, size, start, stop)
+        return self.torch.empty(nbytes, dtype=self.torch.uint8, device=device) if nbytes else None
+
+
+def time_graph(torch, fn, steps: int, warmup: int) -> float:
+    """Seconds per step: `steps` calls of fn captured in one HIP graph,
+    replayed once between events recorded on the capture stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(max(1, warmup)):
+            fn()  # eager warm-up (also settles lazily-created state)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g_warm = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_warm):
+        for _ in range(max(1, warmup)):
+            fn()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(steps):
+            fn()
+    g_warm.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / 1e3 / steps
+
+
+def time_eager(torch, fn, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / 1e3 / steps
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def config2_latent(torch, dtype):
+    torch.manual_seed(1)
+    return torch.randn(32768, dtype=torch.float32).to(dtype)
+
+
+# ---------------------------------------------------------------- headline
+
+C2_N = 32768
+C2_SIZE = 8_388_608
+C2_LAYERS = 3
+C2_SEED = 7
+
+
+def headline(abi, steps, warmup):
+    torch = abi.torch
+    dt = torch.bfloat16
+    latent = config2_latent(torch, dt).cuda()
+    out = torch.empty(C2_SIZE, dtype=dt, device="cuda")
+    ws = abi.fwd_ws(C2_N, C2_SIZE, 0, C2_SIZE, "cuda")
+
+    def step():
+        abi.forward(latent, out, C2_SIZE, C2_LAYERS, C2_SEED, 0, C2_SIZE, ws)
+
+    sec = time_graph(torch, step, steps, warmup)
+    return sec, out
+
+
+# ---------------------------------------------------------------- extra configs
+
+def extra_configs(abi, steps, warmup, only):
+    torch = abi.torch
+    res = {}
+
+    def want(name):
+        return not only or name in only
+
+    def run(name, fn, nbytes, coords, graph=True, nsteps=None):
+        if not want(name):
+            return
+        try:
+            k = nsteps or steps
+            sec = time_graph(torch, fn, k, warmup) if graph else time_eager(torch, fn, k, warmup)
+            res[name] = {"ms": round(sec * 1e3, 5), "coords_per_s": coords / sec,
+                         "algo_GBs": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
+        except Exception as exc:  # noqa: BLE001 - reported, not fatal
+            res[name] = {"error": f"{type(exc).__name__}: {exc}"}
+
+    for dt, es in ((torch.bfloat16, 2), (torch.float32, 4)):
+        tag = "bf16" if dt == torch.bfloat16 else "f32"
+        latent = config2_latent(torch, dt).cuda()
+        out = torch.empty(C2_SIZE, dtype=dt, device="cuda")
+        grad = torch.randn(C2_SIZE, generator=torch.Generator().manual_seed(5)).to(dt).cuda()
+        gl = torch.empty(C2_N, dtype=dt, device="cuda")
+        bws = abi.bwd_ws(C2_N, C2_SIZE, 0, C2_SIZE, "cuda")
+        if tag == "f32":
+            run(f"c2_fwd_{tag}", lambda: abi.forward(latent, out, C2_SIZE, 3, 7, 0, C2_SIZE),
+                C2_SIZE * es + C2_N * es, C2_SIZE)
+        run(f"c2_bwd_{tag}", lambda: abi.backward(grad, gl, C2_SIZE, 3, 7, 0, C2_SIZE, bws),
+            C2_SIZE * es + C2_N * es, C2_SIZE)
+        s0, s1 = 12_345, 1_012_345
+        sl = torch.empty(s1 - s0, dtype=dt, device="cuda")
+        run(f"c2_slice_{tag}", lambda: abi.forward(latent, sl, C2_SIZE, 3, 7, s0, s1),
+            (s1 - s0) * es + C2_N * es, s1 - s0)
+        del latent, out, grad, gl, bws, sl
+
+    # config 3: multi-pass blocks 2^20 and 2^23, size 2^26, fp32, layers 3, seed 99
+    size = 1 << 26
+    for lb in (20, 23):
+        name = f"c3_b2^{lb}"
+        if not (want(name + "_fwd") or want(name + "_bwd")):
+            continue
+        B = 1 << lb
+        torch.manual_seed(2)
+        latent = torch.randn(B, dtype=torch.float32).cuda()
+        out = torch.empty(size, dtype=torch.float32, device="cuda")
+        fws = abi.fwd_ws(B, size, 0, size, "cuda")
+        run(name + "_fwd", lambda: abi.forward(latent, out, size, 3, 99, 0, size, fws), size * 4 + B * 4, size,
+            nsteps=max(5, steps // 10))
+        del fws
+        grad = torch.randn(size, generator=torch.Generator().manual_seed(3)).cuda()
+        gl = torch.empty(B, dtype=torch.float32, device="cuda")
+        bws = abi.bwd_ws(B, size, 0, size, "cuda")
+        run(name + "_bwd", lambda: abi.backward(grad, gl, size, 3, 99, 0, size, bws), size * 4 + B * 4, size,
+            nsteps=max(5, steps // 10))
+        del latent, out, grad, gl, bws
+        torch.cuda.empty_cache()
+
+    # config 4: fused linear at GPT-2-small MLP shapes vs dense bf16 GEMM on the materialized weight
+    if want("c4_linear"):
+        from latent_weight_lab_amd import block_fht_linear_forward, block_fht_slice
+
+        lin = {}
+        for inf, outf in ((768, 3072), (3072, 768)):
+            try:
+                torch.manual_seed(3)
+                latent = torch.randn(32768, dtype=torch.float32).to(torch.bfloat16).cuda()
+                x = torch.randn(4096, inf, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).cuda()
+                with torch.no_grad():
+                    w = block_fht_slice(latent, inf * outf, 3, 3, 0, inf * outf).view(outf, inf)
+                    flops = 2 * 4096 * inf * outf
+                    fused = time_eager(torch, lambda: block_fht_linear_forward(x, latent, outf, 3, 3), 20, 3)
+                    dense = time_graph(torch, lambda: torch.nn.functional.linear(x, w), 50, 5)
+                lin[f"{inf}x{outf}"] = {"fused_ms": round(fused * 1e3, 4), "dense_gemm_ms": round(dense * 1e3, 4),
+                                        "fused_over_dense": fused / dense,
+                                        "fused_tokens_per_s": 4096 / fused,
+                                        "fused_TFLOPs": flops / fused / 1e12,
+                                        "dense_TFLOPs": flops / dense / 1e12}
+            except Exception as exc:  # noqa: BLE001
+                lin[f"{inf}x{outf}"] = {"error": f"{type(exc).__name__}: {exc}"}
+        res["c4_linear"] = lin
+    return res
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(gpu_out, budget_s: float = 12.0):
+    """The reference's CPU fallback (block_fht_slice_torch, latent_weight_lab/block_fht.py:84-109),
+    restated op for op in oracle/oracle.py, timed on this host on config 2 bf16 forward."""
+    import torch
+
+    from oracle import oracle as O
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    latent = config2_latent(torch, torch.bfloat16)
+    O.torch_port_slice(latent, C2_SIZE, 3, 7, 0, 2 * C2_N)  # warm-up
+    times = []
+    y = None
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        y = O.torch_port_slice(latent, C2_SIZE, 3, 7, 0, C2_SIZE)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end and len(times) >= 1 and times[0] > budget_s:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    # The CPU result is also the checker of the GPU output timed above.
+    err = None
+    if gpu_out is not None:
+        err = O.rel_l2(gpu_out.float().cpu().double().numpy(), y.double().numpy())
+    return {
+        "value": C2_SIZE / med,
+        "unit": "coords/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"config 2 bf16 forward in full (256 blocks x 32768, layers 3, seed 7), torch CPU port of "
+                   f"block_fht_slice_torch, median of {len(times)} runs ({med:.3f} s each); "
+                   f"host {cpu_model()}, os.cpu_count()={os.cpu_count()}"),
+        "gpu_vs_cpu_rel_l2": err,
+    }
+
+
+# ---------------------------------------------------------------- main
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); BlockFHT blocks "
+              "shard across GPUs without communication, but no multi-GPU run is part of this build",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    abi = Abi()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    sec, gpu_out = headline(abi, args.steps, args.warmup)
+    wall = time.perf_counter() - t0
+    coords_per_s = C2_SIZE / sec
+    algo_bytes = C2_SIZE * 2 + C2_N * 2
+    achieved = algo_bytes / sec / 1e9
+    line = {
+        "metric": "generated coords/sec & % HBM roofline @ block 32768; fused-linear tokens/sec",
+        "value": coords_per_s,
+        "unit": "coords/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (latent ~N(0,1), torch seed 1)",
+        "config": {"workload": "config 2: BlockFHT full forward, block_size 32768, 256 blocks (8,388,608 coords), "
+                               "layers 3, hash seed 7, bf16 latent and output, f32 arithmetic",
+                   "block_size": C2_N, "blocks": C2_SIZE // C2_N, "layers": C2_LAYERS, "io_dtype": "bf16",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "hbm_roofline_pct": 100.0 * achieved / HBM_PEAK_GBS,
+        "headline_wall_s": wall,
+    }
+    if not args.no_extra:
+        only = {s for s in args.only.split(",") if s}
+        line["extra"] = extra_configs(abi, args.steps, args.warmup, only)
+        lin = line["extra"].get("c4_linear", {})
+        tok = [v.get("fused_tokens_per_s") for v in lin.values() if isinstance(v, dict) and "fused_tokens_per_s" in v]
+        if tok:
+            line["fused_linear_tokens_per_s"] = {k: v.get("fused_tokens_per_s") for k, v in lin.items()}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(gpu_out)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
