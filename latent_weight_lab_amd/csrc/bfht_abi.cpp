@@ -96,8 +96,10 @@ size_t forward_ws(const lwl::BfhtArgs& a) {
 
 size_t backward_ws(const lwl::BfhtArgs& a) {
   if (a.nblocks == 0) return 0;
+  // whole-block kernels: one float32 partial row of n values per block (the
+  // matrix-core kernel writes it even for a single block)
   if (a.log_block <= lwl::kWholeBlockMaxLog)
-    return a.nblocks == 1 ? 0 : align_up((size_t)a.nblocks * (size_t)a.n * sizeof(float));
+    return align_up((size_t)a.nblocks * (size_t)a.n * sizeof(float));
   return align_up((size_t)a.nblocks * ((size_t)1 << a.log_block) * sizeof(float));
 }
 

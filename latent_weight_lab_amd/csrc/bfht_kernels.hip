@@ -348,6 +348,13 @@ static hipError_t run_typed(const BfhtArgs& a, hipStream_t s, bool fwd) {
                        (T*)a.dst, a.n);
     return hipGetLastError();
   }
+  if (mfma15_applicable(a)) {
+    hipError_t e = launch_mfma15(a, s, fwd);
+    if (e != hipSuccess || fwd) return e;
+    hipLaunchKernelGGL((bfht_reduce_blocks<T>), dim3((unsigned)((a.n + 255) / 256)), dim3(256), 0, s,
+                       (const float*)a.work, a.nblocks, a.n, (int)a.n, (T*)a.dst);
+    return hipGetLastError();
+  }
   if (a.log_block <= kTileLog)
     return dispatch_block<T>(a.log_block, fwd, a, s, std::make_integer_sequence<int, kTileLog + 1>{});
   return run_tiles<T>(a, s, fwd);

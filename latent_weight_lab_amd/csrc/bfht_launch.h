@@ -33,6 +33,11 @@ struct BfhtArgs {
 };
 
 hipError_t launch_bfht(const BfhtArgs& a, hipStream_t s, bool forward);
+
+// Matrix-core path for bfloat16 blocks of exactly 2^15 (bfht_mfma.hip).  The
+// backward writes one float32 partial row of n values per block into `work`.
+bool mfma15_applicable(const BfhtArgs& a);
+hipError_t launch_mfma15(const BfhtArgs& a, hipStream_t s, bool forward);
 hipError_t launch_sign_words(uint32_t seed32, int64_t block, int layer, int64_t first_word,
                              int64_t nwords, uint32_t* out, hipStream_t s);
 

@@ -87,9 +87,11 @@ def test_workspace_sizes():
     assert lib.lwl_bfht_forward_workspace_size(1 << 20, 1 << 26, 0, 1 << 26) == 64 * (1 << 20) * 4
     # slice [12345, 1012345) of B=2^20 touches blocks 0..0
     assert lib.lwl_bfht_forward_workspace_size(1 << 20, 1 << 26, 12345, 1_012_345) == (1 << 20) * 4
-    # backward small-B: one float32 partial per overlapped block (none for one block)
+    # backward whole-block sizes: one float32 partial row of latent_size per overlapped block
     assert lib.lwl_bfht_backward_workspace_size(1024, 108_618, 1000, 2000) == 2 * 1024 * 4
-    assert lib.lwl_bfht_backward_workspace_size(1024, 108_618, 0, 1024) == 0
+    assert lib.lwl_bfht_backward_workspace_size(1024, 108_618, 0, 1024) == 1024 * 4
+    assert lib.lwl_bfht_backward_workspace_size(32768, 8 << 20, 0, 8 << 20) == 256 * 32768 * 4
+    assert lib.lwl_bfht_backward_workspace_size(16, 40, 3, 3) == 0
     assert lib.lwl_bfht_backward_workspace_size(1 << 23, 1 << 26, 0, 1 << 26) == 8 * (1 << 23) * 4
 
 
