@@ -21,15 +21,14 @@ OBJ_DIR = OUT_DIR / "obj"
 LIB = OUT_DIR / "liblwl_bfht.so"
 
 ARCH = "gfx950"
-COMMON_FLAGS = [
+COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}"]
+DEVICE_FLAGS = [
     f"--offload-arch={ARCH}",
-    "-O3",
-    "-std=c++17",
-    "-fPIC",
-    "-Wall",
     # Packed fp32 VALU ops (v_pk_*_f32) stay off: the kernels use scalar fp32 VALU.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    f"-I{INCLUDE}",
+    # MFMA accumulators in VGPRs (the VALU reads them directly; AGPRs would
+    # need a v_accvgpr_read per value)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
@@ -46,10 +45,8 @@ def sources() -> list[Path]:
 
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.name + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
-    if src.suffix == ".cpp":
-        cmd = [hipcc(), *[f for f in COMMON_FLAGS if not f.startswith("--offload-arch")], "-c", str(src),
-               "-o", str(obj)]
+    flags = COMMON_FLAGS + (DEVICE_FLAGS if src.suffix == ".hip" else [])
+    cmd = [hipcc(), *flags, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")

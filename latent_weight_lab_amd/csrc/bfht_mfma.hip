@@ -132,17 +132,6 @@ __device__ __forceinline__ u32x4 pack8(const f32x16& a, int base) {
   return r;
 }
 
-// Data as A operand: acc[t] <- (packed acc[t]) x H, for all 8 tiles.
-__device__ __forceinline__ void stage_rows(f32x16 (&acc)[8], const u32x4 (&h)[2]) {
-  const f32x16 zero = {};
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const u32x4 a0 = pack8(acc[t], 0), a1 = pack8(acc[t], 8);
-    f32x16 d = mfma(a0, h[0], zero);
-    acc[t] = mfma(a1, h[1], d);
-  }
-}
-
 // Stage a of a layer whose input sits in acc: sign D_layer fused into the operands.
 template <bool kOdd>
 __device__ __forceinline__ void stage_rows_signed(f32x16 (&acc)[8], const u32x4 (&h)[2],
@@ -160,30 +149,56 @@ __device__ __forceinline__ void stage_rows_signed(f32x16 (&acc)[8], const u32x4 
   }
 }
 
-// LDS exchange + stage c (data as B operand).  Chunk id of 8 packed values:
-// write side lane32 | (r&7)<<5 | l5<<8 | (r>>3)<<9 | wave<<10 (8 tiles packed),
-// read side lane32 | t<<5 | wave<<8 | l5<<10 | c<<11.
-__device__ __forceinline__ void exchange_and_stage_c(f32x16 (&acc)[8], const u32x4 (&h)[2], u32x4* lds,
-                                                     int lane32, int l5, int wave) {
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    u32x4 chunk;
-    chunk[0] = pk(acc[0][r], acc[1][r]);
-    chunk[1] = pk(acc[2][r], acc[3][r]);
-    chunk[2] = pk(acc[4][r], acc[5][r]);
-    chunk[3] = pk(acc[6][r], acc[7][r]);
-    lds[lane32 | ((r & 7) << 5) | (l5 << 8) | ((r >> 3) << 9) | (wave << 10)] = chunk;
-  }
-  __syncthreads();
+// Exchange chunk ids (16-byte chunks of 8 packed bf16, the values of the 8
+// tiles at one accumulator register r): write side lane32 + (r&7)<<5 + l5<<8 +
+// (r>>3)<<9 + wave<<10, read side lane32 + t<<5 + wave<<8 + l5<<10 + c<<11.
+// Both are a per-lane base plus a compile-time constant.  Bit 4 of the id is
+// folded into bit 0 (id ^ ((id >> 4) & 1)) so that the 4-byte writes of lanes
+// l and l+16 use different banks; 16-byte reads of 32 consecutive ids stay
+// conflict-free.
+__device__ __forceinline__ int xswz(int id) { return id ^ ((id >> 4) & 1); }
+
+// Stage b fused with the exchange writes: as soon as tiles (2v, 2v+1) are
+// transformed, dword v of all 16 chunks goes to LDS (while the next tiles'
+// MFMAs run).
+__device__ __forceinline__ void stage_rows_and_write(f32x16 (&acc)[8], const u32x4 (&h)[2],
+                                                     uint32_t* xbuf, int wbase) {
   const f32x16 zero = {};
-  const int rbase = lane32 | (wave << 8) | (l5 << 10);
+  auto write_pair = [&](int v) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      xbuf[xswz(wbase + ((r & 7) << 5) + ((r >> 3) << 9)) * 4 + v] = pk(acc[2 * v][r], acc[2 * v + 1][r]);
+  };
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int t = 2 * v + e;
+      const u32x4 a0 = pack8(acc[t], 0), a1 = pack8(acc[t], 8);
+      f32x16 d = mfma(a0, h[0], zero);
+      acc[t] = mfma(a1, h[1], d);
+    }
+    if (v > 0) write_pair(v - 1);
+  }
+  write_pair(3);
+}
+
+// Stage c (data as B operand) after the exchange: all 16 operand chunks are
+// read first, the MFMAs start as they arrive.
+__device__ __forceinline__ void read_and_stage_c(f32x16 (&acc)[8], const u32x4 (&h)[2], const u32x4* xbuf,
+                                                 int rbase) {
+  __syncthreads();
+  u32x4 b[8][2];
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const u32x4 b0 = lds[rbase | (t << 5)];
-    const u32x4 b1 = lds[rbase | (t << 5) | (1 << 11)];
-    f32x16 d = mfma(h[0], b0, zero);
-    acc[t] = mfma(h[1], b1, d);
+    b[t][0] = xbuf[xswz(rbase + (t << 5))];
+    b[t][1] = xbuf[xswz(rbase + (t << 5) + (1 << 11))];
+  }
+  const f32x16 zero = {};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    f32x16 d = mfma(h[0], b[t][0], zero);
+    acc[t] = mfma(h[1], b[t][1], d);
   }
 }
 
@@ -191,6 +206,7 @@ struct Ctx {
   int lane32, l5, wave;
   uint32_t bkey;
   uint32_t base0, base1;  // word-index bases in S0 and S1
+  int wbase, rbase;       // LDS exchange chunk-id bases
 };
 
 __device__ __forceinline__ Ctx make_ctx(uint32_t seed32, int64_t block) {
@@ -202,28 +218,61 @@ __device__ __forceinline__ Ctx make_ctx(uint32_t seed32, int64_t block) {
   x.bkey = block_key(seed32, block);
   x.base0 = (uint32_t)(x.lane32 | (x.l5 << 5) | (x.wave << 8));
   x.base1 = (uint32_t)(x.lane32 | (x.wave << 5) | (x.l5 << 7));
+  x.wbase = x.lane32 + (x.l5 << 8) + (x.wave << 10);
+  x.rbase = x.lane32 + (x.wave << 8) + (x.l5 << 10);
   return x;
 }
 
 // Block position of the first of 8 consecutive elements of load/store chunk
 // (t, c) in S0, or of chunk r in S1.
 __device__ __forceinline__ int pos_s0(const Ctx& x, int t, int c) {
-  return ((t & 1) << 3) | (((t >> 1) & 1) << 4) | (x.lane32 << 5) | (x.l5 << 10) | (c << 11) |
-         ((t >> 2) << 12) | (x.wave << 13);
+  return ((x.lane32 << 5) + (x.l5 << 10) + (x.wave << 13)) +
+         (((t & 1) << 3) + (((t >> 1) & 1) << 4) + (c << 11) + ((t >> 2) << 12));
 }
 __device__ __forceinline__ int pos_s1(const Ctx& x, int r) {
-  return ((r & 1) << 3) | (((r >> 1) & 1) << 4) | (x.lane32 << 5) | (x.wave << 10) | (x.l5 << 12) |
-         ((r >> 2) << 13);
+  return ((x.lane32 << 5) + (x.wave << 10) + (x.l5 << 12)) +
+         (((r & 1) << 3) + (((r >> 1) & 1) << 4) + ((r >> 2) << 13));
 }
 
-// Runs the L-layer chain on a block whose signed-input operands are produced by
-// `load(t, c)` (8 bf16 of S0 chunk (t, c), unsigned).  sign_layer(i) gives the
-// sign layer applied before kernel layer i (i = 0..L-1) and after the last (i = L).
-// On return acc holds the unsigned-by-final-layer result in S1 (L odd) or S0 (L even),
-// scaled by the full normalization.
-template <int L, class Load, class SignLayer>
-__device__ __forceinline__ void run_chain(f32x16 (&acc)[8], const Ctx& x, u32x4* lds, Load load,
-                                          SignLayer sign_layer) {
+// Sign words of the layer applied after the chain, for the output layout
+// (S1 when L is odd, S0 when even), optionally in the swap_idx04 pair layout.
+template <int L>
+__device__ __forceinline__ void final_words(const Ctx& x, int layer, uint32_t (&nw)[4], bool permute) {
+  const uint32_t lkey = layer_key(layer);
+  constexpr bool kOutS1 = (L % 2) == 1;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    uint32_t word;
+    if (kOutS1)
+      word = x.base1 | ((uint32_t)s << 8);  // s = r >> 2 (p13, p14)
+    else
+      word = x.base0 | ((uint32_t)(s & 1) << 6) | ((uint32_t)(s >> 1) << 7);  // s = c + 2*t2
+    const uint32_t w = ~sign_word(x.bkey, lkey, word);
+    nw[s] = permute ? swap_idx04(w) : w;
+  }
+}
+
+// Runs the L-layer chain on a block whose unsigned input sits in `src`
+// (src[t][c] = 8 bf16 of S0 chunk (t, c), loads possibly still in flight).
+// sign_layer(i) is the sign layer applied before kernel layer i (i < L) and
+// after the last one (i = L); the words of the latter are returned in `fin`
+// (pair layout when kFinalPairs).  On return acc holds the chain's result,
+// before that last sign layer, in S1 (L odd) or S0 (L even).  Uses both
+// exchange buffers; xbufs[L & 1] is free again for wave-local use on return.
+template <int L, bool kFinalPairs, class SignLayer>
+__device__ __forceinline__ void run_chain(f32x16 (&acc)[8], const Ctx& x, u32x4 (*xbufs)[4096],
+                                          const u32x4 (&src)[8][2], SignLayer sign_layer,
+                                          uint32_t (&fin)[4]) {
+  // Hashes and Walsh operands first: independent of the source loads.
+  uint32_t nw[L][4];
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    if (i & 1)
+      layer_words<true>(x.bkey, sign_layer(i), x.base1, nw[i]);
+    else
+      layer_words<false>(x.bkey, sign_layer(i), x.base0, nw[i]);
+  }
+  final_words<L>(x, sign_layer(L), fin, kFinalPairs);
   const int lane = threadIdx.x & 63;
   u32x4 hp4[2], hq4[2], hq8[2], hlast[2];
   walsh_operand<0, 1, 2, 3, 4>(lane, 0.25f, hp4);
@@ -242,55 +291,50 @@ __device__ __forceinline__ void run_chain(f32x16 (&acc)[8], const Ctx& x, u32x4*
   for (int i = 0; i < L; ++i) {
     const bool odd = i & 1;
     if (i == 0) {
-      uint32_t nw[4];
-      layer_words<false>(x.bkey, sign_layer(0), x.base0, nw);
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
-        u32x4 a[2] = {load(t, 0), load(t, 1)};
+        u32x4 a[2] = {src[t][0], src[t][1]};
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<false>(nw, t, c, v);
+          for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<false>(nw[0], t, c, v);
         f32x16 d = mfma(a[0], hq4[0], zero);
         acc[t] = mfma(a[1], hq4[1], d);
       }
     } else if (odd) {
-      uint32_t nw[4];
-      layer_words<true>(x.bkey, sign_layer(i), x.base1, nw);
-      stage_rows_signed<true>(acc, hp4, nw);
+      stage_rows_signed<true>(acc, hp4, nw[i]);
     } else {
-      uint32_t nw[4];
-      layer_words<false>(x.bkey, sign_layer(i), x.base0, nw);
-      stage_rows_signed<false>(acc, hq4, nw);
+      stage_rows_signed<false>(acc, hq4, nw[i]);
     }
-    stage_rows(acc, hq8);
-    if (i == L - 1)
-      exchange_and_stage_c(acc, hlast, lds, x.lane32, x.l5, x.wave);
-    else
-      exchange_and_stage_c(acc, odd ? hq4 : hp4, lds, x.lane32, x.l5, x.wave);
+    // Layer i exchanges through buffer i & 1: its previous readers (layer
+    // i - 2) are past layer i - 1's barrier.
+    u32x4* xbuf = xbufs[i & 1];
+    stage_rows_and_write(acc, hq8, reinterpret_cast<uint32_t*>(xbuf), x.wbase);
+    read_and_stage_c(acc, i == L - 1 ? hlast : (odd ? hq4 : hp4), xbuf, x.rbase);
   }
 }
 
-// Final sign words (swap_idx04 layout) for the output layout.
-template <int L>
-__device__ __forceinline__ void final_words(const Ctx& x, int layer, uint32_t (&nw)[4], bool permute) {
-  const uint32_t lkey = layer_key(layer);
-  constexpr bool kOutS1 = (L % 2) == 1;
+// Raw buffer resource over `bytes` bytes at `base`: loads past the end read 0,
+// stores past the end are dropped (offsets are 32-bit).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint32_t load16(__amdgpu_buffer_rsrc_t r, int elem) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, elem * 2, 0, 0);
+}
+
+// 8 bf16 at element `p` of a buffer holding `count` elements; elements at or
+// past `count` read as 0.
+__device__ __forceinline__ u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, int p, int count) {
+  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, p * 2, 0, 0);
+  if (p < count && p + 8 > count) {  // straddles the end: exact element loads
+    v = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    uint32_t word;
-    if (kOutS1)
-      word = x.base1 | ((uint32_t)s << 8);  // s = r >> 2 (p13, p14)
-    else
-      word = x.base0 | ((uint32_t)(s & 1) << 6) | ((uint32_t)(s >> 1) << 7);  // s = c + 2*t2
-    const uint32_t w = ~sign_word(x.bkey, lkey, word);
-    nw[s] = permute ? swap_idx04(w) : w;
+    for (int e = 0; e < 8; ++e)
+      if (p + e < count) v[e >> 1] |= load16(r, p + e) << (16 * (e & 1));
   }
-}
-
-template <class T>
-__device__ __forceinline__ u32x4 load8(const T* p) {
-  return *reinterpret_cast<const u32x4*>(p);
+  return v;
 }
 
 // ---------------------------------------------------------------- forward
@@ -300,37 +344,31 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
                                                             __bf16* __restrict__ out, int n,
                                                             int64_t first_block, int64_t start,
                                                             int64_t stop, uint32_t seed32) {
-  __shared__ u32x4 lds[4096];
+  __shared__ u32x4 xbufs[2][4096];  // layer exchanges; xbufs[L & 1] then stages the output
   const int64_t block = first_block + blockIdx.x;
   const Ctx x = make_ctx(seed32, block);
-  const uint16_t* lat16 = reinterpret_cast<const uint16_t*>(latent);
-  auto load = [&](int t, int c) -> u32x4 {
-    const int p = pos_s0(x, t, c);
-    if (p + 8 <= n) return load8(latent + p);
-    u32x4 r = {0u, 0u, 0u, 0u};
+  const auto lat_r = rsrc(latent, (uint32_t)n * 2u);
+  u32x4 src[8][2];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (p + e < n) r[e >> 1] |= (uint32_t)lat16[p + e] << (16 * (e & 1));
-    return r;
-  };
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) src[t][c] = load_chunk(lat_r, pos_s0(x, t, c), n);
   f32x16 acc[8];
-  run_chain<L>(acc, x, lds, load, [](int i) { return i; });
-
   uint32_t nw[4];
-  final_words<L>(x, L, nw, true);
+  run_chain<L, true>(acc, x, xbufs, src, [](int i) { return i; }, nw);
+
+  // block-local output range [lo, hi); out element of block position p is (base - start) + p
   const int64_t base = block * kB;
-  const bool aligned = ((start & 7) == 0);
-  uint16_t* out16 = reinterpret_cast<uint16_t*>(out);
-  auto store = [&](int p, u32x4 v) {
-    const int64_t g = base + p;
-    if (aligned && g >= start && g + 8 <= stop) {
-      *reinterpret_cast<u32x4*>(out + (g - start)) = v;
-    } else if (g + 8 > start && g < stop) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (g + e >= start && g + e < stop) out16[g + e - start] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
-    }
-  };
+  const int lo = (int)(start - base > 0 ? start - base : 0);
+  const int hi = (int)(stop - base < kB ? stop - base : kB);
+  __bf16* oblk = out + (base - start);
+  const bool full = lo == 0 && hi == kB && (((uintptr_t)oblk & 15) == 0);
+  // Each wave owns whole runs of positions (S1: 1024-element runs, S0: 8192):
+  // its signed bf16 chunks go through its own LDS region in position order
+  // (local chunk c at c ^ ((c >> 4) & 3): conflict-free both ways) and out with
+  // consecutive lanes on consecutive 16-byte chunks.  No block barrier.
+  u32x4* region = xbufs[L & 1] + x.wave * 1024;
+  auto put = [&](int local, u32x4 v) { region[local ^ ((local >> 4) & 3)] = v; };
   if constexpr (L % 2 == 1) {  // output in S1: chunk r packs tiles (t, t^1)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -340,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
         const int b = ((r >> 1) & 1) | (q << 1) | ((r & 1) << 3);
         v[q] = pk(acc[2 * q][r], acc[2 * q + 1][r]) ^ ((nw[r >> 2] << (15 - b)) & kPairSign);
       }
-      store(pos_s1(x, r), v);
+      put(((x.lane32 << 2) + (x.l5 << 7)) + ((r & 3) + ((r >> 2) << 8)), v);
     }
   } else {  // output in S0: chunk (t, c) packs registers 8c .. 8c+7
 #pragma unroll
@@ -350,8 +388,38 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
         u32x4 v = pack8(acc[t], 8 * c);
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] ^= operand_mask<false>(nw, t, c, q);
-        store(pos_s0(x, t, c), v);
+        put(((x.lane32 << 2) + (x.l5 << 7)) + ((t & 1) + (((t >> 1) & 1) << 1) + (c << 8) + ((t >> 2) << 9)), v);
       }
+  }
+  // LDS operations of one wave complete in order; keep the compiler from
+  // moving the reads above the writes.
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const auto out_r = rsrc(full ? (const void*)oblk : (const void*)out, full ? (uint32_t)(kB * 2) : 0u);
+  uint16_t* oblk16 = reinterpret_cast<uint16_t*>(oblk);
+  const int lane = threadIdx.x & 63;
+  u32x4 v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int local = i * 64 + lane;
+    v[i] = region[local ^ ((local >> 4) & 3)];
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int local = i * 64 + lane;
+    // local chunk -> block chunk: S1 local bits 0-6 | l5 (7) | r>>2 (8-9), wave at 7-8;
+    // S0 local bits 0-9, wave at 10-11
+    const int c = (L % 2 == 1)
+                      ? ((local & 127) | (x.wave << 7) | (((local >> 7) & 1) << 9) | ((local >> 8) << 10))
+                      : (local | (x.wave << 10));
+    const int p = c * 8;
+    if (full) {
+      __builtin_amdgcn_raw_buffer_store_b128(v[i], out_r, p * 2, 0, 0);
+    } else if (p + 8 > lo && p < hi) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (p + e >= lo && p + e < hi) oblk16[p + e] = (uint16_t)(v[i][e >> 1] >> (16 * (e & 1)));
+    }
   }
 }
 
@@ -364,37 +432,46 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
                                                             float* __restrict__ partial, int n,
                                                             int64_t first_block, int64_t start,
                                                             int64_t stop, uint32_t seed32) {
-  __shared__ u32x4 lds[4096];
+  __shared__ u32x4 xbufs[2][4096];
   const int64_t slot = blockIdx.x;
   const int64_t block = first_block + slot;
   const Ctx x = make_ctx(seed32, block);
   const int64_t base = block * kB;
-  const bool aligned = ((start & 7) == 0);
-  const uint16_t* g16 = reinterpret_cast<const uint16_t*>(grad);
+  const int lo = (int)(start - base > 0 ? start - base : 0);
+  const int hi = (int)(stop - base < kB ? stop - base : kB);
+  const __bf16* gblk = grad + (base - start);
+  const bool full = lo == 0 && hi == kB && (((uintptr_t)gblk & 15) == 0);
+  const auto g_r = rsrc(full ? (const void*)gblk : (const void*)grad, full ? (uint32_t)(kB * 2) : 0u);
+  const uint16_t* gblk16 = reinterpret_cast<const uint16_t*>(gblk);
   auto load = [&](int t, int c) -> u32x4 {
-    const int64_t g = base + pos_s0(x, t, c);
-    if (aligned && g >= start && g + 8 <= stop) return load8(grad + (g - start));
-    u32x4 r = {0u, 0u, 0u, 0u};
-    if (g + 8 > start && g < stop) {
+    const int p = pos_s0(x, t, c);
+    if (full) return __builtin_amdgcn_raw_buffer_load_b128(g_r, p * 2, 0, 0);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (p + 8 > lo && p < hi) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (g + e >= start && g + e < stop) r[e >> 1] |= (uint32_t)g16[g + e - start] << (16 * (e & 1));
+        if (p + e >= lo && p + e < hi) v[e >> 1] |= (uint32_t)gblk16[p + e] << (16 * (e & 1));
     }
-    return r;
+    return v;
   };
+  u32x4 src[8][2];
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) src[t][c] = load(t, c);
   f32x16 acc[8];
-  run_chain<L>(acc, x, lds, load, [](int i) { return L - i; });
-
   uint32_t nw[4];
-  final_words<L>(x, 0, nw, false);
+  run_chain<L, false>(acc, x, xbufs, src, [](int i) { return L - i; }, nw);
+
   float* prow = partial + slot * (int64_t)n;
+  const auto p_r = rsrc(prow, (uint32_t)n * 4u);
   auto flip = [](float v, uint32_t w, int b) {
     return __uint_as_float(__float_as_uint(v) ^ ((w << (31 - b)) & 0x80000000u));
   };
   auto store = [&](int p, const float (&v)[8]) {
     if (p + 8 <= n) {
-      *reinterpret_cast<f32x4*>(prow + p) = f32x4{v[0], v[1], v[2], v[3]};
-      *reinterpret_cast<f32x4*>(prow + p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+      __builtin_amdgcn_raw_buffer_store_b128(f32x4{v[0], v[1], v[2], v[3]}, p_r, p * 4, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(f32x4{v[4], v[5], v[6], v[7]}, p_r, p * 4 + 16, 0, 0);
     } else if (p < n) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
@@ -426,8 +503,9 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
 }  // namespace
 
 bool mfma15_applicable(const BfhtArgs& a) {
-  // 16-byte vector loads/stores of the latent, grad and output need aligned bases.
-  const bool aligned = ((uintptr_t)a.src % 16 == 0) && ((uintptr_t)a.dst % 16 == 0);
+  // 16-byte vector loads of the latent and the partial rows need aligned bases;
+  // output and grad alignment is checked per block in the kernels.
+  const bool aligned = ((uintptr_t)a.src % 16 == 0) && (a.work == nullptr || (uintptr_t)a.work % 16 == 0);
   return a.dtype == kBF16 && a.log_block == kLog && a.nblocks > 0 && a.n <= kB && aligned;
 }
 
