@@ -47,6 +47,9 @@ def parse_args():
     p.add_argument("--only", default="", help="comma list of extra names to run (default: all)")
     p.add_argument("--eager", action="store_true",
                    help="time the headline with eager launches instead of one graph replay (for counter runs)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a 64 MiB device-to-device copy 20 times (reference kernel for the HBM byte "
+                        "counters: FETCH_SIZE/WRITE_SIZE per dispatch vs 64 MiB read and written)")
     return p.parse_args()
 
 
@@ -131,6 +134,19 @@ def time_eager(torch, fn, steps: int, warmup: int) -> float:
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / 1e3 / steps
+
+
+def profiled_traffic(name: str):
+    """HBM bytes per launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, each scaled by the same
+    counter on a plain copy of known size), read from the committed summary in profiles/."""
+    path = ROOT / "profiles" / name
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def cpu_model() -> str:
@@ -310,6 +326,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").random_(0, 255)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": 64 << 20, "calls": 20}))
+        return
     abi = Abi()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -336,7 +360,8 @@ def main():
                    "block_size": C2_N, "blocks": C2_SIZE // C2_N, "layers": C2_LAYERS, "io_dtype": "bf16",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": profiled_traffic("bfht_mfma15_fwd_c2_bf16.md")},
         "hbm_roofline_pct": 100.0 * achieved / HBM_PEAK_GBS,
         "headline_wall_s": wall,
     }

@@ -1,36 +1,38 @@
 // BlockFHT at block size 2^15 on the matrix cores (gfx950, bf16 operands,
 // float32 accumulation).
 //
-// One workgroup (4 waves, one per SIMD) owns one 32768-element block; each
-// lane holds 128 values as 8 MFMA accumulator tiles of 16 floats.  The
-// normalized Hadamard transform of a layer is split over three 5-bit groups
-// of the position index (H_32768 = H_32 (x) H_32 (x) H_32), each applied as a
-// 32x32 Walsh matrix with v_mfma_f32_32x32x16_bf16:
+// One workgroup of 8 waves (two per SIMD, so one wave's MFMAs overlap the
+// other's VALU and LDS work) owns one 32768-element block; each lane holds 64
+// values as 4 MFMA accumulator tiles of 16 floats.  The normalized Hadamard
+// transform of a layer is split over three 5-bit groups of the position index
+// (H_32768 = H_32 (x) H_32 (x) H_32), each applied as a 32x32 Walsh matrix
+// with v_mfma_f32_32x32x16_bf16:
 //
-//   stage a, b: data is the A operand (rows = lane, k = lane bit 5 + 4
-//               register bits); the transformed group lands in the lane bits
-//               and the old lane bits move into the registers;
-//   stage c:    data is the B operand; its 5 bits include the two wave bits,
-//               so it is preceded by one LDS exchange (64 KiB bf16) that swaps
-//               two already-transformed bits out to the wave index.
+//   stage a, b: data is the A operand (rows = lanes 0-31, k = lane bit 5 and
+//               4 register bits); the transformed group lands in lane bits
+//               0-4 and the old lane bits move into the registers;
+//   stage c:    data is the B operand; its 5 bits include all three wave
+//               bits, so it follows one LDS exchange (64 KiB of bf16) that
+//               swaps three already-transformed bits out to the wave index.
 //
-// Slot -> position bit assignment (p0..p14; Lk = lane bit k, Rk = bit k of
-// the accumulator register index r = 0..15, Tk = bit k of the tile index,
-// Wk = wave bit k):
+// Slot -> position bit assignment (p0..p14; Lk = lane bit k, Rk = bit k of the
+// accumulator register index r = 0..15, Tk = bit k of the tile index,
+// Wk = bit k of the wave index):
 //
-//   S0 (even layer start):  L0-4 = p5-9, L5 = p10, R = p0 p1 p2 p11, T = p3 p4 p12, W = p13 p14
-//   S1 (odd layer start):   L0-4 = p5-9, L5 = p12, R = p3 p4 p13 p14, T = p0 p1 p2, W = p10 p11
+//   S0 (even layer start): L0-4 = p5-9, L5 = p10, R = p0 p1 p4 p11, T = p2 p3, W = p12 p13 p14
+//   S1 (odd layer start):  L0-4 = p5-9, L5 = p12, R = p3 p2 p13 p14, T = p0 p1, W = p4 p10 p11
 //
-// A layer started in S0 ends in S1 and vice versa, so every sign layer D_l
-// meets the five bit-in-word position bits (p0..p4) in registers: the sign
-// words (one 32-bit hash per 32 positions) are computed per lane, four per
-// layer, and applied to packed bf16 pairs as XOR masks
-// (word << (15 - b)) & 0x80008000 after a fixed permutation of the word's
-// bits that matches the pair's position bit.
+// An even layer starts in S0 and ends in S1, an odd one the reverse.  The sign
+// layers meet the five bit-in-word bits (p0..p4) in registers, except p4 at
+// S1, which is a wave bit; sign words (one 32-bit hash per 32 positions) are
+// computed per lane and applied to packed bf16 pairs as XOR masks
+// (word << (15 - b)) & 0x80008000, after a fixed permutation of the word's
+// bits that puts the pair's two positions 16 bits apart (and a wave-uniform
+// pre-shift for p4).
 //
-// The Walsh matrices use entries +-1/4, +-1/8, +-1/4 (exact in bf16); the
-// remaining 2^(-L/2) of the L-layer normalization is folded into the last
-// stage's entries (rounded to bf16, relative error <= 2^-9).
+// Walsh entries are +-1/4, +-1/8, +-1/4 (exact in bf16); the remaining
+// 2^(-L/2) of the L-layer normalization is folded into the last stage's
+// entries, rounded to bf16 (relative error <= 2^-9).
 //
 // Reference semantics: latent_weight_lab/block_fht.py:84-109 (forward) and
 // csrc/block_fht_ext_cuda.cu:185-223 (backward: the same chain with the sign
@@ -43,14 +45,23 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kLog = 15;
 constexpr int kB = 1 << kLog;
-constexpr int kThreads = 256;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTiles = 4;
+constexpr int kChunks = kB / 8;  // 16-byte chunks of 8 bf16 in one block
+// Exchange buffers: 4096 16-byte chunks with 8 bytes of padding after every
+// 16 chunks, so that the 8-byte writes of lanes l and l + 16 hit different
+// banks; two buffers back to back (132 KiB).
+constexpr int kXBufBytes = kChunks * 16 + (kChunks / 16) * 8;
+constexpr int kLdsBytes = 2 * kXBufBytes;
 constexpr uint32_t kPairSign = 0x80008000u;
 
 __device__ __forceinline__ uint32_t pk(float lo, float hi) {
@@ -63,7 +74,7 @@ __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// Sign-word bit permutations: exchange bit-index bit 0 (resp. 3) with bit 4,
+// Sign-word bit permutations exchanging bit-index bit 0 (resp. 3) with bit 4,
 // so that the two positions of a packed pair sit 16 word bits apart.
 __device__ __forceinline__ uint32_t swap_idx04(uint32_t x) {
   const uint32_t t = ((x >> 15) ^ x) & 0x0000aaaau;
@@ -74,53 +85,109 @@ __device__ __forceinline__ uint32_t swap_idx34(uint32_t x) {
   return x ^ t ^ (t << 8);
 }
 
-// Walsh operand of this lane for a 32x32 stage: entry (c, j), k = 16c + 8*(lane>>5) + j,
-// o = lane & 31, is scale * (-1)^popcount(remap(k) & o) where k bit i is o bit Mi.
-// The same registers serve as B operand (o = column) and A operand (o = row).
-template <int M0, int M1, int M2, int M3, int M4>
-__device__ __forceinline__ void walsh_operand(int lane, float scale, u32x4 (&h)[2]) {
-  const int o = lane & 31, hi = lane >> 5;
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float e[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int k = 16 * c + 8 * hi + 2 * v + s;
-        const int km = ((k & 1) << M0) | (((k >> 1) & 1) << M1) | (((k >> 2) & 1) << M2) |
-                       (((k >> 3) & 1) << M3) | (((k >> 4) & 1) << M4);
-        e[s] = (__popc(km & o) & 1) ? -scale : scale;
-      }
-      h[c][v] = pk(e[0], e[1]);
-    }
-  }
+// Walsh operands: for lane l and register pair (c, v), entries k = 16c +
+// 8*(l>>5) + 2v + {0, 1}, o = l & 31, equal scale * (-1)^popcount(remap(k) & o)
+// where remap moves k bit i to bit M[i].  The same registers serve as B operand
+// (o = column) and as A operand (o = row).  Precomputed at compile time as bf16
+// pairs for the five (permutation, scale) combinations the kernels use:
+//   Q = (0,1,3,2,4) (k bits 2 and 3 exchanged), S = (1,0,2,3,4) (bits 0 and 1);
+//   bf16 0x3e80 = 1/4, 0x3e00 = 1/8, 0x3e35 = bf16(2^-2.5), 0x3db5 = bf16(2^-3.5).
+enum { kWalshQ4, kWalshQ8, kWalshS4, kWalshSL1, kWalshSL3, kWalshSets };
+
+struct WalshTable {
+  uint32_t v[kWalshSets][64][8];
+};
+
+constexpr WalshTable make_walsh_table() {
+  WalshTable tab{};
+  const int perm[kWalshSets][5] = {{0, 1, 3, 2, 4}, {0, 1, 3, 2, 4}, {1, 0, 2, 3, 4}, {1, 0, 2, 3, 4}, {1, 0, 2, 3, 4}};
+  const uint32_t mag[kWalshSets] = {0x3e80u, 0x3e00u, 0x3e80u, 0x3e35u, 0x3db5u};
+  for (int set = 0; set < kWalshSets; ++set)
+    for (int lane = 0; lane < 64; ++lane)
+      for (int c = 0; c < 2; ++c)
+        for (int v = 0; v < 4; ++v) {
+          uint32_t word = 0;
+          for (int s = 0; s < 2; ++s) {
+            const int k = 16 * c + 8 * (lane >> 5) + 2 * v + s;
+            int km = 0;
+            for (int i = 0; i < 5; ++i) km |= ((k >> i) & 1) << perm[set][i];
+            int par = 0;
+            for (int b = km & (lane & 31); b; b >>= 1) par ^= b & 1;
+            word |= (mag[set] | (par ? 0x8000u : 0u)) << (16 * s);
+          }
+          tab.v[set][lane][4 * c + v] = word;
+        }
+  return tab;
 }
 
-// Four sign words of one layer for this lane, inverted (set bit = flip) and
-// permuted for the pair layout.  Even (S0): word index = base | c<<6 | t2<<7,
-// slot = c + 2*t2.  Odd (S1): base | v1<<8 | c<<9, slot = v1 + 2*c.
+__device__ const WalshTable kWalsh = make_walsh_table();
+
+__device__ __forceinline__ void walsh_operand(int set, int lane, u32x4 (&h)[2]) {
+  const u32x4* row = reinterpret_cast<const u32x4*>(kWalsh.v[set][lane]);
+  h[0] = row[0];
+  h[1] = row[1];
+}
+
+struct Ctx {
+  int lane32, l5, wave;
+  uint32_t bkey;
+  uint32_t base0, base1;  // sign-word index bases in S0 and S1
+  uint32_t gw0, gw1;      // 0xc2b2ae35 * (base + 1): the word term of the hash input
+  int p4;                 // position bit p4 of this wave in S1
+  int wid, rid;           // exchange chunk-id bases (write / read side)
+};
+
+__device__ __forceinline__ Ctx make_ctx(uint32_t seed32, int64_t block) {
+  Ctx x;
+  const int tid = threadIdx.x;
+  x.lane32 = tid & 31;
+  x.l5 = (tid >> 5) & 1;
+  x.wave = tid >> 6;
+  x.bkey = block_key(seed32, block);
+  // word = p >> 5.  S0 word bits: p5-9 = lane32, p10 = l5, p11 = slot, p12-14 = wave
+  x.base0 = (uint32_t)(x.lane32 | (x.l5 << 5) | (x.wave << 7));
+  // S1 word bits: p5-9 = lane32, p10-11 = wave >> 1, p12 = l5, p13-14 = slot
+  x.base1 = (uint32_t)(x.lane32 | ((x.wave >> 1) << 5) | (x.l5 << 7));
+  x.gw0 = 0xc2b2ae35u * (x.base0 + 1u);
+  x.gw1 = 0xc2b2ae35u * (x.base1 + 1u);
+  x.p4 = x.wave & 1;
+  x.wid = x.lane32 + (x.l5 << 8) + ((x.wave >> 1) << 10);
+  x.rid = x.lane32 + (x.wave << 7) + (x.l5 << 10);
+  return x;
+}
+
+// Hash word of slot s: word index base + s * 2^shift (disjoint bits, so the
+// word term 0xc2b2ae35 * (index + 1) is the lane's base term plus a constant).
+__device__ __forceinline__ uint32_t slot_word(uint32_t key, uint32_t gw, int s, int shift) {
+  return lowbias32(key ^ (gw + 0xc2b2ae35u * ((uint32_t)s << shift)));
+}
+
+// Sign words of one layer for this lane, inverted (set bit = flip) and
+// permuted for the pair layout.  S0: 2 words, slot = p11.  S1: 4 words,
+// slot = p13 + 2*p14, pre-shifted right by 8 when this wave's p4 is 1.
+
 template <bool kOdd>
-__device__ __forceinline__ void layer_words(uint32_t bkey, int layer, uint32_t base, uint32_t (&nw)[4]) {
-  const uint32_t lkey = layer_key(layer);
+__device__ __forceinline__ void layer_words(const Ctx& x, int layer, uint32_t (&nw)[4]) {
+  const uint32_t key = x.bkey ^ layer_key(layer);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const uint32_t word = kOdd ? (base | ((uint32_t)(s & 1) << 8) | ((uint32_t)(s >> 1) << 9))
-                               : (base | ((uint32_t)(s & 1) << 6) | ((uint32_t)(s >> 1) << 7));
-    const uint32_t w = ~sign_word(bkey, lkey, word);
-    nw[s] = kOdd ? swap_idx34(w) : swap_idx04(w);
+  for (int s = 0; s < (kOdd ? 4 : 2); ++s) {
+    const uint32_t w = ~(kOdd ? slot_word(key, x.gw1, s, 8) : slot_word(key, x.gw0, s, 6));
+    nw[s] = kOdd ? (swap_idx34(w) >> (8 * x.p4)) : swap_idx04(w);
   }
+  if (!kOdd) nw[2] = nw[3] = 0;
 }
 
-// XOR mask of stage-a operand VGPR v of tile t, instruction c.
+// XOR mask of stage-a operand VGPR v (pair j = 2v, 2v+1) of tile t, instruction c.
+//   S0: j0 = p0 (pair), j1 = p1, j2 = p4, c = p11, t = (p2, p3)
+//   S1: j0 = p3 (pair), j1 = p2, j2 = p13, c = p14, t = (p0, p1)
 template <bool kOdd>
 __device__ __forceinline__ uint32_t operand_mask(const uint32_t (&nw)[4], int t, int c, int v) {
   if (kOdd) {
-    const int b = t | ((v & 1) << 3);
+    const int b = t | ((v & 1) << 2);  // + 8*p4, folded into the word
     return (nw[(v >> 1) + 2 * c] << (15 - b)) & kPairSign;
   }
-  const int b = ((t >> 1) & 1) | (v << 1) | ((t & 1) << 3);
-  return (nw[c + 2 * (t >> 2)] << (15 - b)) & kPairSign;
+  const int b = (v >> 1) | ((v & 1) << 1) | (t << 2);
+  return (nw[c] << (15 - b)) & kPairSign;
 }
 
 __device__ __forceinline__ u32x4 pack8(const f32x16& a, int base) {
@@ -132,167 +199,111 @@ __device__ __forceinline__ u32x4 pack8(const f32x16& a, int base) {
   return r;
 }
 
-// Stage a of a layer whose input sits in acc: sign D_layer fused into the operands.
-template <bool kOdd>
-__device__ __forceinline__ void stage_rows_signed(f32x16 (&acc)[8], const u32x4 (&h)[2],
-                                                  const uint32_t (&nw)[4]) {
+// Data as A operand: acc[t] <- packed(acc[t]) x H, sign layer fused when kSigned.
+template <bool kSigned, bool kOdd>
+__device__ __forceinline__ void stage_rows(f32x16 (&acc)[kTiles], const u32x4 (&h)[2],
+                                           const uint32_t (&nw)[4]) {
   const f32x16 zero = {};
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
+  for (int t = 0; t < kTiles; ++t) {
     u32x4 a[2] = {pack8(acc[t], 0), pack8(acc[t], 8)};
+    if (kSigned) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<kOdd>(nw, t, c, v);
+        for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<kOdd>(nw, t, c, v);
+    }
     f32x16 d = mfma(a[0], h[0], zero);
     acc[t] = mfma(a[1], h[1], d);
   }
 }
 
-// Exchange chunk ids (16-byte chunks of 8 packed bf16, the values of the 8
-// tiles at one accumulator register r): write side lane32 + (r&7)<<5 + l5<<8 +
-// (r>>3)<<9 + wave<<10, read side lane32 + t<<5 + wave<<8 + l5<<10 + c<<11.
-// Both are a per-lane base plus a compile-time constant.  Bit 4 of the id is
-// folded into bit 0 (id ^ ((id >> 4) & 1)) so that the 4-byte writes of lanes
-// l and l+16 use different banks; 16-byte reads of 32 consecutive ids stay
-// conflict-free.
-__device__ __forceinline__ int xswz(int id) { return id ^ ((id >> 4) & 1); }
+// Exchange: 16-byte chunk id (12 bits) of 8 packed values; each wave writes one
+// 8-byte half (its 4 tiles at register r), the half being wave bit 0:
+//   write: id = lane32 + (r&7)<<5 + l5<<8 + (r>>3)<<9 + (wave>>1)<<10, half = wave & 1
+//   read:  id = lane32 + t<<5 + wave<<7 + l5<<10 + c<<11 (whole chunk = B operand)
+// 8-byte slot of (id, half) in a padded buffer: 2*id + (id >> 4) + half.
+__device__ __forceinline__ int xslot(int id) { return 2 * id + (id >> 4); }
 
-// Stage b fused with the exchange writes: as soon as tiles (2v, 2v+1) are
-// transformed, dword v of all 16 chunks goes to LDS (while the next tiles'
-// MFMAs run).
-__device__ __forceinline__ void stage_rows_and_write(f32x16 (&acc)[8], const u32x4 (&h)[2],
-                                                     uint32_t* xbuf, int wbase) {
-  const f32x16 zero = {};
-  auto write_pair = [&](int v) {
+__device__ __forceinline__ void exchange_write(const f32x16 (&acc)[kTiles], u32x2* xbuf, const Ctx& x) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      xbuf[xswz(wbase + ((r & 7) << 5) + ((r >> 3) << 9)) * 4 + v] = pk(acc[2 * v][r], acc[2 * v + 1][r]);
-  };
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int t = 2 * v + e;
-      const u32x4 a0 = pack8(acc[t], 0), a1 = pack8(acc[t], 8);
-      f32x16 d = mfma(a0, h[0], zero);
-      acc[t] = mfma(a1, h[1], d);
-    }
-    if (v > 0) write_pair(v - 1);
+  for (int r = 0; r < 16; ++r) {
+    u32x2 v;
+    v[0] = pk(acc[0][r], acc[1][r]);
+    v[1] = pk(acc[2][r], acc[3][r]);
+    xbuf[xslot(x.wid + ((r & 7) << 5) + ((r >> 3) << 9)) + (x.wave & 1)] = v;
   }
-  write_pair(3);
 }
 
-// Stage c (data as B operand) after the exchange: all 16 operand chunks are
-// read first, the MFMAs start as they arrive.
-__device__ __forceinline__ void read_and_stage_c(f32x16 (&acc)[8], const u32x4 (&h)[2], const u32x4* xbuf,
-                                                 int rbase) {
-  __syncthreads();
-  u32x4 b[8][2];
+__device__ __forceinline__ void exchange_read_stage_c(f32x16 (&acc)[kTiles], const u32x4 (&h)[2],
+                                                      const u32x2* xbuf, const Ctx& x) {
+  u32x4 b[kTiles][2];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    b[t][0] = xbuf[xswz(rbase + (t << 5))];
-    b[t][1] = xbuf[xswz(rbase + (t << 5) + (1 << 11))];
-  }
+  for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int sl = xslot(x.rid + (t << 5) + (c << 11));
+      const u32x2 lo = xbuf[sl], hi = xbuf[sl + 1];
+      b[t][c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
   const f32x16 zero = {};
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
+  for (int t = 0; t < kTiles; ++t) {
     f32x16 d = mfma(h[0], b[t][0], zero);
     acc[t] = mfma(h[1], b[t][1], d);
   }
 }
 
-struct Ctx {
-  int lane32, l5, wave;
-  uint32_t bkey;
-  uint32_t base0, base1;  // word-index bases in S0 and S1
-  int wbase, rbase;       // LDS exchange chunk-id bases
-};
-
-__device__ __forceinline__ Ctx make_ctx(uint32_t seed32, int64_t block) {
-  Ctx x;
-  const int tid = threadIdx.x;
-  x.lane32 = tid & 31;
-  x.l5 = (tid >> 5) & 1;
-  x.wave = tid >> 6;
-  x.bkey = block_key(seed32, block);
-  x.base0 = (uint32_t)(x.lane32 | (x.l5 << 5) | (x.wave << 8));
-  x.base1 = (uint32_t)(x.lane32 | (x.wave << 5) | (x.l5 << 7));
-  x.wbase = x.lane32 + (x.l5 << 8) + (x.wave << 10);
-  x.rbase = x.lane32 + (x.wave << 8) + (x.l5 << 10);
-  return x;
-}
-
-// Block position of the first of 8 consecutive elements of load/store chunk
-// (t, c) in S0, or of chunk r in S1.
-__device__ __forceinline__ int pos_s0(const Ctx& x, int t, int c) {
-  return ((x.lane32 << 5) + (x.l5 << 10) + (x.wave << 13)) +
-         (((t & 1) << 3) + (((t >> 1) & 1) << 4) + (c << 11) + ((t >> 2) << 12));
-}
-__device__ __forceinline__ int pos_s1(const Ctx& x, int r) {
-  return ((x.lane32 << 5) + (x.wave << 10) + (x.l5 << 12)) +
-         (((r & 1) << 3) + (((r >> 1) & 1) << 4) + ((r >> 2) << 13));
-}
-
-// Sign words of the layer applied after the chain, for the output layout
-// (S1 when L is odd, S0 when even), optionally in the swap_idx04 pair layout.
+// Inverted sign words of the layer applied after the chain, in the output
+// layout (S1 when L is odd: 4 words, slot = p13 + 2*p14; S0 when L is even:
+// 2 words, slot = p11), unpermuted.
 template <int L>
-__device__ __forceinline__ void final_words(const Ctx& x, int layer, uint32_t (&nw)[4], bool permute) {
-  const uint32_t lkey = layer_key(layer);
+__device__ __forceinline__ void final_words(const Ctx& x, int layer, uint32_t (&nw)[4]) {
+  const uint32_t key = x.bkey ^ layer_key(layer);
   constexpr bool kOutS1 = (L % 2) == 1;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    uint32_t word;
-    if (kOutS1)
-      word = x.base1 | ((uint32_t)s << 8);  // s = r >> 2 (p13, p14)
-    else
-      word = x.base0 | ((uint32_t)(s & 1) << 6) | ((uint32_t)(s >> 1) << 7);  // s = c + 2*t2
-    const uint32_t w = ~sign_word(x.bkey, lkey, word);
-    nw[s] = permute ? swap_idx04(w) : w;
-  }
+  for (int s = 0; s < (kOutS1 ? 4 : 2); ++s)
+    nw[s] = ~(kOutS1 ? slot_word(key, x.gw1, s, 8) : slot_word(key, x.gw0, s, 6));
+  if (!kOutS1) nw[2] = nw[3] = 0;
 }
 
 // Runs the L-layer chain on a block whose unsigned input sits in `src`
-// (src[t][c] = 8 bf16 of S0 chunk (t, c), loads possibly still in flight).
-// sign_layer(i) is the sign layer applied before kernel layer i (i < L) and
-// after the last one (i = L); the words of the latter are returned in `fin`
-// (pair layout when kFinalPairs).  On return acc holds the chain's result,
-// before that last sign layer, in S1 (L odd) or S0 (L even).  Uses both
-// exchange buffers; xbufs[L & 1] is free again for wave-local use on return.
-template <int L, bool kFinalPairs, class SignLayer>
-__device__ __forceinline__ void run_chain(f32x16 (&acc)[8], const Ctx& x, u32x4 (*xbufs)[4096],
-                                          const u32x4 (&src)[8][2], SignLayer sign_layer,
+// (src[t][c] = stage-a operand of tile t, instruction c, in S0; loads may still
+// be in flight).  sign_layer(i) is the sign layer applied before kernel layer i
+// (i < L) and after the last one (i = L); the latter's words are returned in
+// `fin`.  On return acc holds the chain's result, before that last sign layer,
+// in S1 (L odd) or S0 (L even).  Layer i exchanges through buffer i & 1 of
+// `lds`: the previous readers of that buffer (layer i - 2) are past layer
+// i - 1's barrier, and buffer L & 1 needs no barrier before its next writes.
+template <int L, class SignLayer>
+__device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, unsigned char* lds,
+                                          const u32x4 (&src)[kTiles][2], SignLayer sign_layer,
                                           uint32_t (&fin)[4]) {
-  // Hashes and Walsh operands first: independent of the source loads.
   uint32_t nw[L][4];
 #pragma unroll
   for (int i = 0; i < L; ++i) {
     if (i & 1)
-      layer_words<true>(x.bkey, sign_layer(i), x.base1, nw[i]);
+      layer_words<true>(x, sign_layer(i), nw[i]);
     else
-      layer_words<false>(x.bkey, sign_layer(i), x.base0, nw[i]);
+      layer_words<false>(x, sign_layer(i), nw[i]);
   }
-  final_words<L>(x, sign_layer(L), fin, kFinalPairs);
+  final_words<L>(x, sign_layer(L), fin);
   const int lane = threadIdx.x & 63;
-  u32x4 hp4[2], hq4[2], hq8[2], hlast[2];
-  walsh_operand<0, 1, 2, 3, 4>(lane, 0.25f, hp4);
-  walsh_operand<0, 1, 3, 2, 4>(lane, 0.25f, hq4);
-  walsh_operand<0, 1, 3, 2, 4>(lane, 0.125f, hq8);
-  {
-    // last stage c: plain Walsh (even last layer) or permuted (odd), scaled by 2^(-2 - L/2)
-    const float s = (L == 1) ? 0.17677669529663688f : (L == 2) ? 0.125f : 0.08838834764831845f;
-    if ((L - 1) % 2 == 0)
-      walsh_operand<0, 1, 2, 3, 4>(lane, s, hlast);
-    else
-      walsh_operand<0, 1, 3, 2, 4>(lane, s, hlast);
-  }
+  // Stage a: Q/4 (even layers), S/4 (odd); stage b: Q/8; stage c: S/4 (even),
+  // Q/4 (odd); the last stage c carries the residual 2^(-L/2): S/4*2^-0.5
+  // (L = 1), Q/8 (L = 2), S/4*2^-1.5 (L = 3).
+  u32x4 hq4[2], hq8[2], hs4[2], hlast[2];
+  walsh_operand(kWalshQ4, lane, hq4);
+  walsh_operand(kWalshQ8, lane, hq8);
+  walsh_operand(kWalshS4, lane, hs4);
+  walsh_operand(L == 1 ? kWalshSL1 : L == 2 ? kWalshQ8 : kWalshSL3, lane, hlast);
   const f32x16 zero = {};
 #pragma unroll
   for (int i = 0; i < L; ++i) {
     const bool odd = i & 1;
     if (i == 0) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
+      for (int t = 0; t < kTiles; ++t) {
         u32x4 a[2] = {src[t][0], src[t][1]};
 #pragma unroll
         for (int c = 0; c < 2; ++c)
@@ -302,15 +313,15 @@ __device__ __forceinline__ void run_chain(f32x16 (&acc)[8], const Ctx& x, u32x4 
         acc[t] = mfma(a[1], hq4[1], d);
       }
     } else if (odd) {
-      stage_rows_signed<true>(acc, hp4, nw[i]);
+      stage_rows<true, true>(acc, hs4, nw[i]);
     } else {
-      stage_rows_signed<false>(acc, hq4, nw[i]);
+      stage_rows<true, false>(acc, hq4, nw[i]);
     }
-    // Layer i exchanges through buffer i & 1: its previous readers (layer
-    // i - 2) are past layer i - 1's barrier.
-    u32x4* xbuf = xbufs[i & 1];
-    stage_rows_and_write(acc, hq8, reinterpret_cast<uint32_t*>(xbuf), x.wbase);
-    read_and_stage_c(acc, i == L - 1 ? hlast : (odd ? hq4 : hp4), xbuf, x.rbase);
+    stage_rows<false, false>(acc, hq8, nw[i]);
+    u32x2* xbuf = reinterpret_cast<u32x2*>(lds + (i & 1) * kXBufBytes);
+    exchange_write(acc, xbuf, x);
+    __syncthreads();
+    exchange_read_stage_c(acc, i == L - 1 ? hlast : (odd ? hq4 : hs4), xbuf, x);
   }
 }
 
@@ -320,19 +331,64 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-__device__ __forceinline__ uint32_t load16(__amdgpu_buffer_rsrc_t r, int elem) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, elem * 2, 0, 0);
+// Source operands in S0 from 16-byte chunks of 8 consecutive positions:
+// chunk (t1, p4, c) holds p0..p2 for p3 = t1; its VGPR q (p1 = q&1, p2 = q>>1)
+// is VGPR (q&1) + 2*p4 of operand (tile (q>>1) + 2*t1, instruction c).
+// `load(p)` returns the 8 bf16 at block position p (a multiple of 8).
+template <class Load>
+__device__ __forceinline__ void load_source(const Ctx& x, Load load, u32x4 (&src)[kTiles][2]) {
+  const int base = (x.lane32 << 5) + (x.l5 << 10) + (x.wave << 12);
+#pragma unroll
+  for (int t1 = 0; t1 < 2; ++t1)
+#pragma unroll
+    for (int p4 = 0; p4 < 2; ++p4)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u32x4 v = load(base + ((t1 << 3) + (p4 << 4) + (c << 11)));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) src[(q >> 1) + 2 * t1][c][(q & 1) + 2 * p4] = v[q];
+      }
 }
 
-// 8 bf16 at element `p` of a buffer holding `count` elements; elements at or
-// past `count` read as 0.
-__device__ __forceinline__ u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, int p, int count) {
-  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, p * 2, 0, 0);
-  if (p < count && p + 8 > count) {  // straddles the end: exact element loads
-    v = u32x4{0u, 0u, 0u, 0u};
+// Output chunk k = 0..7 of this lane (8 consecutive positions): its block
+// position and its packed, signed content.
+//   S1 (L odd):  r = (p3, p2, p13, p14), t = (p0, p1), wave = (p4, p10, p11), l5 = p12; k = (p3, p13, p14)
+//   S0 (L even): r = (p0, p1, p4, p11), t = (p2, p3), wave = (p12, p13, p14), l5 = p10; k = (p3, p4, p11)
+template <int L>
+__device__ __forceinline__ int out_chunk_pos(const Ctx& x, int k) {
+  if constexpr (L % 2 == 1)
+    return ((k & 1) << 3) + (x.p4 << 4) + (x.lane32 << 5) + ((x.wave >> 1) << 10) + (x.l5 << 12) +
+           ((k >> 1) << 13);
+  else
+    return ((k & 1) << 3) + (((k >> 1) & 1) << 4) + (x.lane32 << 5) + (x.l5 << 10) + ((k >> 2) << 11) +
+           (x.wave << 12);
+}
+
+template <int L>
+__device__ __forceinline__ u32x4 out_chunk(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4], const Ctx& x,
+                                           int k) {
+  u32x4 v;
+  if constexpr (L % 2 == 1) {
+    // VGPR q: p1 = q&1 (tile bit 1), p2 = q>>1 (register bit 1); pair = p0 (tile bit 0).
+    // Pair-layout bit of the low element: p4 + 2p1 + 4p2 + 8p3, p4 folded into the word.
+    const int r0 = (k & 1) | ((k >> 1) << 2);
+    const uint32_t w = swap_idx04(nw[k >> 1]) >> x.p4;
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (p + e < count) v[e >> 1] |= load16(r, p + e) << (16 * (e & 1));
+    for (int q = 0; q < 4; ++q) {
+      const int r = r0 | ((q >> 1) << 1);
+      const int b = ((q & 1) << 1) | ((q >> 1) << 2) | ((k & 1) << 3);
+      v[q] = pk(acc[2 * (q & 1)][r], acc[2 * (q & 1) + 1][r]) ^ ((w << (15 - b)) & kPairSign);
+    }
+  } else {
+    // VGPR q: tile (q>>1) + 2*p3, register pair 2*(q&1) + 4*p4 + 8*p11 (+1); pair = p0.
+    const uint32_t w = swap_idx04(nw[k >> 2]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int t = (q >> 1) + 2 * (k & 1);
+      const int r = 2 * (q & 1) + 4 * ((k >> 1) & 1) + 8 * (k >> 2);
+      const int b = ((k >> 1) & 1) | ((q & 1) << 1) | ((q >> 1) << 2) | ((k & 1) << 3);
+      v[q] = pk(acc[t][r], acc[t][r + 1]) ^ ((w << (15 - b)) & kPairSign);
+    }
   }
   return v;
 }
@@ -344,75 +400,58 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
                                                             __bf16* __restrict__ out, int n,
                                                             int64_t first_block, int64_t start,
                                                             int64_t stop, uint32_t seed32) {
-  __shared__ u32x4 xbufs[2][4096];  // layer exchanges; xbufs[L & 1] then stages the output
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
   const int64_t block = first_block + blockIdx.x;
   const Ctx x = make_ctx(seed32, block);
   const auto lat_r = rsrc(latent, (uint32_t)n * 2u);
-  u32x4 src[8][2];
+  const bool tail = (n & 7) != 0;
+  const uint16_t* lat16 = reinterpret_cast<const uint16_t*>(latent);
+  u32x4 src[kTiles][2];
+  load_source(
+      x,
+      [&](int p) -> u32x4 {
+        u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(lat_r, p * 2, 0, 0);  // 0 past n
+        if (tail && p < n && p + 8 > n) {  // straddles the end of the latent: exact element loads
+          v = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) src[t][c] = load_chunk(lat_r, pos_s0(x, t, c), n);
-  f32x16 acc[8];
+          for (int e = 0; e < 8; ++e)
+            if (p + e < n) v[e >> 1] |= (uint32_t)lat16[p + e] << (16 * (e & 1));
+        }
+        return v;
+      },
+      src);
+  f32x16 acc[kTiles];
   uint32_t nw[4];
-  run_chain<L, true>(acc, x, xbufs, src, [](int i) { return i; }, nw);
+  run_chain<L>(acc, x, lds, src, [](int i) { return i; }, nw);
 
+  // The signed bf16 block goes through the free exchange buffer in position
+  // order (16-byte chunk c at c ^ ((c >> 4) & 3): conflict-free both ways) and
+  // then to memory with consecutive threads on consecutive chunks.
+  u32x4* stage = reinterpret_cast<u32x4*>(lds + (L & 1) * kXBufBytes);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int c = out_chunk_pos<L>(x, k) >> 3;
+    stage[c ^ ((c >> 4) & 3)] = out_chunk<L>(acc, nw, x, k);
+  }
+  __syncthreads();
   // block-local output range [lo, hi); out element of block position p is (base - start) + p
   const int64_t base = block * kB;
   const int lo = (int)(start - base > 0 ? start - base : 0);
   const int hi = (int)(stop - base < kB ? stop - base : kB);
   __bf16* oblk = out + (base - start);
   const bool full = lo == 0 && hi == kB && (((uintptr_t)oblk & 15) == 0);
-  // Each wave owns whole runs of positions (S1: 1024-element runs, S0: 8192):
-  // its signed bf16 chunks go through its own LDS region in position order
-  // (local chunk c at c ^ ((c >> 4) & 3): conflict-free both ways) and out with
-  // consecutive lanes on consecutive 16-byte chunks.  No block barrier.
-  u32x4* region = xbufs[L & 1] + x.wave * 1024;
-  auto put = [&](int local, u32x4 v) { region[local ^ ((local >> 4) & 3)] = v; };
-  if constexpr (L % 2 == 1) {  // output in S1: chunk r packs tiles (t, t^1)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      u32x4 v;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int b = ((r >> 1) & 1) | (q << 1) | ((r & 1) << 3);
-        v[q] = pk(acc[2 * q][r], acc[2 * q + 1][r]) ^ ((nw[r >> 2] << (15 - b)) & kPairSign);
-      }
-      put(((x.lane32 << 2) + (x.l5 << 7)) + ((r & 3) + ((r >> 2) << 8)), v);
-    }
-  } else {  // output in S0: chunk (t, c) packs registers 8c .. 8c+7
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        u32x4 v = pack8(acc[t], 8 * c);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] ^= operand_mask<false>(nw, t, c, q);
-        put(((x.lane32 << 2) + (x.l5 << 7)) + ((t & 1) + (((t >> 1) & 1) << 1) + (c << 8) + ((t >> 2) << 9)), v);
-      }
-  }
-  // LDS operations of one wave complete in order; keep the compiler from
-  // moving the reads above the writes.
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
   const auto out_r = rsrc(full ? (const void*)oblk : (const void*)out, full ? (uint32_t)(kB * 2) : 0u);
   uint16_t* oblk16 = reinterpret_cast<uint16_t*>(oblk);
-  const int lane = threadIdx.x & 63;
-  u32x4 v[16];
+  constexpr int kPer = kChunks / kThreads;
+  u32x4 v[kPer];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int local = i * 64 + lane;
-    v[i] = region[local ^ ((local >> 4) & 3)];
+  for (int i = 0; i < kPer; ++i) {
+    const int c = i * kThreads + (int)threadIdx.x;
+    v[i] = stage[c ^ ((c >> 4) & 3)];
   }
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int local = i * 64 + lane;
-    // local chunk -> block chunk: S1 local bits 0-6 | l5 (7) | r>>2 (8-9), wave at 7-8;
-    // S0 local bits 0-9, wave at 10-11
-    const int c = (L % 2 == 1)
-                      ? ((local & 127) | (x.wave << 7) | (((local >> 7) & 1) << 9) | ((local >> 8) << 10))
-                      : (local | (x.wave << 10));
-    const int p = c * 8;
+  for (int i = 0; i < kPer; ++i) {
+    const int p = (i * kThreads + (int)threadIdx.x) * 8;
     if (full) {
       __builtin_amdgcn_raw_buffer_store_b128(v[i], out_r, p * 2, 0, 0);
     } else if (p + 8 > lo && p < hi) {
@@ -432,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
                                                             float* __restrict__ partial, int n,
                                                             int64_t first_block, int64_t start,
                                                             int64_t stop, uint32_t seed32) {
-  __shared__ u32x4 xbufs[2][4096];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
   const int64_t slot = blockIdx.x;
   const int64_t block = first_block + slot;
   const Ctx x = make_ctx(seed32, block);
@@ -443,76 +482,85 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
   const bool full = lo == 0 && hi == kB && (((uintptr_t)gblk & 15) == 0);
   const auto g_r = rsrc(full ? (const void*)gblk : (const void*)grad, full ? (uint32_t)(kB * 2) : 0u);
   const uint16_t* gblk16 = reinterpret_cast<const uint16_t*>(gblk);
-  auto load = [&](int t, int c) -> u32x4 {
-    const int p = pos_s0(x, t, c);
-    if (full) return __builtin_amdgcn_raw_buffer_load_b128(g_r, p * 2, 0, 0);
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (p + 8 > lo && p < hi) {
+  u32x4 src[kTiles][2];
+  load_source(
+      x,
+      [&](int p) -> u32x4 {
+        if (full) return __builtin_amdgcn_raw_buffer_load_b128(g_r, p * 2, 0, 0);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (p + 8 > lo && p < hi) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (p + e >= lo && p + e < hi) v[e >> 1] |= (uint32_t)gblk16[p + e] << (16 * (e & 1));
-    }
-    return v;
-  };
-  u32x4 src[8][2];
-#pragma unroll
-  for (int t = 0; t < 8; ++t)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) src[t][c] = load(t, c);
-  f32x16 acc[8];
+          for (int e = 0; e < 8; ++e)
+            if (p + e >= lo && p + e < hi) v[e >> 1] |= (uint32_t)gblk16[p + e] << (16 * (e & 1));
+        }
+        return v;
+      },
+      src);
+  f32x16 acc[kTiles];
   uint32_t nw[4];
-  run_chain<L, false>(acc, x, xbufs, src, [](int i) { return L - i; }, nw);
+  run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
 
-  float* prow = partial + slot * (int64_t)n;
-  const auto p_r = rsrc(prow, (uint32_t)n * 4u);
+  // D_0, then the float32 partial row of the first n positions, staged through
+  // the exchange space (128 KiB; 4-float chunk c at c ^ ((c >> 4) & 15)).
   auto flip = [](float v, uint32_t w, int b) {
     return __uint_as_float(__float_as_uint(v) ^ ((w << (31 - b)) & 0x80000000u));
   };
-  auto store = [&](int p, const float (&v)[8]) {
-    if (p + 8 <= n) {
-      __builtin_amdgcn_raw_buffer_store_b128(f32x4{v[0], v[1], v[2], v[3]}, p_r, p * 4, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b128(f32x4{v[4], v[5], v[6], v[7]}, p_r, p * 4 + 16, 0, 0);
+  f32x4* stage = reinterpret_cast<f32x4*>(lds);  // 128 KiB of the 132
+  __syncthreads();  // every wave has read its last exchange
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    f32x4 v;
+    int p;
+    if constexpr (L % 2 == 1) {
+      // S1: chunk = the 4 tiles at register r (p0, p1 = tile bits)
+      p = (((r >> 1) & 1) << 2) + ((r & 1) << 3) + (x.p4 << 4) + (x.lane32 << 5) + ((x.wave >> 1) << 10) +
+          (x.l5 << 12) + ((r >> 2) << 13);
+      const uint32_t w = nw[r >> 2];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] = flip(acc[t][r], w, (p & 31) + t);
+    } else {
+      // S0: chunk = registers r0 .. r0+3 of tile t (p0, p1 = register bits)
+      const int t = r & 3, r0 = (r >> 2) << 2;
+      p = (t << 2) + (((r0 >> 2) & 1) << 4) + (x.lane32 << 5) + (x.l5 << 10) + ((r0 >> 3) << 11) +
+          (x.wave << 12);
+      const uint32_t w = nw[r0 >> 3];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = flip(acc[t][r0 + e], w, (p & 31) + e);
+    }
+    const int c = p >> 2;
+    stage[c ^ ((c >> 4) & 15)] = v;
+  }
+  __syncthreads();
+  float* prow = partial + slot * (int64_t)n;
+  const auto p_r = rsrc(prow, (uint32_t)n * 4u);
+#pragma unroll
+  for (int i = 0; i < (kB / 4) / kThreads; ++i) {
+    const int c = i * kThreads + (int)threadIdx.x;
+    const f32x4 v = stage[c ^ ((c >> 4) & 15)];
+    const int p = c * 4;
+    if (p + 4 <= n) {
+      __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, 0);
     } else if (p < n) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
+      for (int e = 0; e < 4; ++e)
         if (p + e < n) prow[p + e] = v[e];
     }
-  };
-  if constexpr (L % 2 == 1) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float v[8];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) v[t] = flip(acc[t][r], nw[r >> 2], t | ((r & 3) << 3));
-      store(pos_s1(x, r), v);
-    }
-  } else {
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          v[j] = flip(acc[t][8 * c + j], nw[c + 2 * (t >> 2)], j | ((t & 3) << 3));
-        store(pos_s0(x, t, c), v);
-      }
   }
 }
 
 }  // namespace
 
 bool mfma15_applicable(const BfhtArgs& a) {
-  // 16-byte vector loads of the latent and the partial rows need aligned bases;
-  // output and grad alignment is checked per block in the kernels.
+  // 16-byte vector loads of the latent and stores of the partial rows need
+  // aligned bases; output and grad alignment is checked per block in the kernels.
   const bool aligned = ((uintptr_t)a.src % 16 == 0) && (a.work == nullptr || (uintptr_t)a.work % 16 == 0);
   return a.dtype == kBF16 && a.log_block == kLog && a.nblocks > 0 && a.n <= kB && aligned;
 }
 
 hipError_t launch_mfma15(const BfhtArgs& a, hipStream_t s, bool fwd) {
   const dim3 grid((unsigned)a.nblocks), block(kThreads);
+  auto* src = (const __bf16*)a.src;
   if (fwd) {
-    auto* src = (const __bf16*)a.src;
     auto* dst = (__bf16*)a.dst;
     switch (a.layers) {
       case 1: hipLaunchKernelGGL(bfht_mfma15_fwd<1>, grid, block, 0, s, src, dst, (int)a.n, a.first_block, a.start, a.stop, a.seed32); break;
@@ -522,7 +570,6 @@ hipError_t launch_mfma15(const BfhtArgs& a, hipStream_t s, bool fwd) {
     }
     return hipGetLastError();
   }
-  auto* src = (const __bf16*)a.src;
   auto* part = (float*)a.work;
   switch (a.layers) {
     case 1: hipLaunchKernelGGL(bfht_mfma15_bwd<1>, grid, block, 0, s, src, part, (int)a.n, a.first_block, a.start, a.stop, a.seed32); break;
