@@ -84,6 +84,19 @@ class Abi:
                                         layers, seed, start, stop, grad_latent.data_ptr(), wp, wn, self.stream())
         N.check(rc)
 
+    def linear(self, x, latent, out, out_f, layers, seed, scale, ws=None):
+        N = self.N
+        tokens, in_f = x.shape
+        wp, wn = (ws.data_ptr(), ws.numel()) if ws is not None else (0, 0)
+        rc = self.lib.lwl_bfht_linear_forward(x.data_ptr(), latent.data_ptr(), N.dtype_code(x.dtype), tokens, in_f,
+                                              latent.numel(), out_f, layers, seed, scale, out.data_ptr(), wp, wn,
+                                              self.stream())
+        N.check(rc)
+
+    def linear_ws(self, tokens, in_f, out_f, n, device):
+        nbytes = self.lib.lwl_bfht_linear_forward_workspace_size(tokens, in_f, out_f, n)
+        return self.torch.empty(nbytes, dtype=self.torch.uint8, device=device) if nbytes else None
+
     def fwd_ws(self, n, size, start, stop, device):
         nbytes = self.lib.lwl_bfht_forward_workspace_size(n, size, start, stop)
         return self.torch.empty(nbytes, dtype=self.torch.uint8, device=device) if nbytes else None
@@ -248,7 +261,7 @@ def extra_configs(abi, steps, warmup, only):
 
     # config 4: fused linear at GPT-2-small MLP shapes vs dense bf16 GEMM on the materialized weight
     if want("c4_linear"):
-        from latent_weight_lab_amd import block_fht_linear_forward, block_fht_slice
+        from latent_weight_lab_amd import block_fht_slice
 
         lin = {}
         for inf, outf in ((768, 3072), (3072, 768)):
@@ -256,19 +269,85 @@ def extra_configs(abi, steps, warmup, only):
                 torch.manual_seed(3)
                 latent = torch.randn(32768, dtype=torch.float32).to(torch.bfloat16).cuda()
                 x = torch.randn(4096, inf, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).cuda()
+                out = torch.empty(4096, outf, dtype=torch.bfloat16, device="cuda")
+                ws = abi.linear_ws(4096, inf, outf, 32768, "cuda")
                 with torch.no_grad():
                     w = block_fht_slice(latent, inf * outf, 3, 3, 0, inf * outf).view(outf, inf)
-                    flops = 2 * 4096 * inf * outf
-                    fused = time_eager(torch, lambda: block_fht_linear_forward(x, latent, outf, 3, 3), 20, 3)
-                    dense = time_graph(torch, lambda: torch.nn.functional.linear(x, w), 50, 5)
+                flops = 2 * 4096 * inf * outf
+                fused = time_graph(torch, lambda: abi.linear(x, latent, out, outf, 3, 3, 1.0, ws), 50, 5)
+                dense = time_graph(torch, lambda: torch.nn.functional.linear(x, w), 50, 5)
                 lin[f"{inf}x{outf}"] = {"fused_ms": round(fused * 1e3, 4), "dense_gemm_ms": round(dense * 1e3, 4),
                                         "fused_over_dense": fused / dense,
                                         "fused_tokens_per_s": 4096 / fused,
                                         "fused_TFLOPs": flops / fused / 1e12,
                                         "dense_TFLOPs": flops / dense / 1e12}
+                del latent, x, out, ws, w
             except Exception as exc:  # noqa: BLE001
                 lin[f"{inf}x{outf}"] = {"error": f"{type(exc).__name__}: {exc}"}
         res["c4_linear"] = lin
+
+    # config 5: 12-layer GPT-2-small linear stack (qkv, proj, fc, fc-proj per layer = 48 matrices,
+    # latents of 32768 bf16, seeds 100+i), forward only, fused vs dense on materialized weights
+    if want("c5_stack"):
+        res["c5_stack"] = stack_bench(abi, torch)
+    return res
+
+
+GPT2_SHAPES = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
+
+
+def stack_bench(abi, torch):
+    from latent_weight_lab_amd import block_fht_slice
+
+    mats = []
+    for layer in range(12):
+        for j, (inf, outf) in enumerate(GPT2_SHAPES):
+            i = 4 * layer + j
+            torch.manual_seed(100 + i)
+            mats.append((inf, outf, torch.randn(32768).to(torch.bfloat16).cuda(), 100 + i))
+    torch.cuda.synchronize()
+    out = {}
+    for tokens in (1, 16, 64, 8 * 1024):
+        row = {}
+        try:
+            xs = {inf: torch.randn(tokens, inf, generator=torch.Generator().manual_seed(tokens)).to(torch.bfloat16).cuda()
+                  for inf in (768, 3072)}
+            outs = [torch.empty(tokens, outf, dtype=torch.bfloat16, device="cuda") for _, outf, _, _ in mats]
+            wss = [abi.linear_ws(tokens, inf, outf, 32768, "cuda") for inf, outf, _, _ in mats]
+
+            def fused_stack():
+                for (inf, outf, lat, seed), o, ws in zip(mats, outs, wss):
+                    abi.linear(xs[inf], lat, o, outf, 3, seed, 1.0, ws)
+
+            torch.cuda.synchronize()
+            base = torch.cuda.memory_allocated()
+            torch.cuda.reset_peak_memory_stats()
+            fused_stack()
+            torch.cuda.synchronize()
+            row["fused_peak_extra_MiB"] = (torch.cuda.max_memory_allocated() - base) / 2**20
+            sec = time_graph(torch, fused_stack, 5, 2)
+            row["fused_ms"] = sec * 1e3
+            row["fused_tokens_per_s"] = tokens / sec
+            with torch.no_grad():
+                ws_dense = [block_fht_slice(lat, inf * outf, 3, seed, 0, inf * outf).view(outf, inf)
+                            for inf, outf, lat, seed in mats]
+            torch.cuda.synchronize()
+            row["dense_weights_MiB"] = sum(w.numel() * 2 for w in ws_dense) / 2**20
+
+            def dense_stack():
+                for (inf, outf, _, _), o, w in zip(mats, outs, ws_dense):
+                    torch.matmul(xs[inf], w.t(), out=o)
+
+            sec = time_graph(torch, dense_stack, 5, 2)
+            row["dense_ms"] = sec * 1e3
+            row["dense_tokens_per_s"] = tokens / sec
+            row["fused_over_dense"] = row["fused_ms"] / row["dense_ms"]
+            del ws_dense, xs, outs, wss
+            torch.cuda.empty_cache()
+        except Exception as exc:  # noqa: BLE001
+            row["error"] = f"{type(exc).__name__}: {exc}"
+        out[f"tokens_{tokens}"] = row
+    return out
     return res
 
 

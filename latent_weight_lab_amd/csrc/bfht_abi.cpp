@@ -127,6 +127,13 @@ int check_linear(int dtype, int64_t tokens, int64_t in_features, int64_t latent_
                 lwl::kLinearMaxInFeatures);
   if (!lwl::kLinearKernelAvailable)
     return fail(LWL_ERR_UNSUPPORTED, "fused linear kernel not available in this build");
+  if (!lwl::linear_applicable(dtype, lb, in_features))
+    return fail(LWL_ERR_UNSUPPORTED,
+                "fused linear forward takes bfloat16 latents of length 16385..32768 (block 2^15) with "
+                "in_features %% 8 == 0 and in_features >= 521 (dtype code %d, latent size %lld, in_features %lld)",
+                dtype, (long long)latent_size, (long long)in_features);
+  if (tokens * in_features * 2 >= ((int64_t)1 << 31))
+    return fail(LWL_ERR_UNSUPPORTED, "fused linear forward: tokens * in_features must stay below 2^30");
   return LWL_OK;
 }
 
@@ -228,8 +235,9 @@ int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features
 
 size_t lwl_bfht_linear_forward_workspace_size(int64_t tokens, int64_t in_features,
                                               int64_t out_features, int64_t latent_size) {
-  if (check_linear(LWL_DTYPE_F32, tokens, in_features, latent_size, out_features, 1)) return 0;
-  return linear_ws(plan_linear(LWL_DTYPE_F32, tokens, in_features, latent_size, out_features, 1, 0,
+  // the workspace does not depend on the element type; bf16 is the type the kernel takes
+  if (check_linear(LWL_DTYPE_BF16, tokens, in_features, latent_size, out_features, 1)) return 0;
+  return linear_ws(plan_linear(LWL_DTYPE_BF16, tokens, in_features, latent_size, out_features, 1, 0,
                                1.0));
 }
 

@@ -60,6 +60,9 @@ struct LinearArgs {
 // in LDS; in_features bounds the padded row length.
 constexpr int kLinearMaxInFeatures = 32768;
 extern const bool kLinearKernelAvailable;
+// Shapes the fused kernel (bfht_linear.hip) takes: bf16 blocks of 2^15,
+// in_features % 8 == 0, at most 64 output rows per generated block.
+bool linear_applicable(int dtype, int log_block, int64_t in_features);
 int linear_token_splits(const LinearArgs& a);
 hipError_t launch_linear(const LinearArgs& a, hipStream_t s);
 

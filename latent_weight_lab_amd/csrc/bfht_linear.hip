@@ -1,7 +1,261 @@
-// placeholder: fused linear kernels
-#include "bfht_launch.h"
+// Fused BlockFHTLinear forward: out = weight_scale * x @ W^T with W generated
+// on chip, block by block, never written to memory.
+//
+// W[o, i] = y[o * in + i] where y is the BlockFHT output of the latent over
+// size = in * out (reference latent_weight_lab/block_fht.py:251-288).  One
+// workgroup owns one generated block b (2^15 weights, the matrix-core chain of
+// bfht_mfma_chain.h) and one range of tokens: it generates the block into LDS
+// as bf16, then contracts it with its tokens' rows of x on v_mfma_f32_16x16x32_bf16:
+//
+//   D[t][o] = sum_k x[t][k] * W[o][k]     A = x tile (16 tokens x 32 k, from memory)
+//                                          B = W^T tile (32 k x 16 rows, from LDS)
+//
+// Block b covers flat positions [b*B, (b+1)*B): rows o_first .. o_last.  A row
+// whose positions start in an earlier block or end in a later one is partial:
+// its float32 partial dot products go to the workspace, and a second kernel
+// adds the two halves of each straddling row (two terms: the sum does not
+// depend on the order).  Rows inside the block are written directly.
+//
+// Reference kernel: csrc/block_fht_ext_cuda.cu:225-329 (which regenerates each
+// block per 8-token tile and requires block_size % in_features == 0).
+#include "bfht_mfma_chain.h"
+
 namespace lwl {
-const bool kLinearKernelAvailable = false;
-int linear_token_splits(const LinearArgs&) { return 1; }
-hipError_t launch_linear(const LinearArgs&, hipStream_t) { return hipErrorNotSupported; }
+namespace {
+
+using namespace mfma15;
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+constexpr int kTokTile = 16;  // tokens per MFMA tile
+constexpr int kKStep = 32;    // k per MFMA
+constexpr int kGroup = 4;     // token tiles per wave pass (each W read feeds kGroup MFMAs)
+constexpr int kDepth = 4;     // x prefetch distance in k steps
+
+__device__ __forceinline__ f32x4v mfma16(u32x4 a, u32x4 b, f32x4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
 }
+
+// Up to kMaxNT tiles of 16 output rows per block (in_features >= 2^15/(16*kMaxNT - 2)), and the
+// k-major table (4*ceil(in/32) chunks x 16*NT rows x 16 bytes) must fit in the LDS.
+constexpr int kMaxNT = 4;
+
+__host__ __device__ constexpr int64_t linear_row_tiles(int64_t in_features) {
+  return ((kB + in_features - 1) / in_features + 1 + 15) / 16;  // incl. two partial rows
+}
+
+// k steps of 32 per row, rounded up to whole prefetch rounds of kDepth steps
+__host__ __device__ constexpr int linear_steps(int64_t in_features) {
+  return (int)(((in_features + kKStep - 1) / kKStep + kDepth - 1) / kDepth * kDepth);
+}
+
+template <int L, int NT>
+__global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __restrict__ x,
+                                                               const __bf16* __restrict__ latent,
+                                                               __bf16* __restrict__ out,
+                                                               float* __restrict__ partial, int tokens,
+                                                               int in_f, int out_f, int n, uint32_t seed32,
+                                                               float scale, int token_split) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  const int64_t block = blockIdx.x / token_split;
+  const int split = blockIdx.x % token_split;
+  constexpr int kRows = 16 * NT;  // table rows (output rows of the block, zero-padded)
+
+  const int64_t size = (int64_t)in_f * out_f;
+  const int64_t g0 = block * kB;                         // first flat position
+  const int64_t g1 = (g0 + kB < size) ? g0 + kB : size;  // one past the last
+  const int o_first = (int)(g0 / in_f);
+  const int o_last = (int)((g1 - 1) / in_f);
+  const bool first_partial = (g0 % in_f) != 0;
+  const bool last_partial = (g1 % in_f) != 0;
+  // k steps, padded to whole prefetch rounds: the padding reads zeros (table
+  // rows past the row length are zero, x offsets past it are out of range)
+  const int nsteps = linear_steps(in_f);
+  const int kchunks = 4 * nsteps;  // 8-element k chunks per table row
+
+  // 1. generate the block (signed bf16) and scatter it into LDS as a k-major
+  //    table of 16-byte chunks: table[kc * kRows + (o - o_first)] holds
+  //    W[o][8*kc .. 8*kc+7]; entries outside the block read 0.
+  u32x4* table = reinterpret_cast<u32x4*>(lds);
+  {
+    const Ctx c = make_ctx(seed32, block);
+    u32x4 src[kTiles][2];
+    load_latent(c, latent, n, src);
+    f32x16 acc[kTiles];
+    uint32_t nw[4];
+    run_chain<L>(acc, c, lds, src, [](int i) { return i; }, nw);
+    u32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = out_chunk<L>(acc, nw, c, k);
+    __syncthreads();  // every wave has read its last exchange
+    for (int i = threadIdx.x; i < kchunks * kRows; i += kThreads) table[i] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int64_t gp = g0 + out_chunk_pos<L>(c, k);
+      if (gp < g1) {
+        const uint32_t o = (uint32_t)(gp / in_f), kc = (uint32_t)(gp - (int64_t)o * in_f) >> 3;
+        table[kc * kRows + (o - o_first)] = v[k];
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. this workgroup's token tiles
+  const int ntiles_tok = (tokens + kTokTile - 1) / kTokTile;
+  const int per_split = (ntiles_tok + token_split - 1) / token_split;
+  const int tt0 = split * per_split;
+  const int tt1 = (tt0 + per_split < ntiles_tok) ? tt0 + per_split : ntiles_tok;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, kq = lane >> 4;  // A/B: row/col l16, k = 8*kq + j
+  const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * in_f * 2));  // offsets past the end read 0
+  float* part_first = partial + (block * 2 + 0) * (int64_t)tokens;
+  float* part_last = partial + (block * 2 + 1) * (int64_t)tokens;
+  const u32x4* brow = table + kq * kRows + l16;  // + step*4*kRows + 16*nt
+  constexpr uint32_t kOff = 0x80000000u;  // voffset that reads 0
+
+  // Each wave takes groups of kGroup token tiles (64 tokens): per k step it
+  // reads the NT W tiles once from LDS and issues kGroup * NT MFMAs; x is
+  // prefetched kDepth steps ahead into a register ring.  The loop body has no
+  // branches, so the compiler can count the loads in flight.
+  for (int tg = tt0 + kGroup * wave; tg < tt1; tg += kGroup * kWaves) {
+    uint32_t xo[kGroup];
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g) {
+      const int tt = tg + g, t = tt * kTokTile + l16;
+      xo[g] = (tt < tt1 && t < tokens) ? (uint32_t)((t * in_f + 8 * kq) * 2) : kOff;
+    }
+    // lanes whose 8 k-values of the step lie past the row (in % 8 == 0: all or none) read 0
+    auto xload = [&](int g, int step) -> u32x4 {
+      const uint32_t off = (step * kKStep + 8 * kq < in_f) ? xo[g] : kOff;
+      return __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)off, step * kKStep * 2, 0);
+    };
+    f32x4v acc[kGroup][NT];
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[g][nt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    u32x4 ring[kDepth][kGroup];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d)
+#pragma unroll
+      for (int g = 0; g < kGroup; ++g) ring[d][g] = xload(g, d);
+    const u32x4* bs = brow;
+    for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        u32x4 bt[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) bt[nt] = bs[16 * nt];
+        bs += 4 * kRows;
+        u32x4 a[kGroup];
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g) {
+          a[g] = ring[d][g];
+          ring[d][g] = xload(g, s0 + d + kDepth);
+        }
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) acc[g][nt] = mfma16(a[g], bt[nt], acc[g][nt]);
+      }
+    }
+    // D[m = 4*kq + r][n = l16]
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g) {
+      const int tt = tg + g;
+      if (tt >= tt1) continue;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int o = o_first + 16 * nt + l16;
+        if (o > o_last) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tr = tt * kTokTile + 4 * kq + r;
+          if (tr >= tokens) continue;
+          const float v = acc[g][nt][r];
+          if (o == o_first && first_partial)
+            part_first[tr] = v;
+          else if (o == o_last && last_partial)
+            part_last[tr] = v;
+          else
+            out[(int64_t)tr * out_f + o] = (__bf16)(scale * v);
+        }
+      }
+    }
+  }
+}
+
+// Rows straddling blocks b-1 and b: out[t][o] = scale * (last(b-1)[t] + first(b)[t]).
+__global__ __launch_bounds__(256) void bfht_linear_combine(const float* __restrict__ partial,
+                                                           __bf16* __restrict__ out, int tokens, int in_f,
+                                                           int out_f, int64_t nblocks, float scale) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int64_t b = (int64_t)blockIdx.y + 1;
+  if (t >= tokens || b >= nblocks) return;
+  const int64_t g0 = b * mfma15::kB;
+  if (g0 % in_f == 0) return;
+  const int o = (int)(g0 / in_f);
+  const float v = partial[((b - 1) * 2 + 1) * (int64_t)tokens + t] + partial[(b * 2) * (int64_t)tokens + t];
+  out[(int64_t)t * out_f + o] = (__bf16)(scale * v);
+}
+
+template <int L>
+hipError_t launch_linear_L(const LinearArgs& a, hipStream_t s) {
+  const int nt = (int)linear_row_tiles(a.in_features);
+  const dim3 grid((unsigned)(a.nblocks_w * a.token_splits)), block(mfma15::kThreads);
+  auto* x = (const __bf16*)a.x;
+  auto* lat = (const __bf16*)a.latent;
+  auto* o = (__bf16*)a.out;
+#define LWL_LIN(NT)                                                                                           \
+  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT>), grid, block, 0, s, x, lat, o, a.partial, (int)a.tokens,      \
+                     (int)a.in_features, (int)a.out_features, (int)a.n, a.seed32, a.weight_scale, a.token_splits)
+  switch (nt) {
+    case 1: LWL_LIN(1); break;
+    case 2: LWL_LIN(2); break;
+    case 3: LWL_LIN(3); break;
+    case 4: LWL_LIN(4); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef LWL_LIN
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.nblocks_w < 2) return e;
+  hipLaunchKernelGGL(bfht_linear_combine, dim3((unsigned)((a.tokens + 255) / 256), (unsigned)(a.nblocks_w - 1)),
+                     dim3(256), 0, s, (const float*)a.partial, o, (int)a.tokens, (int)a.in_features,
+                     (int)a.out_features, a.nblocks_w, a.weight_scale);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+const bool kLinearKernelAvailable = true;
+
+bool linear_applicable(int dtype, int log_block, int64_t in_features) {
+  // bf16 matrix-core generator (B = 2^15); 16-byte rows of x and W (in % 8 == 0);
+  // at most kMaxNT tiles of 16 rows per block; the k-major table fits in LDS.
+  if (dtype != kBF16 || log_block != mfma15::kLog || in_features % 8 != 0 || in_features > mfma15::kB) return false;
+  const int64_t nt = linear_row_tiles(in_features);
+  const int64_t table_bytes = (int64_t)4 * linear_steps(in_features) * 16 * nt * 16;
+  return nt <= kMaxNT && table_bytes <= mfma15::kLdsBytes;
+}
+
+int linear_token_splits(const LinearArgs& a) {
+  // one workgroup per CU: split tokens so that blocks x splits fills 256 CUs,
+  // never below one 16-token tile per split
+  const int64_t tiles = (a.tokens + kTokTile - 1) / kTokTile;
+  int64_t split = a.nblocks_w >= 256 ? 1 : 256 / a.nblocks_w;
+  if (split > tiles) split = tiles;
+  return (int)(split < 1 ? 1 : split);
+}
+
+hipError_t launch_linear(const LinearArgs& a, hipStream_t s) {
+  switch (a.layers) {
+    case 1: return launch_linear_L<1>(a, s);
+    case 2: return launch_linear_L<2>(a, s);
+    case 3: return launch_linear_L<3>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace lwl

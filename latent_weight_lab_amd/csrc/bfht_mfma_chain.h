@@ -1,0 +1,435 @@
+// Matrix-core BlockFHT chain for block size 2^15 (gfx950, bf16 operands,
+// float32 accumulation), shared by the generator kernels (bfht_mfma.hip) and
+// the fused linear kernel (bfht_linear.hip).
+//
+// One workgroup of 8 waves (two per SIMD, so one wave's MFMAs overlap the
+// other's VALU and LDS work) owns one 32768-element block; each lane holds 64
+// values as 4 MFMA accumulator tiles of 16 floats.  The normalized Hadamard
+// transform of a layer is split over three 5-bit groups of the position index
+// (H_32768 = H_32 (x) H_32 (x) H_32), each applied as a 32x32 Walsh matrix
+// with v_mfma_f32_32x32x16_bf16:
+//
+//   stage a, b: data is the A operand (rows = lanes 0-31, k = lane bit 5 and
+//               4 register bits); the transformed group lands in lane bits
+//               0-4 and the old lane bits move into the registers;
+//   stage c:    data is the B operand; its 5 bits include all three wave
+//               bits, so it follows one LDS exchange (64 KiB of bf16) that
+//               swaps three already-transformed bits out to the wave index.
+//
+// Slot -> position bit assignment (p0..p14; Lk = lane bit k, Rk = bit k of the
+// accumulator register index r = 0..15, Tk = bit k of the tile index,
+// Wk = bit k of the wave index):
+//
+//   S0 (even layer start): L0-4 = p5-9, L5 = p10, R = p0 p1 p4 p11, T = p2 p3, W = p12 p13 p14
+//   S1 (odd layer start):  L0-4 = p5-9, L5 = p12, R = p3 p2 p13 p14, T = p0 p1, W = p4 p10 p11
+//
+// An even layer starts in S0 and ends in S1, an odd one the reverse.  The sign
+// layers meet the five bit-in-word bits (p0..p4) in registers, except p4 at
+// S1, which is a wave bit; sign words (one 32-bit hash per 32 positions) are
+// computed per lane and applied to packed bf16 pairs as XOR masks
+// (word << (15 - b)) & 0x80008000, after a fixed permutation of the word's
+// bits that puts the pair's two positions 16 bits apart (and a wave-uniform
+// pre-shift for p4).
+//
+// Walsh entries are +-1/4, +-1/8, +-1/4 (exact in bf16); the remaining
+// 2^(-L/2) of the L-layer normalization is folded into the last stage's
+// entries, rounded to bf16 (relative error <= 2^-9).
+//
+// Reference semantics: latent_weight_lab/block_fht.py:84-109 (forward) and
+// csrc/block_fht_ext_cuda.cu:185-223 (backward: the same chain with the sign
+// layers in reverse order).
+#pragma once
+
+#include "bfht_device.h"
+#include "bfht_launch.h"
+
+namespace lwl {
+namespace mfma15 {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kLog = 15;
+constexpr int kB = 1 << kLog;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTiles = 4;
+constexpr int kChunks = kB / 8;  // 16-byte chunks of 8 bf16 in one block
+// Exchange buffers: 4096 16-byte chunks with 8 bytes of padding after every
+// 16 chunks, so that the 8-byte writes of lanes l and l + 16 hit different
+// banks; two buffers back to back (132 KiB).
+constexpr int kXBufBytes = kChunks * 16 + (kChunks / 16) * 8;
+constexpr int kLdsBytes = 2 * kXBufBytes;
+constexpr uint32_t kPairSign = 0x80008000u;
+
+__device__ __forceinline__ uint32_t pk(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Sign-word bit permutations exchanging bit-index bit 0 (resp. 3) with bit 4,
+// so that the two positions of a packed pair sit 16 word bits apart.
+__device__ __forceinline__ uint32_t swap_idx04(uint32_t x) {
+  const uint32_t t = ((x >> 15) ^ x) & 0x0000aaaau;
+  return x ^ t ^ (t << 15);
+}
+__device__ __forceinline__ uint32_t swap_idx34(uint32_t x) {
+  const uint32_t t = ((x >> 8) ^ x) & 0x0000ff00u;
+  return x ^ t ^ (t << 8);
+}
+
+// Walsh operands: for lane l and register pair (c, v), entries k = 16c +
+// 8*(l>>5) + 2v + {0, 1}, o = l & 31, equal scale * (-1)^popcount(remap(k) & o)
+// where remap moves k bit i to bit M[i].  The same registers serve as B operand
+// (o = column) and as A operand (o = row).  Precomputed at compile time as bf16
+// pairs for the five (permutation, scale) combinations the kernels use:
+//   Q = (0,1,3,2,4) (k bits 2 and 3 exchanged), S = (1,0,2,3,4) (bits 0 and 1);
+//   bf16 0x3e80 = 1/4, 0x3e00 = 1/8, 0x3e35 = bf16(2^-2.5), 0x3db5 = bf16(2^-3.5).
+enum { kWalshQ4, kWalshQ8, kWalshS4, kWalshSL1, kWalshSL3, kWalshSets };
+
+struct WalshTable {
+  uint32_t v[kWalshSets][64][8];
+};
+
+constexpr WalshTable make_walsh_table() {
+  WalshTable tab{};
+  const int perm[kWalshSets][5] = {{0, 1, 3, 2, 4}, {0, 1, 3, 2, 4}, {1, 0, 2, 3, 4}, {1, 0, 2, 3, 4}, {1, 0, 2, 3, 4}};
+  const uint32_t mag[kWalshSets] = {0x3e80u, 0x3e00u, 0x3e80u, 0x3e35u, 0x3db5u};
+  for (int set = 0; set < kWalshSets; ++set)
+    for (int lane = 0; lane < 64; ++lane)
+      for (int c = 0; c < 2; ++c)
+        for (int v = 0; v < 4; ++v) {
+          uint32_t word = 0;
+          for (int s = 0; s < 2; ++s) {
+            const int k = 16 * c + 8 * (lane >> 5) + 2 * v + s;
+            int km = 0;
+            for (int i = 0; i < 5; ++i) km |= ((k >> i) & 1) << perm[set][i];
+            int par = 0;
+            for (int b = km & (lane & 31); b; b >>= 1) par ^= b & 1;
+            word |= (mag[set] | (par ? 0x8000u : 0u)) << (16 * s);
+          }
+          tab.v[set][lane][4 * c + v] = word;
+        }
+  return tab;
+}
+
+__device__ const WalshTable kWalsh = make_walsh_table();
+
+__device__ __forceinline__ void walsh_operand(int set, int lane, u32x4 (&h)[2]) {
+  const u32x4* row = reinterpret_cast<const u32x4*>(kWalsh.v[set][lane]);
+  h[0] = row[0];
+  h[1] = row[1];
+}
+
+struct Ctx {
+  int lane32, l5, wave;
+  uint32_t bkey;
+  uint32_t base0, base1;  // sign-word index bases in S0 and S1
+  uint32_t gw0, gw1;      // 0xc2b2ae35 * (base + 1): the word term of the hash input
+  int p4;                 // position bit p4 of this wave in S1
+  int wid, rid;           // exchange chunk-id bases (write / read side)
+};
+
+__device__ __forceinline__ Ctx make_ctx(uint32_t seed32, int64_t block) {
+  Ctx x;
+  const int tid = threadIdx.x;
+  x.lane32 = tid & 31;
+  x.l5 = (tid >> 5) & 1;
+  x.wave = tid >> 6;
+  x.bkey = block_key(seed32, block);
+  // word = p >> 5.  S0 word bits: p5-9 = lane32, p10 = l5, p11 = slot, p12-14 = wave
+  x.base0 = (uint32_t)(x.lane32 | (x.l5 << 5) | (x.wave << 7));
+  // S1 word bits: p5-9 = lane32, p10-11 = wave >> 1, p12 = l5, p13-14 = slot
+  x.base1 = (uint32_t)(x.lane32 | ((x.wave >> 1) << 5) | (x.l5 << 7));
+  x.gw0 = 0xc2b2ae35u * (x.base0 + 1u);
+  x.gw1 = 0xc2b2ae35u * (x.base1 + 1u);
+  x.p4 = x.wave & 1;
+  x.wid = x.lane32 + (x.l5 << 8) + ((x.wave >> 1) << 10);
+  x.rid = x.lane32 + (x.wave << 7) + (x.l5 << 10);
+  return x;
+}
+
+// Hash word of slot s: word index base + s * 2^shift (disjoint bits, so the
+// word term 0xc2b2ae35 * (index + 1) is the lane's base term plus a constant).
+__device__ __forceinline__ uint32_t slot_word(uint32_t key, uint32_t gw, int s, int shift) {
+  return lowbias32(key ^ (gw + 0xc2b2ae35u * ((uint32_t)s << shift)));
+}
+
+// Sign words of one layer for this lane, inverted (set bit = flip) and
+// permuted for the pair layout.  S0: 2 words, slot = p11.  S1: 4 words,
+// slot = p13 + 2*p14, pre-shifted right by 8 when this wave's p4 is 1.
+
+template <bool kOdd>
+__device__ __forceinline__ void layer_words(const Ctx& x, int layer, uint32_t (&nw)[4]) {
+  const uint32_t key = x.bkey ^ layer_key(layer);
+#pragma unroll
+  for (int s = 0; s < (kOdd ? 4 : 2); ++s) {
+    const uint32_t w = ~(kOdd ? slot_word(key, x.gw1, s, 8) : slot_word(key, x.gw0, s, 6));
+    nw[s] = kOdd ? (swap_idx34(w) >> (8 * x.p4)) : swap_idx04(w);
+  }
+  if (!kOdd) nw[2] = nw[3] = 0;
+}
+
+// XOR mask of stage-a operand VGPR v (pair j = 2v, 2v+1) of tile t, instruction c.
+//   S0: j0 = p0 (pair), j1 = p1, j2 = p4, c = p11, t = (p2, p3)
+//   S1: j0 = p3 (pair), j1 = p2, j2 = p13, c = p14, t = (p0, p1)
+template <bool kOdd>
+__device__ __forceinline__ uint32_t operand_mask(const uint32_t (&nw)[4], int t, int c, int v) {
+  if (kOdd) {
+    const int b = t | ((v & 1) << 2);  // + 8*p4, folded into the word
+    return (nw[(v >> 1) + 2 * c] << (15 - b)) & kPairSign;
+  }
+  const int b = (v >> 1) | ((v & 1) << 1) | (t << 2);
+  return (nw[c] << (15 - b)) & kPairSign;
+}
+
+__device__ __forceinline__ u32x4 pack8(const f32x16& a, int base) {
+  u32x4 r;
+  r[0] = pk(a[base + 0], a[base + 1]);
+  r[1] = pk(a[base + 2], a[base + 3]);
+  r[2] = pk(a[base + 4], a[base + 5]);
+  r[3] = pk(a[base + 6], a[base + 7]);
+  return r;
+}
+
+// Data as A operand: acc[t] <- packed(acc[t]) x H, sign layer fused when kSigned.
+template <bool kSigned, bool kOdd>
+__device__ __forceinline__ void stage_rows(f32x16 (&acc)[kTiles], const u32x4 (&h)[2],
+                                           const uint32_t (&nw)[4]) {
+  const f32x16 zero = {};
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) {
+    u32x4 a[2] = {pack8(acc[t], 0), pack8(acc[t], 8)};
+    if (kSigned) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<kOdd>(nw, t, c, v);
+    }
+    f32x16 d = mfma(a[0], h[0], zero);
+    acc[t] = mfma(a[1], h[1], d);
+  }
+}
+
+// Exchange: 16-byte chunk id (12 bits) of 8 packed values; each wave writes one
+// 8-byte half (its 4 tiles at register r), the half being wave bit 0:
+//   write: id = lane32 + (r&7)<<5 + l5<<8 + (r>>3)<<9 + (wave>>1)<<10, half = wave & 1
+//   read:  id = lane32 + t<<5 + wave<<7 + l5<<10 + c<<11 (whole chunk = B operand)
+// 8-byte slot of (id, half) in a padded buffer: 2*id + (id >> 4) + half.
+__device__ __forceinline__ int xslot(int id) { return 2 * id + (id >> 4); }
+
+__device__ __forceinline__ void exchange_write(const f32x16 (&acc)[kTiles], u32x2* xbuf, const Ctx& x) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    u32x2 v;
+    v[0] = pk(acc[0][r], acc[1][r]);
+    v[1] = pk(acc[2][r], acc[3][r]);
+    xbuf[xslot(x.wid + ((r & 7) << 5) + ((r >> 3) << 9)) + (x.wave & 1)] = v;
+  }
+}
+
+__device__ __forceinline__ void exchange_read_stage_c(f32x16 (&acc)[kTiles], const u32x4 (&h)[2],
+                                                      const u32x2* xbuf, const Ctx& x) {
+  u32x4 b[kTiles][2];
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int sl = xslot(x.rid + (t << 5) + (c << 11));
+      const u32x2 lo = xbuf[sl], hi = xbuf[sl + 1];
+      b[t][c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  const f32x16 zero = {};
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) {
+    f32x16 d = mfma(h[0], b[t][0], zero);
+    acc[t] = mfma(h[1], b[t][1], d);
+  }
+}
+
+// Inverted sign words of the layer applied after the chain, in the output
+// layout (S1 when L is odd: 4 words, slot = p13 + 2*p14; S0 when L is even:
+// 2 words, slot = p11), unpermuted.
+template <int L>
+__device__ __forceinline__ void final_words(const Ctx& x, int layer, uint32_t (&nw)[4]) {
+  const uint32_t key = x.bkey ^ layer_key(layer);
+  constexpr bool kOutS1 = (L % 2) == 1;
+#pragma unroll
+  for (int s = 0; s < (kOutS1 ? 4 : 2); ++s)
+    nw[s] = ~(kOutS1 ? slot_word(key, x.gw1, s, 8) : slot_word(key, x.gw0, s, 6));
+  if (!kOutS1) nw[2] = nw[3] = 0;
+}
+
+// Runs the L-layer chain on a block whose unsigned input sits in `src`
+// (src[t][c] = stage-a operand of tile t, instruction c, in S0; loads may still
+// be in flight).  sign_layer(i) is the sign layer applied before kernel layer i
+// (i < L) and after the last one (i = L); the latter's words are returned in
+// `fin`.  On return acc holds the chain's result, before that last sign layer,
+// in S1 (L odd) or S0 (L even).  Layer i exchanges through buffer i & 1 of
+// `lds`: the previous readers of that buffer (layer i - 2) are past layer
+// i - 1's barrier, and buffer L & 1 needs no barrier before its next writes.
+template <int L, class SignLayer>
+__device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, unsigned char* lds,
+                                          const u32x4 (&src)[kTiles][2], SignLayer sign_layer,
+                                          uint32_t (&fin)[4]) {
+  uint32_t nw[L][4];
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    if (i & 1)
+      layer_words<true>(x, sign_layer(i), nw[i]);
+    else
+      layer_words<false>(x, sign_layer(i), nw[i]);
+  }
+  final_words<L>(x, sign_layer(L), fin);
+  const int lane = threadIdx.x & 63;
+  // Stage a: Q/4 (even layers), S/4 (odd); stage b: Q/8; stage c: S/4 (even),
+  // Q/4 (odd); the last stage c carries the residual 2^(-L/2): S/4*2^-0.5
+  // (L = 1), Q/8 (L = 2), S/4*2^-1.5 (L = 3).
+  u32x4 hq4[2], hq8[2], hs4[2], hlast[2];
+  walsh_operand(kWalshQ4, lane, hq4);
+  walsh_operand(kWalshQ8, lane, hq8);
+  walsh_operand(kWalshS4, lane, hs4);
+  walsh_operand(L == 1 ? kWalshSL1 : L == 2 ? kWalshQ8 : kWalshSL3, lane, hlast);
+  const f32x16 zero = {};
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    const bool odd = i & 1;
+    if (i == 0) {
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+        u32x4 a[2] = {src[t][0], src[t][1]};
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<false>(nw[0], t, c, v);
+        f32x16 d = mfma(a[0], hq4[0], zero);
+        acc[t] = mfma(a[1], hq4[1], d);
+      }
+    } else if (odd) {
+      stage_rows<true, true>(acc, hs4, nw[i]);
+    } else {
+      stage_rows<true, false>(acc, hq4, nw[i]);
+    }
+    stage_rows<false, false>(acc, hq8, nw[i]);
+    u32x2* xbuf = reinterpret_cast<u32x2*>(lds + (i & 1) * kXBufBytes);
+    exchange_write(acc, xbuf, x);
+    __syncthreads();
+    exchange_read_stage_c(acc, i == L - 1 ? hlast : (odd ? hq4 : hs4), xbuf, x);
+  }
+}
+
+// Raw buffer resource over `bytes` bytes at `base`: loads past the end read 0,
+// stores past the end are dropped (offsets are 32-bit).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Source operands in S0 from 16-byte chunks of 8 consecutive positions:
+// chunk (t1, p4, c) holds p0..p2 for p3 = t1; its VGPR q (p1 = q&1, p2 = q>>1)
+// is VGPR (q&1) + 2*p4 of operand (tile (q>>1) + 2*t1, instruction c).
+// `load(p)` returns the 8 bf16 at block position p (a multiple of 8).
+template <class Load>
+__device__ __forceinline__ void load_source(const Ctx& x, Load load, u32x4 (&src)[kTiles][2]) {
+  const int base = (x.lane32 << 5) + (x.l5 << 10) + (x.wave << 12);
+#pragma unroll
+  for (int t1 = 0; t1 < 2; ++t1)
+#pragma unroll
+    for (int p4 = 0; p4 < 2; ++p4)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u32x4 v = load(base + ((t1 << 3) + (p4 << 4) + (c << 11)));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) src[(q >> 1) + 2 * t1][c][(q & 1) + 2 * p4] = v[q];
+      }
+}
+
+// Output chunk k = 0..7 of this lane (8 consecutive positions): its block
+// position and its packed, signed content.
+//   S1 (L odd):  r = (p3, p2, p13, p14), t = (p0, p1), wave = (p4, p10, p11), l5 = p12; k = (p3, p13, p14)
+//   S0 (L even): r = (p0, p1, p4, p11), t = (p2, p3), wave = (p12, p13, p14), l5 = p10; k = (p3, p4, p11)
+template <int L>
+__device__ __forceinline__ int out_chunk_pos(const Ctx& x, int k) {
+  if constexpr (L % 2 == 1)
+    return ((k & 1) << 3) + (x.p4 << 4) + (x.lane32 << 5) + ((x.wave >> 1) << 10) + (x.l5 << 12) +
+           ((k >> 1) << 13);
+  else
+    return ((k & 1) << 3) + (((k >> 1) & 1) << 4) + (x.lane32 << 5) + (x.l5 << 10) + ((k >> 2) << 11) +
+           (x.wave << 12);
+}
+
+template <int L>
+__device__ __forceinline__ u32x4 out_chunk(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4], const Ctx& x,
+                                           int k) {
+  u32x4 v;
+  if constexpr (L % 2 == 1) {
+    // VGPR q: p1 = q&1 (tile bit 1), p2 = q>>1 (register bit 1); pair = p0 (tile bit 0).
+    // Pair-layout bit of the low element: p4 + 2p1 + 4p2 + 8p3, p4 folded into the word.
+    const int r0 = (k & 1) | ((k >> 1) << 2);
+    const uint32_t w = swap_idx04(nw[k >> 1]) >> x.p4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = r0 | ((q >> 1) << 1);
+      const int b = ((q & 1) << 1) | ((q >> 1) << 2) | ((k & 1) << 3);
+      v[q] = pk(acc[2 * (q & 1)][r], acc[2 * (q & 1) + 1][r]) ^ ((w << (15 - b)) & kPairSign);
+    }
+  } else {
+    // VGPR q: tile (q>>1) + 2*p3, register pair 2*(q&1) + 4*p4 + 8*p11 (+1); pair = p0.
+    const uint32_t w = swap_idx04(nw[k >> 2]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int t = (q >> 1) + 2 * (k & 1);
+      const int r = 2 * (q & 1) + 4 * ((k >> 1) & 1) + 8 * (k >> 2);
+      const int b = ((k >> 1) & 1) | ((q & 1) << 1) | ((q >> 1) << 2) | ((k & 1) << 3);
+      v[q] = pk(acc[t][r], acc[t][r + 1]) ^ ((w << (15 - b)) & kPairSign);
+    }
+  }
+  return v;
+}
+
+// Stages the chain's result (acc, before the last sign layer, words `nw`) as
+// signed bf16 in block-position order into `stage` (4096 16-byte chunks;
+// chunk c at c ^ ((c >> 4) & 3): conflict-free for these writes and for reads
+// of consecutive chunks).  The caller synchronizes before reading.
+template <int L>
+__device__ __forceinline__ void stage_output(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4], const Ctx& x,
+                                             u32x4* stage) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int c = out_chunk_pos<L>(x, k) >> 3;
+    stage[c ^ ((c >> 4) & 3)] = out_chunk<L>(acc, nw, x, k);
+  }
+}
+
+// Loads the S0 source operands of a block from the latent (n bf16 elements,
+// zero past the end).
+__device__ __forceinline__ void load_latent(const Ctx& x, const __bf16* latent, int n, u32x4 (&src)[kTiles][2]) {
+  const auto lat_r = rsrc(latent, (uint32_t)n * 2u);
+  const uint16_t* lat16 = reinterpret_cast<const uint16_t*>(latent);
+  const bool tail = (n & 7) != 0;
+  load_source(
+      x,
+      [&](int p) -> u32x4 {
+        u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(lat_r, p * 2, 0, 0);  // 0 past n
+        if (tail && p < n && p + 8 > n) {  // straddles the end of the latent: exact element loads
+          v = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (p + e < n) v[e >> 1] |= (uint32_t)lat16[p + e] << (16 * (e & 1));
+        }
+        return v;
+      },
+      src);
+}
+
+}  // namespace mfma15
+}  // namespace lwl

@@ -133,3 +133,32 @@ def test_next_power_of_two():
     assert [ops.next_power_of_two(v) for v in (1, 2, 3, 1024, 1025, 20000)] == [1, 2, 4, 1024, 2048, 32768]
     with pytest.raises(ValueError):
         ops.next_power_of_two(0)
+
+
+@pytest.mark.parametrize(
+    "args, code, msg",
+    [
+        # (dtype, tokens, in_features, latent_size, out_features, layers)
+        ((2, 4096, 768, 32768, 3072, 3), N.LWL_OK, ""),           # GPT-2 MLP up, bf16: fused
+        ((2, 4096, 3072, 32768, 768, 3), N.LWL_OK, ""),           # GPT-2 MLP down
+        ((2, 1, 1000, 30000, 77, 2), N.LWL_OK, ""),               # rows straddle blocks
+        ((0, 16, 768, 32768, 3072, 3), N.LWL_ERR_UNSUPPORTED, "bfloat16"),  # fp32: generate + F.linear
+        ((2, 16, 768, 16384, 3072, 3), N.LWL_ERR_UNSUPPORTED, "bfloat16"),  # block 2^14
+        ((2, 16, 100, 32768, 30, 3), N.LWL_ERR_UNSUPPORTED, "in_features"),  # in % 8 != 0, >64 rows
+        ((2, 16, 40000, 32768, 3, 3), N.LWL_ERR_UNSUPPORTED, "block_size"),  # in > B
+        ((2, 16, 768, 32768, 3072, 4), N.LWL_ERR_INVALID, "layers must be 1, 2, or 3"),
+        ((2, 16, 0, 32768, 3072, 3), N.LWL_ERR_INVALID, "in_features must be positive"),
+        ((2, 1 << 20, 1024, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "2^30"),
+    ],
+)
+def test_linear_validation(args, code, msg):
+    lib = N.lib()
+    assert lib.lwl_bfht_check_linear_forward(*args) == code
+    if msg:
+        assert msg in lib.lwl_last_error().decode()
+
+
+def test_linear_workspace_size():
+    # one pair of float32 partial rows (first / last row of the block) per generated block and token
+    lib = N.lib()
+    assert lib.lwl_bfht_linear_forward_workspace_size(4096, 768, 3072, 32768) == 72 * 2 * 4096 * 4
