@@ -156,9 +156,7 @@ lwl::LinearArgs plan_linear(int dtype, int64_t tokens, int64_t in_features, int6
   return a;
 }
 
-size_t linear_ws(const lwl::LinearArgs& a) {
-  return align_up((size_t)a.nblocks_w * 2 * (size_t)a.tokens * sizeof(float));
-}
+size_t linear_ws(const lwl::LinearArgs& a) { return align_up(lwl::linear_workspace_bytes(a)); }
 
 int check_workspace(size_t need, const void* ws, size_t have) {
   if (need == 0) return LWL_OK;
@@ -257,7 +255,7 @@ int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, in
   a.x = input;
   a.latent = latent;
   a.out = out;
-  a.partial = (float*)workspace;
+  a.work = workspace;
   return hip_status(lwl::launch_linear(a, (hipStream_t)stream), "lwl_bfht_linear_forward");
 }
 

@@ -46,7 +46,7 @@ struct LinearArgs {
   const void* x;       // [tokens, in]
   const void* latent;  // [n]
   void* out;           // [tokens, out]
-  float* partial;      // [nblocks_w, 2, tokens] float32 straddling-row partials
+  void* work;          // linear_workspace_bytes(*this) bytes, 256-byte aligned
   int64_t tokens, in_features, out_features, n;
   int log_block;
   int64_t nblocks_w;   // ceil(in*out / B)
@@ -64,6 +64,9 @@ extern const bool kLinearKernelAvailable;
 // in_features % 8 == 0, at most 64 output rows per generated block.
 bool linear_applicable(int dtype, int log_block, int64_t in_features);
 int linear_token_splits(const LinearArgs& a);
+// Workspace of one call: float32 partial dot products of the rows that
+// straddle two blocks, then (for large batches) x re-laid out in MFMA order.
+size_t linear_workspace_bytes(const LinearArgs& a);
 hipError_t launch_linear(const LinearArgs& a, hipStream_t s);
 
 }  // namespace lwl

@@ -16,6 +16,12 @@
 // adds the two halves of each straddling row (two terms: the sum does not
 // depend on the order).  Rows inside the block are written directly.
 //
+// x is read as MFMA A operands: per k step, lane (l16, kq) holds the 8 values
+// k = 32*step + 8*kq .. +7 of token 16*tile + l16.  Read in place from the
+// row-major [tokens, in] input, one such load touches 16 rows x 64 bytes, and
+// every generated block re-reads all of x, so for large batches x is first
+// re-laid out (bfht_linear_tile_x) so that each load reads 1 KiB contiguous.
+//
 // Reference kernel: csrc/block_fht_ext_cuda.cu:225-329 (which regenerates each
 // block per 8-token tile and requires block_size % in_features == 0).
 #include "bfht_mfma_chain.h"
@@ -50,7 +56,46 @@ __host__ __device__ constexpr int linear_steps(int64_t in_features) {
   return (int)(((in_features + kKStep - 1) / kKStep + kDepth - 1) / kDepth * kDepth);
 }
 
-template <int L, int NT>
+// Batches from this many tokens read x from the tiled copy.
+constexpr int64_t kTiledMinTokens = 256;
+
+// Tiled x: for token tile T (16 tokens) and k step s, 64 16-byte chunks in
+// lane order, chunk (l16 + 16*kq) = x[16*T + l16][32*s + 8*kq .. +7]; tokens
+// past the end and k past the row are zero.
+struct XTiling {
+  int64_t tiles;  // token tiles
+  int steps;      // k steps holding data: ceil(in / 32)
+  size_t bytes() const { return (size_t)tiles * (size_t)steps * 1024; }
+};
+
+XTiling x_tiling(const LinearArgs& a) {
+  return XTiling{(a.tokens + kTokTile - 1) / kTokTile, (int)((a.in_features + kKStep - 1) / kKStep)};
+}
+
+// buffer offsets into the tiled copy stay below 2^31 (the out-of-range voffset is 2^31)
+bool linear_tiled(const LinearArgs& a) {
+  return a.tokens >= kTiledMinTokens && x_tiling(a).bytes() < ((size_t)1 << 31);
+}
+
+size_t partial_bytes(const LinearArgs& a) {
+  return ((size_t)a.nblocks_w * 2 * (size_t)a.tokens * sizeof(float) + 255) / 256 * 256;
+}
+
+__global__ __launch_bounds__(256) void bfht_linear_tile_x(const __bf16* __restrict__ x, u32x4* __restrict__ xt,
+                                                          int tokens, int in_f, int steps, int64_t chunks) {
+  const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * in_f * 2));
+  for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < chunks; j += (int64_t)gridDim.x * 256) {
+    const int lane = (int)(j & 63);
+    const int64_t r = j >> 6;
+    const int s = (int)(r % steps);
+    const int t = (int)(r / steps) * kTokTile + (lane & 15);
+    const int k = kKStep * s + 8 * (lane >> 4);
+    const bool in_range = t < tokens && k < in_f;
+    xt[j] = __builtin_amdgcn_raw_buffer_load_b128(x_r, in_range ? (t * in_f + k) * 2 : (int)0x80000000, 0, 0);
+  }
+}
+
+template <int L, int NT, bool kTiled>
 __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __restrict__ x,
                                                                const __bf16* __restrict__ latent,
                                                                __bf16* __restrict__ out,
@@ -109,7 +154,11 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   const int tt1 = (tt0 + per_split < ntiles_tok) ? tt0 + per_split : ntiles_tok;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, kq = lane >> 4;  // A/B: row/col l16, k = 8*kq + j
-  const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * in_f * 2));  // offsets past the end read 0
+  // x: the tiled copy (kTiled) or the row-major input; offsets past the end read 0
+  const int xsteps = (in_f + kKStep - 1) / kKStep;
+  const int ntiles_all = (tokens + kTokTile - 1) / kTokTile;
+  const auto x_r = rsrc(x, kTiled ? (uint32_t)((int64_t)ntiles_all * xsteps * 1024)
+                                  : (uint32_t)((int64_t)tokens * in_f * 2));
   float* part_first = partial + (block * 2 + 0) * (int64_t)tokens;
   float* part_last = partial + (block * 2 + 1) * (int64_t)tokens;
   const u32x4* brow = table + kq * kRows + l16;  // + step*4*kRows + 16*nt
@@ -124,23 +173,37 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
 #pragma unroll
     for (int g = 0; g < kGroup; ++g) {
       const int tt = tg + g, t = tt * kTokTile + l16;
-      xo[g] = (tt < tt1 && t < tokens) ? (uint32_t)((t * in_f + 8 * kq) * 2) : kOff;
+      if constexpr (kTiled)
+        xo[g] = tt < tt1 ? (uint32_t)((tt * xsteps * 64 + lane) * 16) : kOff;
+      else
+        xo[g] = (tt < tt1 && t < tokens) ? (uint32_t)((t * in_f + 8 * kq) * 2) : kOff;
     }
-    // lanes whose 8 k-values of the step lie past the row (in % 8 == 0: all or none) read 0
+    // steps past the row (row-major: the lanes whose 8 k-values lie past it,
+    // all or none as in % 8 == 0) read 0
     auto xload = [&](int g, int step) -> u32x4 {
-      const uint32_t off = (step * kKStep + 8 * kq < in_f) ? xo[g] : kOff;
-      return __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)off, step * kKStep * 2, 0);
+      if constexpr (kTiled) {
+        const uint32_t off = step < xsteps ? xo[g] : kOff;
+        return __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)off, step * 1024, 0);
+      } else {
+        const uint32_t off = (step * kKStep + 8 * kq < in_f) ? xo[g] : kOff;
+        return __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)off, step * kKStep * 2, 0);
+      }
     };
     f32x4v acc[kGroup][NT];
 #pragma unroll
     for (int g = 0; g < kGroup; ++g)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) acc[g][nt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    // Issue the first kDepth steps' loads in slot order, the order the loop
+    // refills them in: the wait counts the compiler derives at the loop
+    // head then let slot d's data arrive behind the later slots' requests.
     u32x4 ring[kDepth][kGroup];
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d)
+    for (int d = 0; d < kDepth; ++d) {
 #pragma unroll
       for (int g = 0; g < kGroup; ++g) ring[d][g] = xload(g, d);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     const u32x4* bs = brow;
     for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
 #pragma unroll
@@ -149,16 +212,17 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) bt[nt] = bs[16 * nt];
         bs += 4 * kRows;
-        u32x4 a[kGroup];
-#pragma unroll
-        for (int g = 0; g < kGroup; ++g) {
-          a[g] = ring[d][g];
-          ring[d][g] = xload(g, s0 + d + kDepth);
-        }
 #pragma unroll
         for (int g = 0; g < kGroup; ++g)
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) acc[g][nt] = mfma16(a[g], bt[nt], acc[g][nt]);
+          for (int nt = 0; nt < NT; ++nt) acc[g][nt] = mfma16(ring[d][g], bt[nt], acc[g][nt]);
+        // Refill slot d only after its last use, so the load writes the
+        // slot's own registers: a load issued earlier would need a second
+        // register set and a copy (with a wait on the fresh load) at the
+        // loop back-edge, which serialises the whole prefetch.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g) ring[d][g] = xload(g, s0 + d + kDepth);
       }
     }
     // D[m = 4*kq + r][n = l16]
@@ -201,15 +265,14 @@ __global__ __launch_bounds__(256) void bfht_linear_combine(const float* __restri
   out[(int64_t)t * out_f + o] = (__bf16)(scale * v);
 }
 
-template <int L>
-hipError_t launch_linear_L(const LinearArgs& a, hipStream_t s) {
+template <int L, bool kTiled>
+hipError_t launch_linear_L(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
   const int nt = (int)linear_row_tiles(a.in_features);
   const dim3 grid((unsigned)(a.nblocks_w * a.token_splits)), block(mfma15::kThreads);
-  auto* x = (const __bf16*)a.x;
   auto* lat = (const __bf16*)a.latent;
   auto* o = (__bf16*)a.out;
-#define LWL_LIN(NT)                                                                                           \
-  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT>), grid, block, 0, s, x, lat, o, a.partial, (int)a.tokens,      \
+#define LWL_LIN(NT)                                                                                             \
+  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT, kTiled>), grid, block, 0, s, x, lat, o, partial, (int)a.tokens, \
                      (int)a.in_features, (int)a.out_features, (int)a.n, a.seed32, a.weight_scale, a.token_splits)
   switch (nt) {
     case 1: LWL_LIN(1); break;
@@ -222,9 +285,24 @@ hipError_t launch_linear_L(const LinearArgs& a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.nblocks_w < 2) return e;
   hipLaunchKernelGGL(bfht_linear_combine, dim3((unsigned)((a.tokens + 255) / 256), (unsigned)(a.nblocks_w - 1)),
-                     dim3(256), 0, s, (const float*)a.partial, o, (int)a.tokens, (int)a.in_features,
+                     dim3(256), 0, s, (const float*)partial, o, (int)a.tokens, (int)a.in_features,
                      (int)a.out_features, a.nblocks_w, a.weight_scale);
   return hipGetLastError();
+}
+
+template <int L>
+hipError_t launch_linear_L(const LinearArgs& a, hipStream_t s) {
+  float* partial = (float*)a.work;
+  if (!linear_tiled(a)) return launch_linear_L<L, false>(a, (const __bf16*)a.x, partial, s);
+  const XTiling xt = x_tiling(a);
+  auto* tiled = reinterpret_cast<u32x4*>((unsigned char*)a.work + partial_bytes(a));
+  const int64_t chunks = (int64_t)xt.bytes() / 16;
+  const int64_t grid = std::min<int64_t>((chunks + 255) / 256, 4096);
+  hipLaunchKernelGGL(bfht_linear_tile_x, dim3((unsigned)grid), dim3(256), 0, s, (const __bf16*)a.x, tiled,
+                     (int)a.tokens, (int)a.in_features, xt.steps, chunks);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_linear_L<L, true>(a, (const __bf16*)tiled, partial, s);
 }
 
 }  // namespace
@@ -238,6 +316,10 @@ bool linear_applicable(int dtype, int log_block, int64_t in_features) {
   const int64_t nt = linear_row_tiles(in_features);
   const int64_t table_bytes = (int64_t)4 * linear_steps(in_features) * 16 * nt * 16;
   return nt <= kMaxNT && table_bytes <= mfma15::kLdsBytes;
+}
+
+size_t linear_workspace_bytes(const LinearArgs& a) {
+  return partial_bytes(a) + (linear_tiled(a) ? x_tiling(a).bytes() : 0);
 }
 
 int linear_token_splits(const LinearArgs& a) {

@@ -159,6 +159,11 @@ def test_linear_validation(args, code, msg):
 
 
 def test_linear_workspace_size():
-    # one pair of float32 partial rows (first / last row of the block) per generated block and token
+    # one pair of float32 partial rows (first / last row of the block) per generated block and token,
+    # then, from 256 tokens, x re-laid out in 16-token x 32-k tiles of 1 KiB (zero-padded)
     lib = N.lib()
-    assert lib.lwl_bfht_linear_forward_workspace_size(4096, 768, 3072, 32768) == 72 * 2 * 4096 * 4
+    assert lib.lwl_bfht_linear_forward_workspace_size(4096, 768, 3072, 32768) == 72 * 2 * 4096 * 4 + 256 * 24 * 1024
+    partial = (18 * 2 * 255 * 4 + 255) // 256 * 256
+    assert lib.lwl_bfht_linear_forward_workspace_size(255, 768, 768, 32768) == partial
+    partial = (14 * 2 * 300 * 4 + 255) // 256 * 256
+    assert lib.lwl_bfht_linear_forward_workspace_size(300, 1000, 450, 32768) == partial + 19 * 32 * 1024

@@ -38,7 +38,9 @@ def oracle_linear(x: torch.Tensor, latent: torch.Tensor, out_f: int, layers: int
         (1, 768, 768, 32768, 2, 101, 2.0),      # decode batch 1, proj shape
         (64, 1024, 100, 20000, 1, -7, 1.0),     # in divides 2^15; last block partial; latent padded
         (33, 2048, 40, 32768, 3, 9, 0.25),      # rows of 2048 (16 per block)
-        (300, 1000, 77, 30000, 2, 5, 1.0),      # in % 16 != 0, rows straddle blocks
+        (300, 1000, 77, 30000, 2, 5, 1.0),      # in % 16 != 0, rows straddle blocks; tiled x, padded
+        (255, 1024, 200, 32768, 2, 21, 1.0),    # just below the tiled-x batch size: x read in place
+        (257, 1024, 200, 32768, 2, 21, 1.0),    # just above it: tiled x, last tile holds one token
     ],
 )
 def test_fused_linear_matches_oracle(tokens, in_f, out_f, n, layers, seed, scale):
