@@ -130,7 +130,7 @@ int check_linear(int dtype, int64_t tokens, int64_t in_features, int64_t latent_
   if (!lwl::linear_applicable(dtype, lb, in_features))
     return fail(LWL_ERR_UNSUPPORTED,
                 "fused linear forward takes bfloat16 latents of length 16385..32768 (block 2^15) with "
-                "in_features %% 8 == 0 and in_features >= 521 (dtype code %d, latent size %lld, in_features %lld)",
+                "in_features %% 8 == 0 and 528 <= in_features <= 5120 (dtype code %d, latent size %lld, in_features %lld)",
                 dtype, (long long)latent_size, (long long)in_features);
   if (tokens * in_features * 2 >= ((int64_t)1 << 31))
     return fail(LWL_ERR_UNSUPPORTED, "fused linear forward: tokens * in_features must stay below 2^30");

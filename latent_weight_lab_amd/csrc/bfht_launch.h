@@ -61,7 +61,8 @@ struct LinearArgs {
 constexpr int kLinearMaxInFeatures = 32768;
 extern const bool kLinearKernelAvailable;
 // Shapes the fused kernel (bfht_linear.hip) takes: bf16 blocks of 2^15,
-// in_features % 8 == 0, at most 64 output rows per generated block.
+// in_features % 8 == 0 and 528 <= in_features <= 5120 (at most 64 output rows per
+// generated block, and their k-major table fits in the LDS).
 bool linear_applicable(int dtype, int log_block, int64_t in_features);
 int linear_token_splits(const LinearArgs& a);
 // Workspace of one call: float32 partial dot products of the rows that

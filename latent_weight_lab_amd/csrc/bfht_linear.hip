@@ -44,8 +44,12 @@ __device__ __forceinline__ f32x4v mfma16(u32x4 a, u32x4 b, f32x4v c) {
 }
 
 // Up to kMaxNT tiles of 16 output rows per block (in_features >= 2^15/(16*kMaxNT - 2)), and the
-// k-major table (4*ceil(in/32) chunks x 16*NT rows x 16 bytes) must fit in the LDS.
+// k-major table (4*linear_steps(in) chunks x 16*NT rows x 16 bytes) must fit in the
+// workgroup's LDS (all 160 KiB of a gfx950 CU; the generator's exchange uses the first 128).
+// Together: in_features % 8 == 0 and 528 <= in_features <= 5120.
 constexpr int kMaxNT = 4;
+constexpr int kLinearLdsBytes = 160 * 1024;
+static_assert(kLinearLdsBytes >= kLdsBytes, "the generator chain runs in the same LDS");
 
 __host__ __device__ constexpr int64_t linear_row_tiles(int64_t in_features) {
   return ((kB + in_features - 1) / in_features + 1 + 15) / 16;  // incl. two partial rows
@@ -102,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
                                                                float* __restrict__ partial, int tokens,
                                                                int in_f, int out_f, int n, uint32_t seed32,
                                                                float scale, int token_split) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLinearLdsBytes];
   const int64_t block = blockIdx.x / token_split;
   const int split = blockIdx.x % token_split;
   constexpr int kRows = 16 * NT;  // table rows (output rows of the block, zero-padded)
@@ -315,7 +319,7 @@ bool linear_applicable(int dtype, int log_block, int64_t in_features) {
   if (dtype != kBF16 || log_block != mfma15::kLog || in_features % 8 != 0 || in_features > mfma15::kB) return false;
   const int64_t nt = linear_row_tiles(in_features);
   const int64_t table_bytes = (int64_t)4 * linear_steps(in_features) * 16 * nt * 16;
-  return nt <= kMaxNT && table_bytes <= mfma15::kLdsBytes;
+  return nt <= kMaxNT && table_bytes <= kLinearLdsBytes;
 }
 
 size_t linear_workspace_bytes(const LinearArgs& a) {

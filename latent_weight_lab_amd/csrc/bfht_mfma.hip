@@ -14,7 +14,9 @@ namespace {
 
 // ---------------------------------------------------------------- forward
 
-template <int L>
+// kWhole: every block is written whole to a 16-byte aligned place and n % 8
+// == 0 (the launcher checks), so no partial-chunk paths are needed.
+template <int L, bool kWhole>
 __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __restrict__ latent,
                                                             __bf16* __restrict__ out, int n,
                                                             int64_t first_block, int64_t start,
@@ -23,7 +25,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
   const int64_t block = first_block + blockIdx.x;
   const Ctx x = make_ctx(seed32, block);
   u32x4 src[kTiles][2];
-  load_latent(x, latent, n, src);
+  load_latent<kWhole>(x, latent, n, src);
   f32x16 acc[kTiles];
   uint32_t nw[4];
   run_chain<L>(acc, x, lds, src, [](int i) { return i; }, nw);
@@ -34,10 +36,10 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
   __syncthreads();
   // block-local output range [lo, hi); out element of block position p is (base - start) + p
   const int64_t base = block * kB;
-  const int lo = (int)(start - base > 0 ? start - base : 0);
-  const int hi = (int)(stop - base < kB ? stop - base : kB);
+  const int lo = kWhole ? 0 : (int)(start - base > 0 ? start - base : 0);
+  const int hi = kWhole ? kB : (int)(stop - base < kB ? stop - base : kB);
   __bf16* oblk = out + (base - start);
-  const bool full = lo == 0 && hi == kB && (((uintptr_t)oblk & 15) == 0);
+  const bool full = kWhole || (lo == 0 && hi == kB && (((uintptr_t)oblk & 15) == 0));
   const auto out_r = rsrc(full ? (const void*)oblk : (const void*)out, full ? (uint32_t)(kB * 2) : 0u);
   uint16_t* oblk16 = reinterpret_cast<uint16_t*>(oblk);
   constexpr int kPer = kChunks / kThreads;
@@ -45,7 +47,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int c = i * kThreads + (int)threadIdx.x;
-    v[i] = stage[c ^ ((c >> 4) & 3)];
+    v[i] = stage[stage_slot(c)];
   }
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -64,7 +66,9 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
 
 // Per-block partial latent gradient (float32, first n positions) of the
 // adjoint chain D_0 H D_1 ... H D_L applied to grad scattered into the block.
-template <int L>
+// kWhole: every block's gradient is read whole from a 16-byte aligned place
+// and n % 4 == 0 (the launcher checks), so no partial-chunk paths are needed.
+template <int L, bool kWhole>
 __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __restrict__ grad,
                                                             float* __restrict__ partial, int n,
                                                             int64_t first_block, int64_t start,
@@ -74,10 +78,10 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
   const int64_t block = first_block + slot;
   const Ctx x = make_ctx(seed32, block);
   const int64_t base = block * kB;
-  const int lo = (int)(start - base > 0 ? start - base : 0);
-  const int hi = (int)(stop - base < kB ? stop - base : kB);
+  const int lo = kWhole ? 0 : (int)(start - base > 0 ? start - base : 0);
+  const int hi = kWhole ? kB : (int)(stop - base < kB ? stop - base : kB);
   const __bf16* gblk = grad + (base - start);
-  const bool full = lo == 0 && hi == kB && (((uintptr_t)gblk & 15) == 0);
+  const bool full = kWhole || (lo == 0 && hi == kB && (((uintptr_t)gblk & 15) == 0));
   const auto g_r = rsrc(full ? (const void*)gblk : (const void*)grad, full ? (uint32_t)(kB * 2) : 0u);
   const uint16_t* gblk16 = reinterpret_cast<const uint16_t*>(gblk);
   u32x4 src[kTiles][2];
@@ -99,11 +103,14 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
 
   // D_0, then the float32 partial row of the first n positions, staged through
-  // the exchange space (128 KiB; 4-float chunk c at c ^ ((c >> 4) & 15)).
+  // the exchange space (128 KiB; 4-float chunk c at c ^ ((c >> 3) & 7): the
+  // lanes of one write hold chunks 8 apart, and this XOR spreads 8 of them
+  // over the 8 16-byte bank groups of a 128-byte row, while every aligned
+  // group of 8 chunks stays in place for the consecutive reads).
   auto flip = [](float v, uint32_t w, int b) {
     return __uint_as_float(__float_as_uint(v) ^ ((w << (31 - b)) & 0x80000000u));
   };
-  f32x4* stage = reinterpret_cast<f32x4*>(lds);  // 128 KiB of the 132
+  f32x4* stage = reinterpret_cast<f32x4*>(lds);  // all 128 KiB
   __syncthreads();  // every wave has read its last exchange
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -126,7 +133,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
       for (int e = 0; e < 4; ++e) v[e] = flip(acc[t][r0 + e], w, (p & 31) + e);
     }
     const int c = p >> 2;
-    stage[c ^ ((c >> 4) & 15)] = v;
+    stage[c ^ ((c >> 3) & 7)] = v;
   }
   __syncthreads();
   float* prow = partial + slot * (int64_t)n;
@@ -134,10 +141,10 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
 #pragma unroll
   for (int i = 0; i < (kB / 4) / kThreads; ++i) {
     const int c = i * kThreads + (int)threadIdx.x;
-    const f32x4 v = stage[c ^ ((c >> 4) & 15)];
+    const f32x4 v = stage[c ^ ((c >> 3) & 7)];
     const int p = c * 4;
-    if (p + 4 <= n) {
-      __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, 0);
+    if (kWhole || p + 4 <= n) {
+      __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, 0);  // dropped past n
     } else if (p < n) {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -156,28 +163,43 @@ bool mfma15_applicable(const BfhtArgs& a) {
   return a.dtype == kBF16 && a.log_block == mfma15::kLog && a.nblocks > 0 && a.n <= mfma15::kB && aligned;
 }
 
-hipError_t launch_mfma15(const BfhtArgs& a, hipStream_t s, bool fwd) {
+namespace {
+
+template <bool kWhole>
+hipError_t launch_mfma15_shape(const BfhtArgs& a, hipStream_t s, bool fwd) {
   using namespace mfma15;
   const dim3 grid((unsigned)a.nblocks), block(kThreads);
   auto* src = (const __bf16*)a.src;
+  const int n = (int)a.n;
   if (fwd) {
     auto* dst = (__bf16*)a.dst;
     switch (a.layers) {
-      case 1: hipLaunchKernelGGL(bfht_mfma15_fwd<1>, grid, block, 0, s, src, dst, (int)a.n, a.first_block, a.start, a.stop, a.seed32); break;
-      case 2: hipLaunchKernelGGL(bfht_mfma15_fwd<2>, grid, block, 0, s, src, dst, (int)a.n, a.first_block, a.start, a.stop, a.seed32); break;
-      case 3: hipLaunchKernelGGL(bfht_mfma15_fwd<3>, grid, block, 0, s, src, dst, (int)a.n, a.first_block, a.start, a.stop, a.seed32); break;
+      case 1: hipLaunchKernelGGL((bfht_mfma15_fwd<1, kWhole>), grid, block, 0, s, src, dst, n, a.first_block, a.start, a.stop, a.seed32); break;
+      case 2: hipLaunchKernelGGL((bfht_mfma15_fwd<2, kWhole>), grid, block, 0, s, src, dst, n, a.first_block, a.start, a.stop, a.seed32); break;
+      case 3: hipLaunchKernelGGL((bfht_mfma15_fwd<3, kWhole>), grid, block, 0, s, src, dst, n, a.first_block, a.start, a.stop, a.seed32); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
   }
   auto* part = (float*)a.work;
   switch (a.layers) {
-    case 1: hipLaunchKernelGGL(bfht_mfma15_bwd<1>, grid, block, 0, s, src, part, (int)a.n, a.first_block, a.start, a.stop, a.seed32); break;
-    case 2: hipLaunchKernelGGL(bfht_mfma15_bwd<2>, grid, block, 0, s, src, part, (int)a.n, a.first_block, a.start, a.stop, a.seed32); break;
-    case 3: hipLaunchKernelGGL(bfht_mfma15_bwd<3>, grid, block, 0, s, src, part, (int)a.n, a.first_block, a.start, a.stop, a.seed32); break;
+    case 1: hipLaunchKernelGGL((bfht_mfma15_bwd<1, kWhole>), grid, block, 0, s, src, part, n, a.first_block, a.start, a.stop, a.seed32); break;
+    case 2: hipLaunchKernelGGL((bfht_mfma15_bwd<2, kWhole>), grid, block, 0, s, src, part, n, a.first_block, a.start, a.stop, a.seed32); break;
+    case 3: hipLaunchKernelGGL((bfht_mfma15_bwd<3, kWhole>), grid, block, 0, s, src, part, n, a.first_block, a.start, a.stop, a.seed32); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_mfma15(const BfhtArgs& a, hipStream_t s, bool fwd) {
+  using namespace mfma15;
+  // whole blocks: [start, stop) covers exactly blocks first_block .. +nblocks, and the
+  // slice base (out / grad) is 16-byte aligned, so every block's base is too
+  const bool whole = a.start == a.first_block * kB && a.stop == (a.first_block + a.nblocks) * kB &&
+                     (uintptr_t)a.dst % 16 == 0 && (uintptr_t)a.src % 16 == 0 && a.n % 8 == 0;
+  return whole ? launch_mfma15_shape<true>(a, s, fwd) : launch_mfma15_shape<false>(a, s, fwd);
 }
 
 }  // namespace lwl

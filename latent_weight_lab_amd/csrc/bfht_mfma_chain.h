@@ -60,10 +60,11 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTiles = 4;
 constexpr int kChunks = kB / 8;  // 16-byte chunks of 8 bf16 in one block
-// Exchange buffers: 4096 16-byte chunks with 8 bytes of padding after every
-// 16 chunks, so that the 8-byte writes of lanes l and l + 16 hit different
-// banks; two buffers back to back (132 KiB).
-constexpr int kXBufBytes = kChunks * 16 + (kChunks / 16) * 8;
+// Exchange buffers: 4096 16-byte chunks, stored as two 32 KiB halves (bytes
+// 0-7 of every chunk, then bytes 8-15), so that the 8-byte writes and reads
+// of consecutive lanes cover consecutive LDS bytes (any gap between lanes
+// costs LDS cycles in proportion); two buffers back to back (128 KiB).
+constexpr int kXBufBytes = kChunks * 16;
 constexpr int kLdsBytes = 2 * kXBufBytes;
 constexpr uint32_t kPairSign = 0x80008000u;
 
@@ -225,28 +226,28 @@ __device__ __forceinline__ void stage_rows(f32x16 (&acc)[kTiles], const u32x4 (&
 // 8-byte half (its 4 tiles at register r), the half being wave bit 0:
 //   write: id = lane32 + (r&7)<<5 + l5<<8 + (r>>3)<<9 + (wave>>1)<<10, half = wave & 1
 //   read:  id = lane32 + t<<5 + wave<<7 + l5<<10 + c<<11 (whole chunk = B operand)
-// 8-byte slot of (id, half) in a padded buffer: 2*id + (id >> 4) + half.
-__device__ __forceinline__ int xslot(int id) { return 2 * id + (id >> 4); }
-
+// Half h of chunk id is 8-byte slot h * kChunks + id.
 __device__ __forceinline__ void exchange_write(const f32x16 (&acc)[kTiles], u32x2* xbuf, const Ctx& x) {
+  u32x2* half = xbuf + (x.wave & 1) * kChunks + x.wid;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     u32x2 v;
     v[0] = pk(acc[0][r], acc[1][r]);
     v[1] = pk(acc[2][r], acc[3][r]);
-    xbuf[xslot(x.wid + ((r & 7) << 5) + ((r >> 3) << 9)) + (x.wave & 1)] = v;
+    half[((r & 7) << 5) + ((r >> 3) << 9)] = v;
   }
 }
 
 __device__ __forceinline__ void exchange_read_stage_c(f32x16 (&acc)[kTiles], const u32x4 (&h)[2],
                                                       const u32x2* xbuf, const Ctx& x) {
   u32x4 b[kTiles][2];
+  const u32x2* lo_half = xbuf + x.rid;
 #pragma unroll
   for (int t = 0; t < kTiles; ++t)
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const int sl = xslot(x.rid + (t << 5) + (c << 11));
-      const u32x2 lo = xbuf[sl], hi = xbuf[sl + 1];
+      const int id = (t << 5) + (c << 11);
+      const u32x2 lo = lo_half[id], hi = lo_half[kChunks + id];
       b[t][c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
   const f32x16 zero = {};
@@ -282,15 +283,11 @@ template <int L, class SignLayer>
 __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, unsigned char* lds,
                                           const u32x4 (&src)[kTiles][2], SignLayer sign_layer,
                                           uint32_t (&fin)[4]) {
+  // The words of sign layer i + 1 are hashed during layer i, after its stage
+  // a: the VALU work then overlaps stage b's matrix-core work instead of
+  // delaying the first stage.
   uint32_t nw[L][4];
-#pragma unroll
-  for (int i = 0; i < L; ++i) {
-    if (i & 1)
-      layer_words<true>(x, sign_layer(i), nw[i]);
-    else
-      layer_words<false>(x, sign_layer(i), nw[i]);
-  }
-  final_words<L>(x, sign_layer(L), fin);
+  layer_words<false>(x, sign_layer(0), nw[0]);
   const int lane = threadIdx.x & 63;
   // Stage a: Q/4 (even layers), S/4 (odd); stage b: Q/8; stage c: S/4 (even),
   // Q/4 (odd); the last stage c carries the residual 2^(-L/2): S/4*2^-0.5
@@ -319,6 +316,14 @@ __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, u
       stage_rows<true, true>(acc, hs4, nw[i]);
     } else {
       stage_rows<true, false>(acc, hq4, nw[i]);
+    }
+    if (i + 1 < L) {
+      if ((i + 1) & 1)
+        layer_words<true>(x, sign_layer(i + 1), nw[i + 1]);
+      else
+        layer_words<false>(x, sign_layer(i + 1), nw[i + 1]);
+    } else {
+      final_words<L>(x, sign_layer(L), fin);
     }
     stage_rows<false, false>(acc, hq8, nw[i]);
     u32x2* xbuf = reinterpret_cast<u32x2*>(lds + (i & 1) * kXBufBytes);
@@ -396,26 +401,30 @@ __device__ __forceinline__ u32x4 out_chunk(const f32x16 (&acc)[kTiles], const ui
   return v;
 }
 
+// Slot of 16-byte output chunk c in the staging buffer.  The lanes of one
+// staging write hold chunks 4 apart (c = 4 * lane32 + const); XOR-ing bits
+// 3-4 into bits 0-1 spreads any 8 consecutive lanes over the 8 16-byte bank
+// groups of a 128-byte LDS row, and every aligned group of 8 chunks stays in
+// place as a whole, so reads of consecutive chunks are conflict-free too.
+__device__ __forceinline__ int stage_slot(int c) { return c ^ ((c >> 3) & 3); }
+
 // Stages the chain's result (acc, before the last sign layer, words `nw`) as
-// signed bf16 in block-position order into `stage` (4096 16-byte chunks;
-// chunk c at c ^ ((c >> 4) & 3): conflict-free for these writes and for reads
-// of consecutive chunks).  The caller synchronizes before reading.
+// signed bf16 in block-position order into `stage` (4096 16-byte chunks at
+// stage_slot(c)).  The caller synchronizes before reading.
 template <int L>
 __device__ __forceinline__ void stage_output(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4], const Ctx& x,
                                              u32x4* stage) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int c = out_chunk_pos<L>(x, k) >> 3;
-    stage[c ^ ((c >> 4) & 3)] = out_chunk<L>(acc, nw, x, k);
-  }
+  for (int k = 0; k < 8; ++k) stage[stage_slot(out_chunk_pos<L>(x, k) >> 3)] = out_chunk<L>(acc, nw, x, k);
 }
 
 // Loads the S0 source operands of a block from the latent (n bf16 elements,
-// zero past the end).
+// zero past the end).  kExact: n % 8 == 0, so no 16-byte chunk straddles the end.
+template <bool kExact = false>
 __device__ __forceinline__ void load_latent(const Ctx& x, const __bf16* latent, int n, u32x4 (&src)[kTiles][2]) {
   const auto lat_r = rsrc(latent, (uint32_t)n * 2u);
   const uint16_t* lat16 = reinterpret_cast<const uint16_t*>(latent);
-  const bool tail = (n & 7) != 0;
+  const bool tail = !kExact && (n & 7) != 0;
   load_source(
       x,
       [&](int p) -> u32x4 {

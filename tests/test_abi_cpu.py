@@ -146,6 +146,10 @@ def test_next_power_of_two():
         ((2, 16, 768, 16384, 3072, 3), N.LWL_ERR_UNSUPPORTED, "bfloat16"),  # block 2^14
         ((2, 16, 100, 32768, 30, 3), N.LWL_ERR_UNSUPPORTED, "in_features"),  # in % 8 != 0, >64 rows
         ((2, 16, 40000, 32768, 3, 3), N.LWL_ERR_UNSUPPORTED, "block_size"),  # in > B
+        ((2, 16, 520, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "528 <= in_features <= 5120"),  # > 64 rows per block
+        ((2, 16, 528, 32768, 64, 3), N.LWL_OK, ""),                # 62 rows + 2 partial: 4 row tiles
+        ((2, 16, 5120, 32768, 64, 3), N.LWL_OK, ""),               # largest k-major table (160 KiB)
+        ((2, 16, 5128, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "528 <= in_features <= 5120"),  # table too big
         ((2, 16, 768, 32768, 3072, 4), N.LWL_ERR_INVALID, "layers must be 1, 2, or 3"),
         ((2, 16, 0, 32768, 3072, 3), N.LWL_ERR_INVALID, "in_features must be positive"),
         ((2, 1 << 20, 1024, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "2^30"),

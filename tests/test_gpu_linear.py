@@ -41,6 +41,8 @@ def oracle_linear(x: torch.Tensor, latent: torch.Tensor, out_f: int, layers: int
         (300, 1000, 77, 30000, 2, 5, 1.0),      # in % 16 != 0, rows straddle blocks; tiled x, padded
         (255, 1024, 200, 32768, 2, 21, 1.0),    # just below the tiled-x batch size: x read in place
         (257, 1024, 200, 32768, 2, 21, 1.0),    # just above it: tiled x, last tile holds one token
+        (20, 528, 200, 32768, 3, 31, 1.0),      # smallest in_features: 4 row tiles per block
+        (40, 5120, 30, 32768, 2, 32, 1.0),      # largest: the k-major table fills all 160 KiB of LDS
     ],
 )
 def test_fused_linear_matches_oracle(tokens, in_f, out_f, n, layers, seed, scale):
