@@ -146,25 +146,71 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
 }
 
 // grad_latent[p] = sum_b part[b * stride + p], blocks in order.
-template <class T>
-__global__ __launch_bounds__(256) void bfht_reduce_blocks(const float* __restrict__ part,
-                                                         int64_t nblocks, int64_t stride, int n,
-                                                         T* __restrict__ grad_latent) {
-  const int p = blockIdx.x * 256 + threadIdx.x;
-  if (p >= n) return;
-  float acc = 0.0f;
-  const float* col = part + p;
-  int64_t b = 0;
-  for (; b + 4 <= nblocks; b += 4) {
-    const float a0 = col[(b + 0) * stride], a1 = col[(b + 1) * stride];
-    const float a2 = col[(b + 2) * stride], a3 = col[(b + 3) * stride];
-    acc += a0;
-    acc += a1;
-    acc += a2;
-    acc += a3;
+// Fixed-order sum of the per-block float32 partial rows: grad[p] = sum over b
+// of part[b * stride + p].  Each workgroup owns 128 columns (2 per lane); wave
+// w adds rows w, w + 8, w + 16, ... in ascending order with 16 row loads in
+// flight, and wave 0 adds the 8 wave sums in wave order, so the result does
+// not depend on timing.  (A single column walk per thread keeps only a few
+// loads in flight and leaves most of the chip idle for latent lengths of a
+// few 10^4.)
+constexpr int kRedWaves = 8;
+constexpr int kRedCols = 128;
+constexpr int kRedDepth = 16;
+
+template <class T, bool kPairs>
+__global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_blocks(const float* __restrict__ part,
+                                                                     int64_t nblocks, int64_t stride, int n,
+                                                                     T* __restrict__ grad_latent) {
+  __shared__ float sums[kRedWaves][2][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c0 = blockIdx.x * kRedCols + 2 * lane;
+  const bool has0 = c0 < n, has1 = c0 + 1 < n;
+  float a0 = 0.0f, a1 = 0.0f;
+  auto row = [&](int64_t b) -> float2 {
+    const float* r = part + b * stride + c0;
+    if (kPairs && has1) return *reinterpret_cast<const float2*>(r);
+    return float2{has0 ? r[0] : 0.0f, has1 ? r[1] : 0.0f};
+  };
+  int64_t b = wave;
+  for (; b + (int64_t)kRedWaves * (kRedDepth - 1) < nblocks; b += (int64_t)kRedWaves * kRedDepth) {
+    float2 v[kRedDepth];
+#pragma unroll
+    for (int j = 0; j < kRedDepth; ++j) v[j] = row(b + (int64_t)kRedWaves * j);
+#pragma unroll
+    for (int j = 0; j < kRedDepth; ++j) {
+      a0 += v[j].x;
+      a1 += v[j].y;
+    }
   }
-  for (; b < nblocks; ++b) acc += col[b * stride];
-  grad_latent[p] = from_f32<T>(acc);
+  for (; b < nblocks; b += kRedWaves) {
+    const float2 v = row(b);
+    a0 += v.x;
+    a1 += v.y;
+  }
+  sums[wave][0][lane] = a0;
+  sums[wave][1][lane] = a1;
+  __syncthreads();
+  if (wave != 0) return;
+  float t0 = 0.0f, t1 = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kRedWaves; ++w) {
+    t0 += sums[w][0][lane];
+    t1 += sums[w][1][lane];
+  }
+  if (has0) grad_latent[c0] = from_f32<T>(t0);
+  if (has1) grad_latent[c0 + 1] = from_f32<T>(t1);
+}
+
+template <class T>
+static hipError_t launch_reduce(const float* part, int64_t nblocks, int64_t stride, int64_t n, T* dst,
+                                hipStream_t s) {
+  const dim3 grid((unsigned)((n + kRedCols - 1) / kRedCols)), block(64 * kRedWaves);
+  // 8-byte row loads need even column offsets in every row: part is 256-byte aligned
+  if (stride % 2 == 0)
+    hipLaunchKernelGGL((bfht_reduce_blocks<T, true>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
+  else
+    hipLaunchKernelGGL((bfht_reduce_blocks<T, false>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
+  return hipGetLastError();
 }
 
 template <class T>
@@ -292,9 +338,7 @@ static hipError_t launch_block_bwd(const BfhtArgs& a, hipStream_t s) {
                      a.nblocks, a.start, a.stop, a.seed32, a.layers, direct);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || direct) return e;
-  hipLaunchKernelGGL((bfht_reduce_blocks<T>), dim3((unsigned)((a.n + 255) / 256)), dim3(256), 0, s,
-                     (const float*)a.work, a.nblocks, a.n, (int)a.n, (T*)a.dst);
-  return hipGetLastError();
+  return launch_reduce<T>((const float*)a.work, a.nblocks, a.n, a.n, (T*)a.dst, s);
 }
 
 template <class T>
@@ -334,10 +378,7 @@ static hipError_t run_tiles(const BfhtArgs& a, hipStream_t s, bool fwd) {
     if (e != hipSuccess) return e;
   }
   if (fwd) return hipSuccess;
-  hipLaunchKernelGGL((bfht_reduce_blocks<T>), dim3((unsigned)((a.n + 255) / 256)), dim3(256), 0, s,
-                     (const float*)a.work, a.nblocks, (int64_t)1 << a.log_block, (int)a.n,
-                     (T*)a.dst);
-  return hipGetLastError();
+  return launch_reduce<T>((const float*)a.work, a.nblocks, (int64_t)1 << a.log_block, a.n, (T*)a.dst, s);
 }
 
 template <class T>
@@ -351,9 +392,7 @@ static hipError_t run_typed(const BfhtArgs& a, hipStream_t s, bool fwd) {
   if (mfma15_applicable(a)) {
     hipError_t e = launch_mfma15(a, s, fwd);
     if (e != hipSuccess || fwd) return e;
-    hipLaunchKernelGGL((bfht_reduce_blocks<T>), dim3((unsigned)((a.n + 255) / 256)), dim3(256), 0, s,
-                       (const float*)a.work, a.nblocks, a.n, (int)a.n, (T*)a.dst);
-    return hipGetLastError();
+    return launch_reduce<T>((const float*)a.work, a.nblocks, a.n, a.n, (T*)a.dst, s);
   }
   if (a.log_block <= kTileLog)
     return dispatch_block<T>(a.log_block, fwd, a, s, std::make_integer_sequence<int, kTileLog + 1>{});

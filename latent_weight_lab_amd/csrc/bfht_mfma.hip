@@ -53,7 +53,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
   for (int i = 0; i < kPer; ++i) {
     const int p = (i * kThreads + (int)threadIdx.x) * 8;
     if (full) {
-      __builtin_amdgcn_raw_buffer_store_b128(v[i], out_r, p * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(v[i], out_r, p * 2, 0, kStreamStore);
     } else if (p + 8 > lo && p < hi) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
     const f32x4 v = stage[c ^ ((c >> 3) & 7)];
     const int p = c * 4;
     if (kWhole || p + 4 <= n) {
-      __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, 0);  // dropped past n
+      __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, kStreamStore);  // dropped past n
     } else if (p < n) {
 #pragma unroll
       for (int e = 0; e < 4; ++e)

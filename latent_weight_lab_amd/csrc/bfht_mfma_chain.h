@@ -333,6 +333,13 @@ __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, u
   }
 }
 
+// Cache policy of the kernels' large output stores: sc0 | sc1 (system scope)
+// writes through the XCD's L2.  The L2s of the XCDs are not coherent with each
+// other, so a kernel's end writes every dirty L2 line back before the next
+// kernel may read it; streaming the output through during the kernel instead
+// removes that serial write-back from each launch (about 1 us for 16 MiB).
+constexpr int kStreamStore = 1 | 16;
+
 // Raw buffer resource over `bytes` bytes at `base`: loads past the end read 0,
 // stores past the end are dropped (offsets are 32-bit).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
