@@ -64,11 +64,24 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd(const T* __restric
   float v[Gm::E];
   {
     const uint32_t w = sign_word(bkey, layer_key(0), word);
+    if constexpr (Gm::NG > 1) {
+      // coalesced: thread t loads positions k * TB + t, then takes its
+      // contiguous run from the (padded, conflict-free) LDS copy
 #pragma unroll
-    for (int r = 0; r < Gm::E; ++r) {
-      const int p = p0 + r;
-      const float x = p < n ? to_f32(latent[p]) : 0.0f;
-      v[r] = signed_by(x, w, p & 31);
+      for (int k = 0; k < Gm::E; ++k) {
+        const int p = k * Gm::TB + t;
+        lds[lds_index(p)] = p < n ? to_f32(latent[p]) : 0.0f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(lds[lds_index(p0 + r)], w, (p0 + r) & 31);
+    } else {
+#pragma unroll
+      for (int r = 0; r < Gm::E; ++r) {
+        const int p = p0 + r;
+        const float x = p < n ? to_f32(latent[p]) : 0.0f;
+        v[r] = signed_by(x, w, p & 31);
+      }
     }
   }
   const float scale = inv_sqrt_block<LB>();
@@ -78,14 +91,28 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd(const T* __restric
 #pragma unroll
     for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(v[r], w, (p0 + r) & 31) * scale;
   }
-  if (!active) return;
   const int64_t base = block * Gm::B;
   const int64_t lo = start - base > 0 ? start - base : 0;
   const int64_t hi = stop - base < Gm::B ? stop - base : Gm::B;
+  if constexpr (Gm::NG > 1) {
+    // back through the LDS, so that consecutive threads store consecutive positions
+    __syncthreads();  // the transform's last LDS reads are done
 #pragma unroll
-  for (int r = 0; r < Gm::E; ++r) {
-    const int p = p0 + r;
-    if (p >= lo && p < hi) out[base + p - start] = from_f32<T>(v[r]);
+    for (int r = 0; r < Gm::E; ++r) lds[lds_index(p0 + r)] = v[r];
+    __syncthreads();
+    if (!active) return;
+#pragma unroll
+    for (int k = 0; k < Gm::E; ++k) {
+      const int p = k * Gm::TB + t;
+      if (p >= lo && p < hi) out[base + p - start] = from_f32<T>(lds[lds_index(p)]);
+    }
+  } else {
+    if (!active) return;
+#pragma unroll
+    for (int r = 0; r < Gm::E; ++r) {
+      const int p = p0 + r;
+      if (p >= lo && p < hi) out[base + p - start] = from_f32<T>(v[r]);
+    }
   }
 }
 
@@ -116,10 +143,22 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
   const int64_t hi = stop - base < Gm::B ? stop - base : Gm::B;
 
   float v[Gm::E];
+  if constexpr (Gm::NG > 1) {
+    // coalesced loads through the LDS (see bfht_block_fwd)
 #pragma unroll
-  for (int r = 0; r < Gm::E; ++r) {
-    const int p = p0 + r;
-    v[r] = (active && p >= lo && p < hi) ? to_f32(grad[base + p - start]) : 0.0f;
+    for (int k = 0; k < Gm::E; ++k) {
+      const int p = k * Gm::TB + t;
+      lds[lds_index(p)] = (active && p >= lo && p < hi) ? to_f32(grad[base + p - start]) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < Gm::E; ++r) v[r] = lds[lds_index(p0 + r)];
+  } else {
+#pragma unroll
+    for (int r = 0; r < Gm::E; ++r) {
+      const int p = p0 + r;
+      v[r] = (active && p >= lo && p < hi) ? to_f32(grad[base + p - start]) : 0.0f;
+    }
   }
   const float scale = inv_sqrt_block<LB>();
   for (int layer = layers - 1; layer >= 0; --layer) {
@@ -130,17 +169,36 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
 #pragma unroll
     for (int r = 0; r < Gm::E; ++r) v[r] *= scale;
   }
-  if (!active) return;
   const uint32_t w0 = sign_word(bkey, layer_key(0), word);
+  if constexpr (Gm::NG > 1) {
+    __syncthreads();  // the transform's last LDS reads are done
 #pragma unroll
-  for (int r = 0; r < Gm::E; ++r) {
-    const int p = p0 + r;
-    if (p < n) {
-      const float g = signed_by(v[r], w0, p & 31);
-      if (direct)
-        grad_latent[p] = from_f32<T>(g);
-      else
-        partial[slot * (int64_t)n + p] = g;
+    for (int r = 0; r < Gm::E; ++r) lds[lds_index(p0 + r)] = signed_by(v[r], w0, (p0 + r) & 31);
+    __syncthreads();
+    if (!active) return;
+#pragma unroll
+    for (int k = 0; k < Gm::E; ++k) {
+      const int p = k * Gm::TB + t;
+      if (p < n) {
+        const float g = lds[lds_index(p)];
+        if (direct)
+          grad_latent[p] = from_f32<T>(g);
+        else
+          partial[slot * (int64_t)n + p] = g;
+      }
+    }
+  } else {
+    if (!active) return;
+#pragma unroll
+    for (int r = 0; r < Gm::E; ++r) {
+      const int p = p0 + r;
+      if (p < n) {
+        const float g = signed_by(v[r], w0, p & 31);
+        if (direct)
+          grad_latent[p] = from_f32<T>(g);
+        else
+          partial[slot * (int64_t)n + p] = g;
+      }
     }
   }
 }
