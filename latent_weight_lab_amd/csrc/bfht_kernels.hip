@@ -33,6 +33,17 @@ struct Geo {
   static constexpr int NG = (LB + 4) / 5;
   static constexpr int PADDED = B + (B >> 5);
   static constexpr int LDS_FLOATS = NG > 1 ? G * PADDED : 1;
+  // padded LDS index of position k * TB + t (coalesced order) and of t * E + r
+  // (a thread's own run), written so that the compiler sees a per-thread base
+  // plus a constant per k or r
+  __device__ static int coal(int t, int k) {
+    if constexpr (TB % 32 == 0) return t + (t >> 5) + k * (TB + TB / 32);
+    else return lds_index(k * TB + t);
+  }
+  __device__ static int own(int t, int r) {
+    if constexpr (E == 32) return t * 33 + r;
+    else return lds_index(t * E + r);
+  }
 };
 
 template <int LB>
@@ -70,11 +81,11 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd(const T* __restric
 #pragma unroll
       for (int k = 0; k < Gm::E; ++k) {
         const int p = k * Gm::TB + t;
-        lds[lds_index(p)] = p < n ? to_f32(latent[p]) : 0.0f;
+        lds[Gm::coal(t, k)] = p < n ? to_f32(latent[p]) : 0.0f;
       }
       __syncthreads();
 #pragma unroll
-      for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(lds[lds_index(p0 + r)], w, (p0 + r) & 31);
+      for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(lds[Gm::own(t, r)], w, (p0 + r) & 31);
     } else {
 #pragma unroll
       for (int r = 0; r < Gm::E; ++r) {
@@ -98,13 +109,13 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd(const T* __restric
     // back through the LDS, so that consecutive threads store consecutive positions
     __syncthreads();  // the transform's last LDS reads are done
 #pragma unroll
-    for (int r = 0; r < Gm::E; ++r) lds[lds_index(p0 + r)] = v[r];
+    for (int r = 0; r < Gm::E; ++r) lds[Gm::own(t, r)] = v[r];
     __syncthreads();
     if (!active) return;
 #pragma unroll
     for (int k = 0; k < Gm::E; ++k) {
       const int p = k * Gm::TB + t;
-      if (p >= lo && p < hi) out[base + p - start] = from_f32<T>(lds[lds_index(p)]);
+      if (p >= lo && p < hi) out[base + p - start] = from_f32<T>(lds[Gm::coal(t, k)]);
     }
   } else {
     if (!active) return;
@@ -148,11 +159,11 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
 #pragma unroll
     for (int k = 0; k < Gm::E; ++k) {
       const int p = k * Gm::TB + t;
-      lds[lds_index(p)] = (active && p >= lo && p < hi) ? to_f32(grad[base + p - start]) : 0.0f;
+      lds[Gm::coal(t, k)] = (active && p >= lo && p < hi) ? to_f32(grad[base + p - start]) : 0.0f;
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < Gm::E; ++r) v[r] = lds[lds_index(p0 + r)];
+    for (int r = 0; r < Gm::E; ++r) v[r] = lds[Gm::own(t, r)];
   } else {
 #pragma unroll
     for (int r = 0; r < Gm::E; ++r) {
@@ -173,14 +184,14 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
   if constexpr (Gm::NG > 1) {
     __syncthreads();  // the transform's last LDS reads are done
 #pragma unroll
-    for (int r = 0; r < Gm::E; ++r) lds[lds_index(p0 + r)] = signed_by(v[r], w0, (p0 + r) & 31);
+    for (int r = 0; r < Gm::E; ++r) lds[Gm::own(t, r)] = signed_by(v[r], w0, (p0 + r) & 31);
     __syncthreads();
     if (!active) return;
 #pragma unroll
     for (int k = 0; k < Gm::E; ++k) {
       const int p = k * Gm::TB + t;
       if (p < n) {
-        const float g = lds[lds_index(p)];
+        const float g = lds[Gm::coal(t, k)];
         if (direct)
           grad_latent[p] = from_f32<T>(g);
         else
@@ -308,15 +319,55 @@ __device__ __forceinline__ void tile_fht_bits(float* lds, int tid, int lo_bit) {
   __syncthreads();
 }
 
-// One tile pass.  `high` selects the pass kind; `src` and `dst` the fused
-// prologue/epilogue (TileSrc / TileDst in bfht_launch.h).  Grid: one
-// workgroup per (block slot, tile), 2^(LB-15) tiles per block.
+// Element loads / stores through a raw buffer resource: element index i of the
+// buffer, out-of-range (including negative) indices read 0 / are dropped.  The
+// whole offset goes in the per-lane offset: the range check covers only that
+// part (a scalar offset is added after it).  Buffers stay below 2 GiB.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(bytes < 0x80000000ull ? bytes : 0x80000000ull), 0x00020000);
+}
 template <class T>
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, i * 4, 0, 0));
+  } else {
+    const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, i * 2, 0, 0);
+    return to_f32(__builtin_bit_cast(T, h));
+  }
+}
+template <class T>
+__device__ __forceinline__ void buf_store(float v, __amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, i * 4, 0, 1 | 16);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), r, i * 2, 0, 1 | 16);
+  }
+}
+
+// One pass of the tiled schedule (run_tiles).  A tile is 2^15 positions of one
+// block held in LDS: a low tile is contiguous (block bits 0-14 vary), a high
+// tile is 2^(LB-15) rows of 2^(30-LB) contiguous columns, the rows walking
+// block bits 15..LB-1.  The pass loads the tile (latent, grad or the work
+// buffer), transforms its bit group (`pre`), applies the sign layer
+// `sign_layer`, transforms the same bit group again (`post`), scales, and
+// stores it (work buffer, output slice, or partial gradient row).  Each thread
+// hashes one of the tile's 1024 sign words into a shared table.  Grid: one
+// workgroup per (block slot, tile), 2^(LB-15) tiles per block.
+//
+// Element r * 1024 + tid of the tile sits at block position pt(tid) + pr(r)
+// (disjoint bit fields), so each thread keeps one 32-bit offset and adds a
+// wave-uniform one per register: the 32 loads are issued back to back without
+// per-element addresses, and range limits (latent length, slice ends) are
+// buffer bounds.  SRC / DST are compile-time.
+template <class T, int SRC, int DST>
 __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
-    const T* __restrict__ src_io, float* __restrict__ work, T* __restrict__ dst_io, int LB,
-    int high, int src, int dst, int n, int64_t first_block, int64_t start, int64_t stop,
-    uint32_t seed32, int src_layer, int dst_layer) {
+    const T* __restrict__ src_io, float* __restrict__ work, T* __restrict__ dst_io, int LB, int high,
+    int pre, int post, int n, int64_t first_block, int64_t start, int64_t stop, uint32_t seed32,
+    int sign_layer, float scale) {
   __shared__ float lds[kTilePadded];
+  __shared__ uint32_t words[kTileElems / 32];
+  static_assert(kTileElems / 32 == kTileThreads, "one sign word per thread");
   const int tid = threadIdx.x;
   const int tiles_log = LB - kTileLog;
   const int64_t slot = (int64_t)blockIdx.x >> tiles_log;
@@ -324,52 +375,71 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
   const int64_t block = first_block + slot;
   const int64_t B = (int64_t)1 << LB;
   const int64_t base = block * B;  // global coordinate of the block's position 0
-  float* wblk = work + slot * B;
-  const uint32_t bkey = block_key(seed32, block);
-  const int col_log = kTileLog - tiles_log;  // high pass: columns per tile row
+  const int col_log = kTileLog - tiles_log;  // high tile: columns per row (>= 7 for LB <= 23)
+  const int lo_bit = high ? col_log : 0;     // the tile-index bits the pass transforms
 
-  // tile element e -> block position p
-  auto pos = [&](int e) -> uint32_t {
-    if (!high) return ((uint32_t)tile << kTileLog) | (uint32_t)e;
-    const uint32_t row = (uint32_t)e >> col_log, col = (uint32_t)e & ((1u << col_log) - 1);
+  // tile element e -> block position; elements 32q .. 32q+31 are positions
+  // pos(32q) .. pos(32q)+31 (columns are at least 32 wide)
+  auto pos = [&](uint32_t e) -> uint32_t {
+    if (!high) return ((uint32_t)tile << kTileLog) | e;
+    const uint32_t row = e >> col_log, col = e & ((1u << col_log) - 1);
     return (row << kTileLog) | ((uint32_t)tile << col_log) | col;
   };
+  words[tid] = sign_word(block_key(seed32, block), layer_key(sign_layer), pos(32u * tid) >> 5);
+  // pos(r * 1024 + tid) = pos(tid) + (pos(r * 1024) - pos(0)) for the disjoint fields
+  const int pt = (int)pos((uint32_t)tid);
+  const int p0 = (int)pos(0u);
+  auto pr = [&](int r) { return (int)pos((uint32_t)r * kTileThreads) - p0; };
 
-  const uint32_t skey = layer_key(src_layer);
-#pragma unroll 4
-  for (int r = 0; r < 32; ++r) {
-    const int e = r * kTileThreads + tid;
-    const uint32_t p = pos(e);
-    float x;
-    if (src == kSrcLatent) {
-      x = (int)p < n ? to_f32(src_io[p]) : 0.0f;
-    } else if (src == kSrcGrad) {
-      const int64_t g = base + p;
-      x = (g >= start && g < stop) ? to_f32(src_io[g - start]) : 0.0f;
-    } else {
-      x = wblk[p];
+  // padded LDS index of element r * 1024 + tid: lt + r * (1024 + 32)
+  const int lt = tid + (tid >> 5);
+  constexpr int kRowStride = kTileThreads + kTileThreads / 32;
+  // block-local range [lo, hi) of the slice (grad / out)
+  const int64_t lo = start - base > 0 ? start - base : 0;
+  const int64_t hi = stop - base < B ? stop - base : B;
+  float x[16];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = 16 * half + j;
+      if constexpr (SRC == kSrcLatent) {
+        x[j] = buf_load<T>(tile_rsrc(src_io, (uint64_t)n * sizeof(T)), pt + pr(r));
+      } else if constexpr (SRC == kSrcGrad) {
+        // buffer over grad[lo..hi) of this block, indexed by block position - lo
+        const T* g0 = src_io + (base + lo - start);
+        x[j] = buf_load<T>(tile_rsrc(g0, (uint64_t)(hi - lo) * sizeof(T)), pt + pr(r) - (int)lo);
+      } else {
+        x[j] = buf_load<float>(tile_rsrc(work + slot * B, (uint64_t)B * 4), pt + pr(r));
+      }
     }
-    if (src != kSrcWork) x = signed_at(x, bkey, skey, p);
-    lds[lds_index(e)] = x;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) lds[lt + (16 * half + j) * kRowStride] = x[j];
   }
-  tile_fht_bits(lds, tid, high ? kTileLog - tiles_log : 0);
+  if (pre)
+    tile_fht_bits(lds, tid, lo_bit);
+  else
+    __syncthreads();
+  // each thread flips only the elements it loaded, after the barrier that
+  // published the sign table
+#pragma unroll
+  for (int r = 0; r < 32; ++r)  // element r * 1024 + tid: word r * 32 + tid / 32, bit tid % 32
+    lds[lt + r * kRowStride] = signed_by(lds[lt + r * kRowStride], words[r * 32 + (tid >> 5)], tid & 31);
+  if (post)
+    tile_fht_bits(lds, tid, lo_bit);
+  else
+    __syncthreads();
 
-  const float scale = high ? ((LB & 1) ? 0.70710678118654752440f / (float)(1 << (LB >> 1))
-                                       : 1.0f / (float)(1 << (LB >> 1)))
-                           : 1.0f;
-  const uint32_t dkey = layer_key(dst_layer);
-#pragma unroll 4
+#pragma unroll
   for (int r = 0; r < 32; ++r) {
-    const int e = r * kTileThreads + tid;
-    const uint32_t p = pos(e);
-    float x = lds[lds_index(e)] * scale;
-    if (dst == kDstWork) {
-      wblk[p] = x;
-    } else if (dst == kDstOut) {
-      const int64_t g = base + p;
-      if (g >= start && g < stop) dst_io[g - start] = from_f32<T>(signed_at(x, bkey, dkey, p));
-    } else {  // kDstPartial: first n positions, signed by D_0, left in the work buffer
-      if ((int)p < n) wblk[p] = signed_at(x, bkey, dkey, p);
+    const float v = lds[lt + r * kRowStride] * scale;
+    if constexpr (DST == kDstWork) {
+      buf_store<float>(v, tile_rsrc(work + slot * B, (uint64_t)B * 4), pt + pr(r));
+    } else if constexpr (DST == kDstOut) {
+      T* o0 = dst_io + (base + lo - start);
+      buf_store<T>(v, tile_rsrc(o0, (uint64_t)(hi - lo) * sizeof(T)), pt + pr(r) - (int)lo);
+    } else {  // kDstPartial: the first n positions, left in the work buffer
+      buf_store<float>(v, tile_rsrc(work + slot * B, (uint64_t)n * 4), pt + pr(r));
     }
   }
 }
@@ -410,29 +480,38 @@ static hipError_t dispatch_block(int LB, bool fwd, const BfhtArgs& a, hipStream_
   return fwd ? fwd_table[LB](a, s) : bwd_table[LB](a, s);
 }
 
+// Blocks above 2^15: H = H_low (x) H_high over block bits 0-14 and 15..LB-1,
+// the two factors commute, so consecutive layers share a pass:
+//   [D_0, H_low] [H_high, D_1, H_high] [H_low, D_2, H_low] ... [H_g, D_L, out]
+// (L + 1 passes, each one read and one write of the float32 work buffer).
+// Pass k >= 1 completes layer k - 1 and applies its 2^(-LB/2).  The backward
+// runs the same schedule on grad with the sign layers in reverse (D_L first,
+// D_0 last) and leaves partial rows of n values for the block sum.
 template <class T>
 static hipError_t run_tiles(const BfhtArgs& a, hipStream_t s, bool fwd) {
   const unsigned grid = (unsigned)(a.nblocks << (a.log_block - kTileLog));
   const int L = a.layers;
-  for (int step = 0; step < L; ++step) {
-    // forward layer l = step: D_l at the low pass' load, D_L at the last store.
-    // backward layer l = L-1-step: D_{l+1} at the low pass' load, D_0 at the last store.
-    const int layer = fwd ? step : L - 1 - step;
-    const int low_src = step == 0 ? (fwd ? kSrcLatent : kSrcGrad) : kSrcWorkSigned;
-    const int low_src_layer = fwd ? layer : layer + 1;
-    hipLaunchKernelGGL((bfht_tile_pass<T>), dim3(grid), dim3(kTileThreads), 0, s,
-                       (const T*)a.src, (float*)a.work, (T*)nullptr, a.log_block, 0, low_src,
-                       kDstWork, (int)a.n, a.first_block, a.start, a.stop, a.seed32, low_src_layer,
-                       0);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const bool last = step == L - 1;
-    const int hdst = last ? (fwd ? kDstOut : kDstPartial) : kDstWork;
-    const int hdst_layer = fwd ? L : 0;
-    hipLaunchKernelGGL((bfht_tile_pass<T>), dim3(grid), dim3(kTileThreads), 0, s,
-                       (const T*)nullptr, (float*)a.work, (T*)a.dst, a.log_block, 1, kSrcWork, hdst,
-                       (int)a.n, a.first_block, a.start, a.stop, a.seed32, 0, hdst_layer);
-    e = hipGetLastError();
+  const int LB = a.log_block;
+  const float norm = (LB & 1) ? 0.70710678118654752440f / (float)(1 << (LB >> 1)) : 1.0f / (float)(1 << (LB >> 1));
+  for (int k = 0; k <= L; ++k) {
+    const int src = k == 0 ? (fwd ? kSrcLatent : kSrcGrad) : kSrcWork;
+    const int dst = k == L ? (fwd ? kDstOut : kDstPartial) : kDstWork;
+#define LWL_TILE(S, D)                                                                                          \
+  hipLaunchKernelGGL((bfht_tile_pass<T, S, D>), dim3(grid), dim3(kTileThreads), 0, s, (const T*)a.src,         \
+                     (float*)a.work, (T*)a.dst, LB, k & 1, (int)(k > 0), (int)(k < L), (int)a.n, a.first_block, \
+                     a.start, a.stop, a.seed32, fwd ? k : L - k, k > 0 ? norm : 1.0f)
+    if (src == kSrcLatent)
+      LWL_TILE(kSrcLatent, kDstWork);
+    else if (src == kSrcGrad)
+      LWL_TILE(kSrcGrad, kDstWork);
+    else if (dst == kDstWork)
+      LWL_TILE(kSrcWork, kDstWork);
+    else if (dst == kDstOut)
+      LWL_TILE(kSrcWork, kDstOut);
+    else
+      LWL_TILE(kSrcWork, kDstPartial);
+#undef LWL_TILE
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (fwd) return hipSuccess;

@@ -15,7 +15,7 @@ enum { kF32 = 0, kF16 = 1, kBF16 = 2 };
 constexpr int kWholeBlockMaxLog = 15;
 
 // tile-pass prologues / epilogues
-enum { kSrcLatent = 0, kSrcGrad = 1, kSrcWorkSigned = 2, kSrcWork = 3 };
+enum { kSrcLatent = 0, kSrcGrad = 1, kSrcWork = 2 };
 enum { kDstWork = 0, kDstOut = 1, kDstPartial = 2 };
 
 struct BfhtArgs {
