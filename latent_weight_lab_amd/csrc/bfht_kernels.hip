@@ -303,18 +303,25 @@ constexpr int kTileThreads = 1024;
 constexpr int kTileElems = 1 << kTileLog;
 constexpr int kTilePadded = kTileElems + (kTileElems >> 5);
 
-// In-place unnormalized butterflies over tile-index bits [lo_bit, 15) of an
-// LDS-resident 2^15 tile, in groups of up to 5 bits.
-__device__ __forceinline__ void tile_fht_bits(float* lds, int tid, int lo_bit) {
-  for (int lo = lo_bit; lo < kTileLog; lo += 5) {
+// In-place unnormalized butterflies over tile-index bits [LO_BIT, 15) of an
+// LDS-resident 2^15 tile, in groups of up to 5 bits.  The element thread t
+// holds in register r of a group is a bit field of t OR-ed with a bit field of
+// r; their low 5 bits never overlap, so its padded LDS index is
+// lds_index(field of t) + lds_index(field of r): a per-thread base plus a
+// compile-time offset per register.
+template <int LO_BIT>
+__device__ __forceinline__ void tile_fht_bits(float* lds, int tid) {
+#pragma unroll
+  for (int lo = LO_BIT; lo < kTileLog; lo += 5) {
     const int nb = kTileLog - lo < 5 ? kTileLog - lo : 5;
+    const int base = lds_index(group_pos<kTileLog, 5>(tid, 0, lo, nb));
     float v[32];
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < 32; ++r) v[r] = lds[lds_index(group_pos<kTileLog, 5>(tid, r, lo, nb))];
+    for (int r = 0; r < 32; ++r) v[r] = lds[base + lds_index(group_pos<kTileLog, 5>(0, r, lo, nb))];
     butterflies<32>(v, nb);
 #pragma unroll
-    for (int r = 0; r < 32; ++r) lds[lds_index(group_pos<kTileLog, 5>(tid, r, lo, nb))] = v[r];
+    for (int r = 0; r < 32; ++r) lds[base + lds_index(group_pos<kTileLog, 5>(0, r, lo, nb))] = v[r];
   }
   __syncthreads();
 }
@@ -360,23 +367,24 @@ __device__ __forceinline__ void buf_store(float v, __amdgpu_buffer_rsrc_t r, int
 // wave-uniform one per register: the 32 loads are issued back to back without
 // per-element addresses, and range limits (latent length, slice ends) are
 // buffer bounds.  SRC / DST are compile-time.
-template <class T, int SRC, int DST>
+template <class T, int SRC, int DST, int TL>
 __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
-    const T* __restrict__ src_io, float* __restrict__ work, T* __restrict__ dst_io, int LB, int high,
-    int pre, int post, int n, int64_t first_block, int64_t start, int64_t stop, uint32_t seed32,
-    int sign_layer, float scale) {
+    const T* __restrict__ src_io, float* __restrict__ work, T* __restrict__ dst_io, int LB, int pre, int post,
+    int n, int64_t first_block, int64_t start, int64_t stop, uint32_t seed32, int sign_layer, float scale) {
   __shared__ float lds[kTilePadded];
   __shared__ uint32_t words[kTileElems / 32];
   static_assert(kTileElems / 32 == kTileThreads, "one sign word per thread");
+  // TL = 0: low tile; TL = LB - 15 (the launcher checks): high tile of 2^TL rows
+  constexpr bool high = TL > 0;
   const int tid = threadIdx.x;
-  const int tiles_log = LB - kTileLog;
+  const int tiles_log = LB - kTileLog;  // log2 tiles per block
   const int64_t slot = (int64_t)blockIdx.x >> tiles_log;
   const int tile = (int)(blockIdx.x & ((1u << tiles_log) - 1));
   const int64_t block = first_block + slot;
   const int64_t B = (int64_t)1 << LB;
   const int64_t base = block * B;  // global coordinate of the block's position 0
-  const int col_log = kTileLog - tiles_log;  // high tile: columns per row (>= 7 for LB <= 23)
-  const int lo_bit = high ? col_log : 0;     // the tile-index bits the pass transforms
+  constexpr int col_log = kTileLog - TL;  // high tile: columns per row (>= 7 for LB <= 23)
+  constexpr int lo_bit = high ? col_log : 0;  // the tile-index bits the pass transforms
 
   // tile element e -> block position; elements 32q .. 32q+31 are positions
   // pos(32q) .. pos(32q)+31 (columns are at least 32 wide)
@@ -417,7 +425,7 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
     for (int j = 0; j < 16; ++j) lds[lt + (16 * half + j) * kRowStride] = x[j];
   }
   if (pre)
-    tile_fht_bits(lds, tid, lo_bit);
+    tile_fht_bits<lo_bit>(lds, tid);
   else
     __syncthreads();
   // each thread flips only the elements it loaded, after the barrier that
@@ -426,7 +434,7 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
   for (int r = 0; r < 32; ++r)  // element r * 1024 + tid: word r * 32 + tid / 32, bit tid % 32
     lds[lt + r * kRowStride] = signed_by(lds[lt + r * kRowStride], words[r * 32 + (tid >> 5)], tid & 31);
   if (post)
-    tile_fht_bits(lds, tid, lo_bit);
+    tile_fht_bits<lo_bit>(lds, tid);
   else
     __syncthreads();
 
@@ -480,6 +488,44 @@ static hipError_t dispatch_block(int LB, bool fwd, const BfhtArgs& a, hipStream_
   return fwd ? fwd_table[LB](a, s) : bwd_table[LB](a, s);
 }
 
+// One tile pass: picks the instantiation for (source, destination, tile kind).
+// Passes that neither read nor write the I/O type run the float instantiation.
+template <class T, int SRC, int DST>
+static hipError_t launch_tile_kind(const BfhtArgs& a, hipStream_t s, int tl, int pre, int post, int layer,
+                                   float scale, unsigned grid) {
+  constexpr bool typed = SRC != kSrcWork || DST == kDstOut;
+  using U = std::conditional_t<typed, T, float>;
+#define LWL_TILE(TL)                                                                                      \
+  hipLaunchKernelGGL((bfht_tile_pass<U, SRC, DST, TL>), dim3(grid), dim3(kTileThreads), 0, s,            \
+                     (const U*)a.src, (float*)a.work, (U*)a.dst, a.log_block, pre, post, (int)a.n,         \
+                     a.first_block, a.start, a.stop, a.seed32, layer, scale)
+  switch (tl) {
+    case 0: LWL_TILE(0); break;
+    case 1: if constexpr (SRC == kSrcWork) LWL_TILE(1); break;
+    case 2: if constexpr (SRC == kSrcWork) LWL_TILE(2); break;
+    case 3: if constexpr (SRC == kSrcWork) LWL_TILE(3); break;
+    case 4: if constexpr (SRC == kSrcWork) LWL_TILE(4); break;
+    case 5: if constexpr (SRC == kSrcWork) LWL_TILE(5); break;
+    case 6: if constexpr (SRC == kSrcWork) LWL_TILE(6); break;
+    case 7: if constexpr (SRC == kSrcWork) LWL_TILE(7); break;
+    case 8: if constexpr (SRC == kSrcWork) LWL_TILE(8); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef LWL_TILE
+  return hipGetLastError();
+}
+
+template <class T>
+static hipError_t launch_tile_pass(const BfhtArgs& a, hipStream_t s, int src, int dst, int tl, int pre, int post,
+                                   int layer, float scale, unsigned grid) {
+  // the first pass (the only one reading latent / grad) runs low tiles
+  if (src == kSrcLatent) return launch_tile_kind<T, kSrcLatent, kDstWork>(a, s, 0, pre, post, layer, scale, grid);
+  if (src == kSrcGrad) return launch_tile_kind<T, kSrcGrad, kDstWork>(a, s, 0, pre, post, layer, scale, grid);
+  if (dst == kDstWork) return launch_tile_kind<T, kSrcWork, kDstWork>(a, s, tl, pre, post, layer, scale, grid);
+  if (dst == kDstOut) return launch_tile_kind<T, kSrcWork, kDstOut>(a, s, tl, pre, post, layer, scale, grid);
+  return launch_tile_kind<T, kSrcWork, kDstPartial>(a, s, tl, pre, post, layer, scale, grid);
+}
+
 // Blocks above 2^15: H = H_low (x) H_high over block bits 0-14 and 15..LB-1,
 // the two factors commute, so consecutive layers share a pass:
 //   [D_0, H_low] [H_high, D_1, H_high] [H_low, D_2, H_low] ... [H_g, D_L, out]
@@ -496,22 +542,9 @@ static hipError_t run_tiles(const BfhtArgs& a, hipStream_t s, bool fwd) {
   for (int k = 0; k <= L; ++k) {
     const int src = k == 0 ? (fwd ? kSrcLatent : kSrcGrad) : kSrcWork;
     const int dst = k == L ? (fwd ? kDstOut : kDstPartial) : kDstWork;
-#define LWL_TILE(S, D)                                                                                          \
-  hipLaunchKernelGGL((bfht_tile_pass<T, S, D>), dim3(grid), dim3(kTileThreads), 0, s, (const T*)a.src,         \
-                     (float*)a.work, (T*)a.dst, LB, k & 1, (int)(k > 0), (int)(k < L), (int)a.n, a.first_block, \
-                     a.start, a.stop, a.seed32, fwd ? k : L - k, k > 0 ? norm : 1.0f)
-    if (src == kSrcLatent)
-      LWL_TILE(kSrcLatent, kDstWork);
-    else if (src == kSrcGrad)
-      LWL_TILE(kSrcGrad, kDstWork);
-    else if (dst == kDstWork)
-      LWL_TILE(kSrcWork, kDstWork);
-    else if (dst == kDstOut)
-      LWL_TILE(kSrcWork, kDstOut);
-    else
-      LWL_TILE(kSrcWork, kDstPartial);
-#undef LWL_TILE
-    const hipError_t e = hipGetLastError();
+    const int tl = (k & 1) ? LB - kTileLog : 0;  // odd passes run high tiles
+    const hipError_t e = launch_tile_pass<T>(a, s, src, dst, tl, (int)(k > 0), (int)(k < L), fwd ? k : L - k,
+                                             k > 0 ? norm : 1.0f, grid);
     if (e != hipSuccess) return e;
   }
   if (fwd) return hipSuccess;

@@ -208,18 +208,26 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
       for (int g = 0; g < kGroup; ++g) ring[d][g] = xload(g, d);
       __builtin_amdgcn_sched_barrier(0);
     }
+    // W tiles of step s are read one step ahead (bt holds step s, bn step s + 1),
+    // so no MFMA waits on a just-issued LDS read; the last step re-reads itself.
     const u32x4* bs = brow;
+    u32x4 bt[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) bt[nt] = bs[16 * nt];
     for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
 #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
-        u32x4 bt[NT];
+        const u32x4* bsn = (s0 + d + 1 < nsteps) ? bs + 4 * kRows : bs;
+        u32x4 bn[NT];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) bt[nt] = bs[16 * nt];
-        bs += 4 * kRows;
+        for (int nt = 0; nt < NT; ++nt) bn[nt] = bsn[16 * nt];
+        bs = bsn;
 #pragma unroll
         for (int g = 0; g < kGroup; ++g)
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) acc[g][nt] = mfma16(ring[d][g], bt[nt], acc[g][nt]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) bt[nt] = bn[nt];
         // Refill slot d only after its last use, so the load writes the
         // slot's own registers: a load issued earlier would need a second
         // register set and a copy (with a wait on the fresh load) at the
