@@ -95,6 +95,19 @@ __device__ __forceinline__ void butterflies(float (&v)[E], int nb) {
   }
 }
 
+// Padded LDS index of group_pos(t, r, lo, nb): the position is a bit field of
+// t OR-ed with a disjoint bit field of r, and lds_index of such a sum splits
+// (their low 5 bits cannot carry), so it is a per-thread base plus a term that
+// is a compile-time constant once lo, nb and r are.
+template <int LB, int LE>
+__device__ __forceinline__ int group_lds(int base, int r, int lo, int nb) {
+  return base + lds_index(group_pos<LB, LE>(0, r, lo, nb));
+}
+template <int LB, int LE>
+__device__ __forceinline__ int group_base(int t, int lo, int nb) {
+  return lds_index(group_pos<LB, LE>(t, 0, lo, nb));
+}
+
 // Full unnormalized Walsh-Hadamard transform of an LB-bit block held as
 // v[E] per thread in the contiguous layout (thread t holds positions t*E + r),
 // using `lds` (lds_index-padded, one block) for the group exchanges.  Leaves v
@@ -109,23 +122,27 @@ __device__ __forceinline__ void fht_unnormalized(float (&v)[1 << LE], float* lds
 #pragma unroll
     for (int g = 1; g < NG; ++g) {
       const int plo = (g - 1) * 5;  // every group but the last has 5 bits
+      const int wb = group_base<LB, LE>(t, plo, 5);
       __syncthreads();
 #pragma unroll
-      for (int r = 0; r < E; ++r) lds[lds_index(group_pos<LB, LE>(t, r, plo, 5))] = v[r];
+      for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, plo, 5)] = v[r];
       __syncthreads();
       const int lo = g * 5, nb = (g == NG - 1) ? LB - lo : 5;
+      const int rb = group_base<LB, LE>(t, lo, nb);
 #pragma unroll
-      for (int r = 0; r < E; ++r) v[r] = lds[lds_index(group_pos<LB, LE>(t, r, lo, nb))];
+      for (int r = 0; r < E; ++r) v[r] = lds[group_lds<LB, LE>(rb, r, lo, nb)];
       butterflies<E>(v, nb);
     }
     {
       const int lo = (NG - 1) * 5, nb = LB - lo;
+      const int wb = group_base<LB, LE>(t, lo, nb);
       __syncthreads();
 #pragma unroll
-      for (int r = 0; r < E; ++r) lds[lds_index(group_pos<LB, LE>(t, r, lo, nb))] = v[r];
+      for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, lo, nb)] = v[r];
       __syncthreads();
+      const int cb = lds_index(t * E);  // contiguous layout: t * E + r, r < E <= 32
 #pragma unroll
-      for (int r = 0; r < E; ++r) v[r] = lds[lds_index(t * E + r)];
+      for (int r = 0; r < E; ++r) v[r] = lds[cb + r];
     }
   }
 }
