@@ -177,8 +177,15 @@ def config2_latent(torch, dtype):
     return torch.randn(32768, dtype=torch.float32).to(dtype)
 
 
+def config1_latent(torch):
+    torch.manual_seed(0)
+    return torch.randn(1024, dtype=torch.float32)
+
+
 # ---------------------------------------------------------------- headline
 
+C1_N = 1024
+C1_SIZE = 108_618
 C2_N = 32768
 C2_SIZE = 8_388_608
 C2_LAYERS = 3
@@ -218,6 +225,19 @@ def extra_configs(abi, steps, warmup, only):
                          "algo_GBs": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
         except Exception as exc:  # noqa: BLE001 - reported, not fatal
             res[name] = {"error": f"{type(exc).__name__}: {exc}"}
+
+    # config 1 (the reference's CPU-runnable case): n = 1024, size 108,618, layers 3, seed 123, fp32
+    lat1 = config1_latent(torch).cuda()
+    out1 = torch.empty(C1_SIZE, dtype=torch.float32, device="cuda")
+    sl1 = torch.empty(1000, dtype=torch.float32, device="cuda")
+    g1 = torch.randn(C1_SIZE, generator=torch.Generator().manual_seed(4)).cuda()
+    gl1 = torch.empty(C1_N, dtype=torch.float32, device="cuda")
+    bws1 = abi.bwd_ws(C1_N, C1_SIZE, 0, C1_SIZE, "cuda")
+    run("c1_fwd_f32", lambda: abi.forward(lat1, out1, C1_SIZE, 3, 123, 0, C1_SIZE), C1_SIZE * 4 + C1_N * 4, C1_SIZE)
+    run("c1_slice_f32", lambda: abi.forward(lat1, sl1, C1_SIZE, 3, 123, 1000, 2000), 1000 * 4 + C1_N * 4, 1000)
+    run("c1_bwd_f32", lambda: abi.backward(g1, gl1, C1_SIZE, 3, 123, 0, C1_SIZE, bws1), C1_SIZE * 4 + C1_N * 4,
+        C1_SIZE)
+    del lat1, out1, sl1, g1, gl1, bws1
 
     for dt, es in ((torch.bfloat16, 2), (torch.float32, 4)):
         tag = "bf16" if dt == torch.bfloat16 else "f32"
@@ -348,7 +368,6 @@ def stack_bench(abi, torch):
             row["error"] = f"{type(exc).__name__}: {exc}"
         out[f"tokens_{tokens}"] = row
     return out
-    return res
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -389,6 +408,61 @@ def cpu_baseline(gpu_out, budget_s: float = 12.0):
                    f"host {cpu_model()}, os.cpu_count()={os.cpu_count()}"),
         "gpu_vs_cpu_rel_l2": err,
     }
+
+
+def _median_time(fn, budget_s: float, max_runs: int = 9):
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 1 or (time.perf_counter() < t_end and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_extra(budget_s: float = 4.0):
+    """The reference's CPU fallback on the other configurations, each timed on a bounded sample
+    (median of a few runs): config 1 in full (forward, slice, backward of sum y^2 through autograd
+    of the same torch ops), one 2^20 block of config 3, and config 4's fallback (materialize W
+    through block_fht_slice_torch, then fp32 F.linear) on 256 tokens."""
+    import torch
+
+    from oracle import oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    res = {}
+    lat = config1_latent(torch)
+    sec, n = _median_time(lambda: O.torch_port_slice(lat, C1_SIZE, 3, 123, 0, C1_SIZE), budget_s)
+    res["c1_fwd_f32"] = {"coords_per_s": C1_SIZE / sec, "ms": sec * 1e3, "runs": n}
+    sec, n = _median_time(lambda: O.torch_port_slice(lat, C1_SIZE, 3, 123, 1000, 2000), budget_s)
+    res["c1_slice_f32"] = {"coords_per_s": 1000 / sec, "ms": sec * 1e3, "runs": n}
+
+    def c1_bwd():
+        x = lat.clone().requires_grad_(True)
+        O.torch_port_slice(x, C1_SIZE, 3, 123, 0, C1_SIZE).square().sum().backward()
+
+    sec, n = _median_time(c1_bwd, budget_s)
+    res["c1_fwd_bwd_f32"] = {"coords_per_s": C1_SIZE / sec, "ms": sec * 1e3, "runs": n,
+                             "note": "forward + autograd backward of sum(y^2)"}
+    torch.manual_seed(2)
+    lat3 = torch.randn(1 << 20, dtype=torch.float32)
+    sec, n = _median_time(lambda: O.torch_port_slice(lat3, 1 << 20, 3, 99, 0, 1 << 20), budget_s, 3)
+    res["c3_b2^20_fwd_one_block"] = {"coords_per_s": (1 << 20) / sec, "ms": sec * 1e3, "runs": n,
+                                     "note": "1 of the 64 blocks of config 3 (2^26 coords)"}
+    torch.manual_seed(3)
+    lat4 = torch.randn(32768, dtype=torch.float32)
+    x4 = torch.randn(256, 768, dtype=torch.float32)
+
+    def c4():
+        w = O.torch_port_slice(lat4, 768 * 3072, 3, 3, 0, 768 * 3072).view(3072, 768)
+        return torch.nn.functional.linear(x4, w)
+
+    sec, n = _median_time(c4, budget_s, 5)
+    res["c4_768x3072_fallback_256tok"] = {"tokens_per_s": 256 / sec, "ms": sec * 1e3, "runs": n,
+                                          "note": "materialize W (72 blocks) + fp32 F.linear, 256 tokens"}
+    res["cores"] = torch.get_num_threads()
+    return res
 
 
 # ---------------------------------------------------------------- main
@@ -453,6 +527,8 @@ def main():
             line["fused_linear_tokens_per_s"] = {k: v.get("fused_tokens_per_s") for k, v in lin.items()}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(gpu_out)
+        if not args.no_extra:
+            line["cpu_extra"] = cpu_extra()
     print(json.dumps(line), flush=True)
 
 
