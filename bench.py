@@ -105,6 +105,19 @@ class Abi:
         nbytes = self.lib.lwl_bfht_backward_workspace_size(n, size, start, stop)
         return self.torch.empty(nbytes, dtype=self.torch.uint8, device=device) if nbytes else None
 
+    def linear_bwd_latent(self, grad, x, latent, grad_latent, out_f, layers, seed, scale, ws):
+        N = self.N
+        tokens, in_f = x.shape
+        rc = self.lib.lwl_bfht_linear_backward_latent(grad.data_ptr(), x.data_ptr(), N.dtype_code(x.dtype), tokens,
+                                                      in_f, latent.numel(), out_f, layers, seed, float(scale),
+                                                      grad_latent.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                      self.stream())
+        N.check(rc)
+
+    def linear_bwd_ws(self, tokens, in_f, out_f, n, device):
+        nbytes = self.lib.lwl_bfht_linear_backward_latent_workspace_size(tokens, in_f, out_f, n)
+        return self.torch.empty(nbytes, dtype=self.torch.uint8, device=device)
+
 
 def time_graph(torch, fn, steps: int, warmup: int) -> float:
     """Seconds per step: `steps` calls of fn captured in one HIP graph,
@@ -305,6 +318,39 @@ def extra_configs(abi, steps, warmup, only):
             except Exception as exc:  # noqa: BLE001
                 lin[f"{inf}x{outf}"] = {"error": f"{type(exc).__name__}: {exc}"}
         res["c4_linear"] = lin
+
+    # config 4 training step, latent gradient: fused (grad_weight formed per block on chip) vs
+    # grad_weight = g^T x on hipBLASLt in HBM followed by the generator backward
+    if want("c4_linear_bwd"):
+        lin = {}
+        for inf, outf in ((768, 3072), (3072, 768)):
+            try:
+                torch.manual_seed(3)
+                latent = torch.randn(32768, dtype=torch.float32).to(torch.bfloat16).cuda()
+                x = torch.randn(4096, inf, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).cuda()
+                g = torch.randn(4096, outf, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).cuda()
+                gl = torch.empty(32768, dtype=torch.bfloat16, device="cuda")
+                gl2 = torch.empty(32768, dtype=torch.bfloat16, device="cuda")
+                ws = abi.linear_bwd_ws(4096, inf, outf, 32768, "cuda")
+                size = inf * outf
+                bws = abi.bwd_ws(32768, size, 0, size, "cuda")
+                gw = torch.empty(outf, inf, dtype=torch.bfloat16, device="cuda")
+
+                def unfused():
+                    torch.matmul(g.t(), x, out=gw)
+                    abi.backward(gw.view(-1), gl2, size, 3, 3, 0, size, bws)
+
+                fused = time_graph(torch, lambda: abi.linear_bwd_latent(g, x, latent, gl, outf, 3, 3, 1.0, ws),
+                                   20, 3)
+                base = time_graph(torch, unfused, 20, 3)
+                lin[f"{inf}x{outf}"] = {"fused_ms": round(fused * 1e3, 4), "unfused_ms": round(base * 1e3, 4),
+                                        "fused_over_unfused": fused / base,
+                                        "rel_l2_vs_unfused": float((gl.float() - gl2.float()).norm()
+                                                                   / gl2.float().norm())}
+                del latent, x, g, gl, gl2, ws, bws, gw
+            except Exception as exc:  # noqa: BLE001
+                lin[f"{inf}x{outf}"] = {"error": f"{type(exc).__name__}: {exc}"}
+        res["c4_linear_bwd"] = lin
 
     # config 5: 12-layer GPT-2-small linear stack (qkv, proj, fc, fc-proj per layer = 48 matrices,
     # latents of 32768 bf16, seeds 100+i), forward only, fused vs dense on materialized weights

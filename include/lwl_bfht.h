@@ -106,9 +106,11 @@ int lwl_bfht_backward(const void* grad_out, int dtype, int64_t latent_size, int6
  * <= B works (rows may straddle blocks; partial rows are summed in a fixed
  * order through the workspace).  B <= 2^15.
  *
- * dtype BF16/F16: the generated weight is rounded to the I/O type and the
- * contraction runs on MFMA with float32 accumulation.  dtype F32: float32
- * MFMA, float32 accumulation.
+ * Takes bfloat16 latents of block 2^15 with in_features % 8 == 0 and
+ * 528 <= in_features <= 5120: the generated weight is rounded to bf16 and the
+ * contraction runs on MFMA with float32 accumulation.  Other shapes return
+ * LWL_ERR_UNSUPPORTED and the caller generates the weight and calls a GEMM,
+ * as the reference's fallback does (block_fht.py:263-288).
  */
 size_t lwl_bfht_linear_forward_workspace_size(int64_t tokens, int64_t in_features,
                                               int64_t out_features, int64_t latent_size);
@@ -120,6 +122,35 @@ int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, in
 /* Host-only argument check of lwl_bfht_linear_forward (no GPU needed). */
 int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features,
                                   int64_t latent_size, int64_t out_features, int64_t layers);
+
+/* ---------------------------------------------------------------- fused latent gradient
+ * Replaces the grad_latent branch of _BlockFHTLinearFn.backward (reference
+ * latent_weight_lab/block_fht.py:339-352: grad_weight = grad^T @ input formed
+ * in HBM, then block_fht_grad_latent; the reference's native extension has no
+ * counterpart).
+ *
+ * grad_latent[p] = weight_scale * sum_b (D_0 H D_1 ... H D_L gw_b)[p], p < n,
+ * with gw_b = (grad_out^T @ input) flattened, positions b*B .. b*B + B - 1:
+ * the same value as lwl_bfht_backward applied to weight_scale * grad_weight,
+ * but grad_weight is formed block by block on chip and never written.
+ * grad_out [tokens, out_features], input [tokens, in_features], grad_latent [n],
+ * all bfloat16 (latent length 16385..32768: block 2^15), in_features % 16 == 0,
+ * in_features >= 528.  Each block's tile of grad_weight is rounded to bf16
+ * before the transform (the reference casts grad_weight to the latent dtype);
+ * the per-(block, token range) rows are summed in a fixed order.
+ * The modulation term of the reference (block_fht.py:351-352) is left to the
+ * caller.  Workspace: query *_workspace_size with the same shape.
+ */
+size_t lwl_bfht_linear_backward_latent_workspace_size(int64_t tokens, int64_t in_features,
+                                                      int64_t out_features, int64_t latent_size);
+int lwl_bfht_linear_backward_latent(const void* grad_out, const void* input, int dtype, int64_t tokens,
+                                    int64_t in_features, int64_t latent_size, int64_t out_features,
+                                    int64_t layers, int64_t seed, double weight_scale, void* grad_latent,
+                                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Host-only argument check of lwl_bfht_linear_backward_latent (no GPU needed). */
+int lwl_bfht_check_linear_backward_latent(int dtype, int64_t tokens, int64_t in_features,
+                                          int64_t latent_size, int64_t out_features, int64_t layers);
 
 /* ---------------------------------------------------------------- sign words
  * Parity probe for the device hash (reference device functions

@@ -60,6 +60,9 @@ def _bind(lib) -> None:
         "lwl_bfht_linear_forward_workspace_size": (sz, [i64, i64, i64, i64]),
         "lwl_bfht_linear_forward": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, dbl, vp, vp, sz, vp]),
         "lwl_bfht_check_linear_forward": (i32, [i32, i64, i64, i64, i64, i64]),
+        "lwl_bfht_linear_backward_latent_workspace_size": (sz, [i64, i64, i64, i64]),
+        "lwl_bfht_linear_backward_latent": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, dbl, vp, vp, sz, vp]),
+        "lwl_bfht_check_linear_backward_latent": (i32, [i32, i64, i64, i64, i64, i64]),
         "lwl_bfht_sign_words": (i32, [i64, i64, i64, i64, i64, u32p, vp]),
     }
     for name, (res, args) in sigs.items():

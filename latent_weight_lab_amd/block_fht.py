@@ -113,17 +113,20 @@ def block_fht_linear_forward(input: torch.Tensor, latent: torch.Tensor, out_feat
 class _BlockFHTLinearFn(torch.autograd.Function):
     """Training linear (reference ``block_fht.py:291-356``): W is generated for
     the forward and again for grad_input; grad_latent goes through the HIP
-    backward of the generator."""
+    backward of the generator, with grad_weight = g^T x either on a library GEMM
+    in HBM (the faster route on MI355X, and the reference's) or, with
+    ``fused_latent_grad``, formed block by block on chip and never stored."""
 
     @staticmethod
     def forward(ctx, input, latent, bias, in_features, out_features, size, layers, seed, weight_scale,
-                modulation_alpha):
+                modulation_alpha, fused_latent_grad=False):
         weight = _generated_weight(latent, size, layers, seed, weight_scale, modulation_alpha)
         weight = weight.view(int(out_features), int(in_features)).to(dtype=input.dtype)
         ctx.save_for_backward(input, latent)
         ctx.has_bias = bias is not None
         ctx.meta = (int(in_features), int(out_features), int(size), int(layers), int(seed), float(weight_scale),
                     float(modulation_alpha))
+        ctx.fused_latent_grad = bool(fused_latent_grad)
         return F.linear(input, weight, bias)
 
     @staticmethod
@@ -138,13 +141,24 @@ class _BlockFHTLinearFn(torch.autograd.Function):
                 weight = weight.view(out_f, in_f).to(dtype=grad_output.dtype)
             grad_input = grad_2d.matmul(weight).reshape_as(input)
         if ctx.needs_input_grad[1]:
-            grad_weight = grad_2d.t().to(dtype=latent.dtype).matmul(input.reshape(-1, in_f).to(dtype=latent.dtype))
-            grad_latent = scale * block_fht_grad_latent(latent, grad_weight.reshape(-1), size, layers, seed)
-            if alpha != 0.0:
-                grad_latent = grad_latent + 2.0 * alpha * latent * grad_weight.sum()
+            input_2d = input.reshape(-1, in_f)
+            g = grad_2d.to(dtype=latent.dtype)
+            xl = input_2d.to(dtype=latent.dtype)
+            if (ctx.fused_latent_grad and size == in_f * out_f
+                    and ops.linear_backward_latent_supported(in_f, out_f, latent, xl, g)):
+                # grad_weight = g^T x formed block by block on chip, never in HBM
+                grad_latent = ops.linear_backward_latent(g, xl, latent, out_f, layers, seed, scale)
+                if alpha != 0.0:  # sum of grad_weight = sum_t (sum_o g[t, o]) (sum_i x[t, i])
+                    gw_sum = (g.float().sum(dim=1) * xl.float().sum(dim=1)).sum()
+                    grad_latent = grad_latent + (2.0 * alpha * gw_sum * latent.float()).to(latent.dtype)
+            else:
+                grad_weight = g.t().matmul(xl)
+                grad_latent = scale * block_fht_grad_latent(latent, grad_weight.reshape(-1), size, layers, seed)
+                if alpha != 0.0:
+                    grad_latent = grad_latent + 2.0 * alpha * latent * grad_weight.sum()
         if ctx.has_bias and ctx.needs_input_grad[2]:
             grad_bias = grad_2d.sum(dim=0).to(dtype=grad_output.dtype)
-        return grad_input, grad_latent, grad_bias, None, None, None, None, None, None, None
+        return grad_input, grad_latent, grad_bias, None, None, None, None, None, None, None, None
 
 
 def _generated_weight(latent, size, layers, seed, weight_scale, modulation_alpha):
@@ -179,7 +193,7 @@ class BlockFHTLinear(nn.Module):
                  weight_scale: float = 1.0, modulation_alpha: float = 0.0, modulation_centered: bool = False,
                  residual_base_scale: float = 0.0, residual_base_std: float = 0.02, output_gain: bool = False,
                  input_gain: bool = False, spectral_rank: int = 0, spectral_out_groups: int = 1,
-                 spectral_in_groups: int = 1) -> None:
+                 spectral_in_groups: int = 1, fused_latent_grad: bool = False) -> None:
         super().__init__()
         self.in_features = int(in_features)
         self.out_features = int(out_features)
@@ -193,6 +207,9 @@ class BlockFHTLinear(nn.Module):
         self.weight_scale = float(weight_scale)
         self.modulation_alpha = float(modulation_alpha)
         self.modulation_centered = bool(modulation_centered)
+        # not in the reference: form grad_weight per block on chip in the backward
+        # (lwl_bfht_linear_backward_latent) instead of on a GEMM in HBM
+        self.fused_latent_grad = bool(fused_latent_grad)
         self.latent_init_std = float(latent_init_std)
         self.residual_base_scale = float(residual_base_scale)
         self.output_gain = nn.Parameter(torch.ones(self.out_features)) if output_gain else None
@@ -265,7 +282,8 @@ class BlockFHTLinear(nn.Module):
             return F.linear(input, self.weight.to(dtype=input.dtype), self.bias)
         g = self.generator
         return _BlockFHTLinearFn.apply(input, g.latent, self.bias, self.in_features, self.out_features, g.size,
-                                       g.layers, g.seed, self.weight_scale, self.modulation_alpha)
+                                       g.layers, g.seed, self.weight_scale, self.modulation_alpha,
+                                       self.fused_latent_grad)
 
     def forward_fused(self, input: torch.Tensor, weight_scale: float = 1.0) -> torch.Tensor:
         """Inference forward without materializing W (reference ``block_fht.py:482-501``)."""

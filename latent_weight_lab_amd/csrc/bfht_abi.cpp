@@ -158,6 +158,48 @@ lwl::LinearArgs plan_linear(int dtype, int64_t tokens, int64_t in_features, int6
 
 size_t linear_ws(const lwl::LinearArgs& a) { return align_up(lwl::linear_workspace_bytes(a)); }
 
+// Fused latent-gradient checks (no reference counterpart: the reference forms
+// grad_weight in HBM, block_fht.py:339-352).
+int check_linear_bwd(int dtype, int64_t tokens, int64_t in_features, int64_t latent_size, int64_t out_features,
+                     int64_t layers) {
+  if (!valid_dtype(dtype))
+    return fail(LWL_ERR_UNSUPPORTED, "linear latent gradient supports float32, float16, and bfloat16 (dtype code %d)",
+                dtype);
+  if (tokens < 0) return fail(LWL_ERR_INVALID, "tokens must be non-negative");
+  if (in_features <= 0) return fail(LWL_ERR_INVALID, "in_features must be positive");
+  if (out_features <= 0) return fail(LWL_ERR_INVALID, "out_features must be positive");
+  if (layers < 1 || layers > 3) return fail(LWL_ERR_INVALID, "layers must be 1, 2, or 3");
+  if (latent_size <= 0) return fail(LWL_ERR_INVALID, "latent size must be positive");
+  const int lb = log2_pow2_ceil(latent_size);
+  if (lb > lwl::kWholeBlockMaxLog || !lwl::linear_bwd_applicable(dtype, lb, in_features))
+    return fail(LWL_ERR_UNSUPPORTED,
+                "fused linear latent gradient takes bfloat16 latents of length 16385..32768 (block 2^15) with "
+                "in_features %% 16 == 0 and 528 <= in_features (dtype code %d, latent size %lld, in_features %lld)",
+                dtype, (long long)latent_size, (long long)in_features);
+  const int64_t tpad = (tokens + 31) / 32 * 32;
+  if (tpad * in_features * 2 >= ((int64_t)1 << 31) || tpad * out_features * 2 >= ((int64_t)1 << 31))
+    return fail(LWL_ERR_UNSUPPORTED,
+                "fused linear latent gradient: tokens * in_features and tokens * out_features must stay below 2^30");
+  return LWL_OK;
+}
+
+lwl::LinearBwdArgs plan_linear_bwd(int64_t tokens, int64_t in_features, int64_t latent_size, int64_t out_features,
+                                   int64_t layers, int64_t seed, double weight_scale) {
+  lwl::LinearBwdArgs a{};
+  a.tokens = tokens;
+  a.in_features = in_features;
+  a.out_features = out_features;
+  a.n = latent_size;
+  a.log_block = log2_pow2_ceil(latent_size);
+  const int64_t B = (int64_t)1 << a.log_block;
+  a.nblocks_w = (in_features * out_features + B - 1) / B;
+  a.seed32 = fold_seed(seed);
+  a.layers = (int)layers;
+  a.weight_scale = (float)weight_scale;
+  a.token_splits = lwl::linear_bwd_token_splits(a);
+  return a;
+}
+
 int check_workspace(size_t need, const void* ws, size_t have) {
   if (need == 0) return LWL_OK;
   if (ws == nullptr || have < need)
@@ -257,6 +299,44 @@ int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, in
   a.out = out;
   a.work = workspace;
   return hip_status(lwl::launch_linear(a, (hipStream_t)stream), "lwl_bfht_linear_forward");
+}
+
+int lwl_bfht_check_linear_backward_latent(int dtype, int64_t tokens, int64_t in_features,
+                                          int64_t latent_size, int64_t out_features, int64_t layers) {
+  const int rc = check_linear_bwd(dtype, tokens, in_features, latent_size, out_features, layers);
+  return rc ? rc : ok();
+}
+
+size_t lwl_bfht_linear_backward_latent_workspace_size(int64_t tokens, int64_t in_features,
+                                                      int64_t out_features, int64_t latent_size) {
+  if (check_linear_bwd(LWL_DTYPE_BF16, tokens, in_features, latent_size, out_features, 1)) return 0;
+  if (tokens == 0) return 0;
+  return align_up(lwl::linear_bwd_workspace_bytes(
+      plan_linear_bwd(tokens, in_features, latent_size, out_features, 1, 0, 1.0)));
+}
+
+int lwl_bfht_linear_backward_latent(const void* grad_out, const void* input, int dtype, int64_t tokens,
+                                    int64_t in_features, int64_t latent_size, int64_t out_features,
+                                    int64_t layers, int64_t seed, double weight_scale, void* grad_latent,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_linear_bwd(dtype, tokens, in_features, latent_size, out_features, layers);
+  if (rc) return rc;
+  if (!grad_latent) return fail(LWL_ERR_INVALID, "grad_latent must be non-null");
+  if (tokens > 0 && (!grad_out || !input)) return fail(LWL_ERR_INVALID, "grad_out and input must be non-null");
+  lwl::LinearBwdArgs a = plan_linear_bwd(tokens, in_features, latent_size, out_features, layers, seed, weight_scale);
+  if (tokens == 0) {
+    // no tokens: the gradient is zero (a block sum over zero partial rows)
+    return hip_status(lwl::launch_block_sum(nullptr, 0, latent_size, latent_size, grad_latent, dtype,
+                                            (hipStream_t)stream),
+                      "lwl_bfht_linear_backward_latent");
+  }
+  rc = check_workspace(lwl::linear_bwd_workspace_bytes(a), workspace, workspace_bytes);
+  if (rc) return rc;
+  a.grad = grad_out;
+  a.x = input;
+  a.grad_latent = grad_latent;
+  a.work = workspace;
+  return hip_status(lwl::launch_linear_bwd(a, (hipStream_t)stream), "lwl_bfht_linear_backward_latent");
 }
 
 int lwl_bfht_sign_words(int64_t seed, int64_t block, int64_t layer, int64_t first_word,

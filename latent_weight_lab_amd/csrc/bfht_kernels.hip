@@ -282,6 +282,16 @@ static hipError_t launch_reduce(const float* part, int64_t nblocks, int64_t stri
   return hipGetLastError();
 }
 
+hipError_t launch_block_sum(const float* part, int64_t rows, int64_t stride, int64_t n, void* dst, int dtype,
+                            hipStream_t s) {
+  switch (dtype) {
+    case kF32: return launch_reduce<float>(part, rows, stride, n, (float*)dst, s);
+    case kF16: return launch_reduce<f16>(part, rows, stride, n, (f16*)dst, s);
+    case kBF16: return launch_reduce<bf16>(part, rows, stride, n, (bf16*)dst, s);
+  }
+  return hipErrorInvalidValue;
+}
+
 template <class T>
 __global__ __launch_bounds__(256) void bfht_fill_zero(T* __restrict__ x, int64_t count) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;

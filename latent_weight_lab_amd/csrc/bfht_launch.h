@@ -70,4 +70,30 @@ int linear_token_splits(const LinearArgs& a);
 size_t linear_workspace_bytes(const LinearArgs& a);
 hipError_t launch_linear(const LinearArgs& a, hipStream_t s);
 
+// Fused latent gradient of BlockFHTLinear (bfht_linear_bwd.hip):
+// grad_latent = weight_scale * T^T(grad^T x) with grad^T x formed per block on
+// chip.  bf16, B = 2^15, in_features % 16 == 0, at most 4 row tiles per block.
+struct LinearBwdArgs {
+  const void* grad;    // [tokens, out]
+  const void* x;       // [tokens, in]
+  void* grad_latent;   // [n], bf16
+  void* work;          // linear_bwd_workspace_bytes(*this) bytes, 256-byte aligned
+  int64_t tokens, in_features, out_features, n;
+  int log_block;
+  int64_t nblocks_w;   // ceil(in*out / B)
+  uint32_t seed32;
+  int layers;
+  float weight_scale;
+  int token_splits;
+};
+bool linear_bwd_applicable(int dtype, int log_block, int64_t in_features);
+int linear_bwd_token_splits(const LinearBwdArgs& a);
+size_t linear_bwd_workspace_bytes(const LinearBwdArgs& a);
+hipError_t launch_linear_bwd(const LinearBwdArgs& a, hipStream_t s);
+
+// Fixed-order sum of `rows` float32 partial rows (row r at part + r * stride)
+// into dst[0 .. n) of the given dtype (bfht_kernels.hip).
+hipError_t launch_block_sum(const float* part, int64_t rows, int64_t stride, int64_t n, void* dst, int dtype,
+                            hipStream_t s);
+
 }  // namespace lwl

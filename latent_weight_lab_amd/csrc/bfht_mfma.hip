@@ -102,55 +102,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
   uint32_t nw[4];
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
 
-  // D_0, then the float32 partial row of the first n positions, staged through
-  // the exchange space (128 KiB; 4-float chunk c at c ^ ((c >> 3) & 7): the
-  // lanes of one write hold chunks 8 apart, and this XOR spreads 8 of them
-  // over the 8 16-byte bank groups of a 128-byte row, while every aligned
-  // group of 8 chunks stays in place for the consecutive reads).
-  auto flip = [](float v, uint32_t w, int b) {
-    return __uint_as_float(__float_as_uint(v) ^ ((w << (31 - b)) & 0x80000000u));
-  };
-  f32x4* stage = reinterpret_cast<f32x4*>(lds);  // all 128 KiB
-  __syncthreads();  // every wave has read its last exchange
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    f32x4 v;
-    int p;
-    if constexpr (L % 2 == 1) {
-      // S1: chunk = the 4 tiles at register r (p0, p1 = tile bits)
-      p = (((r >> 1) & 1) << 2) + ((r & 1) << 3) + (x.p4 << 4) + (x.lane32 << 5) + ((x.wave >> 1) << 10) +
-          (x.l5 << 12) + ((r >> 2) << 13);
-      const uint32_t w = nw[r >> 2];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = flip(acc[t][r], w, (p & 31) + t);
-    } else {
-      // S0: chunk = registers r0 .. r0+3 of tile t (p0, p1 = register bits)
-      const int t = r & 3, r0 = (r >> 2) << 2;
-      p = (t << 2) + (((r0 >> 2) & 1) << 4) + (x.lane32 << 5) + (x.l5 << 10) + ((r0 >> 3) << 11) +
-          (x.wave << 12);
-      const uint32_t w = nw[r0 >> 3];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = flip(acc[t][r0 + e], w, (p & 31) + e);
-    }
-    const int c = p >> 2;
-    stage[c ^ ((c >> 3) & 7)] = v;
-  }
-  __syncthreads();
-  float* prow = partial + slot * (int64_t)n;
-  const auto p_r = rsrc(prow, (uint32_t)n * 4u);
-#pragma unroll
-  for (int i = 0; i < (kB / 4) / kThreads; ++i) {
-    const int c = i * kThreads + (int)threadIdx.x;
-    const f32x4 v = stage[c ^ ((c >> 3) & 7)];
-    const int p = c * 4;
-    if (kWhole || p + 4 <= n) {
-      __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, kStreamStore);  // dropped past n
-    } else if (p < n) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (p + e < n) prow[p + e] = v[e];
-    }
-  }
+  write_partial_row<L, kWhole>(acc, nw, x, lds, partial + slot * (int64_t)n, n, 1.0f);
 }
 
 }  // namespace

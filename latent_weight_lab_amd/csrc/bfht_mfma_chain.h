@@ -425,6 +425,63 @@ __device__ __forceinline__ void stage_output(const f32x16 (&acc)[kTiles], const 
   for (int k = 0; k < 8; ++k) stage[stage_slot(out_chunk_pos<L>(x, k) >> 3)] = out_chunk<L>(acc, nw, x, k);
 }
 
+// Backward tail: applies D_0 (inverted words `nw` of the chain's last sign
+// layer, in the chain's output layout) to the adjoint chain's result and
+// writes scale * the float32 row of the first n block positions to prow,
+// staged through the exchange space (128 KiB; 4-float chunk c at
+// c ^ ((c >> 3) & 7): the lanes of one write hold chunks 8 apart, and this XOR
+// spreads 8 of them over the 8 16-byte bank groups of a 128-byte row, while
+// every aligned group of 8 chunks stays in place for the consecutive reads).
+// kExact: n % 4 == 0 (whole 16-byte stores; stores past n are dropped).
+template <int L, bool kExact>
+__device__ __forceinline__ void write_partial_row(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4],
+                                                  const Ctx& x, unsigned char* lds, float* prow, int n,
+                                                  float scale) {
+  auto flip = [](float v, uint32_t w, int b) {
+    return __uint_as_float(__float_as_uint(v) ^ ((w << (31 - b)) & 0x80000000u));
+  };
+  f32x4* stage = reinterpret_cast<f32x4*>(lds);  // all 128 KiB
+  __syncthreads();  // every wave has read its last exchange
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    f32x4 v;
+    int p;
+    if constexpr (L % 2 == 1) {
+      // S1: chunk = the 4 tiles at register r (p0, p1 = tile bits)
+      p = (((r >> 1) & 1) << 2) + ((r & 1) << 3) + (x.p4 << 4) + (x.lane32 << 5) + ((x.wave >> 1) << 10) +
+          (x.l5 << 12) + ((r >> 2) << 13);
+      const uint32_t w = nw[r >> 2];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] = scale * flip(acc[t][r], w, (p & 31) + t);
+    } else {
+      // S0: chunk = registers r0 .. r0+3 of tile t (p0, p1 = register bits)
+      const int t = r & 3, r0 = (r >> 2) << 2;
+      p = (t << 2) + (((r0 >> 2) & 1) << 4) + (x.lane32 << 5) + (x.l5 << 10) + ((r0 >> 3) << 11) +
+          (x.wave << 12);
+      const uint32_t w = nw[r0 >> 3];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = scale * flip(acc[t][r0 + e], w, (p & 31) + e);
+    }
+    const int c = p >> 2;
+    stage[c ^ ((c >> 3) & 7)] = v;
+  }
+  __syncthreads();
+  const auto p_r = rsrc(prow, (uint32_t)n * 4u);
+#pragma unroll
+  for (int i = 0; i < (kB / 4) / kThreads; ++i) {
+    const int c = i * kThreads + (int)threadIdx.x;
+    const f32x4 v = stage[c ^ ((c >> 3) & 7)];
+    const int p = c * 4;
+    if (kExact || p + 4 <= n) {
+      __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, kStreamStore);  // dropped past n
+    } else if (p < n) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (p + e < n) prow[p + e] = v[e];
+    }
+  }
+}
+
 // Loads the S0 source operands of a block from the latent (n bf16 elements,
 // zero past the end).  kExact: n % 8 == 0, so no 16-byte chunk straddles the end.
 template <bool kExact = false>

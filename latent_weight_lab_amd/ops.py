@@ -99,6 +99,46 @@ def linear_forward(x2d: torch.Tensor, latent: torch.Tensor, out_features: int, l
     return out
 
 
+def linear_backward_latent_supported(in_features: int, out_features: int, latent: torch.Tensor,
+                                     x: torch.Tensor, grad: torch.Tensor) -> bool:
+    """Whether the fused latent gradient takes this shape (else grad_weight is formed in HBM)."""
+    if not (x.is_cuda and latent.is_cuda and grad.is_cuda and x.dtype == latent.dtype == grad.dtype
+            and x.dtype in N.DTYPE_CODES):
+        return False
+    tokens = max(1, x.numel() // max(1, in_features))
+    return N.lib().lwl_bfht_check_linear_backward_latent(N.dtype_code(x.dtype), tokens, in_features,
+                                                         latent.numel(), out_features, 1) == N.LWL_OK
+
+
+def linear_backward_latent(grad2d: torch.Tensor, x2d: torch.Tensor, latent: torch.Tensor, out_features: int,
+                           layers: int, seed: int, weight_scale: float) -> torch.Tensor:
+    """``weight_scale * block_fht_grad_latent(latent, (grad2d^T x2d).flatten(), ...)`` with the weight
+    gradient formed block by block on chip (the grad_latent branch of the reference's
+    ``_BlockFHTLinearFn.backward``, ``block_fht.py:339-350``; the modulation term is the caller's)."""
+    dev = N.require_cuda(grad2d, x2d, latent)
+    grad2d = grad2d.contiguous()
+    x2d = x2d.contiguous()
+    code = N.dtype_code(latent.dtype)
+    if not (grad2d.dtype == x2d.dtype == latent.dtype):
+        raise RuntimeError("linear latent gradient: grad, input and latent dtype must match")
+    tokens, in_features = x2d.shape
+    if grad2d.shape != (tokens, out_features):
+        raise ValueError(f"grad shape {tuple(grad2d.shape)} does not match ({tokens}, {out_features})")
+    L = N.lib()
+    N.check(L.lwl_bfht_check_linear_backward_latent(code, tokens, in_features, latent.numel(), out_features,
+                                                    layers))
+    grad_latent = torch.empty(latent.numel(), dtype=latent.dtype, device=dev)
+    with _device_guard(dev):
+        need = L.lwl_bfht_linear_backward_latent_workspace_size(tokens, in_features, out_features, latent.numel())
+        ws_ptr, ws_size, ws = N.workspace(need, dev)
+        N.check(L.lwl_bfht_linear_backward_latent(grad2d.data_ptr() if tokens else 0, x2d.data_ptr() if tokens else 0,
+                                                  code, tokens, in_features, latent.numel(), out_features, layers,
+                                                  seed, float(weight_scale), grad_latent.data_ptr(), ws_ptr,
+                                                  ws_size, N.stream_ptr(dev)))
+    del ws
+    return grad_latent
+
+
 def sign_words(seed: int, block: int, layer: int, nwords: int, first_word: int = 0,
                device: torch.device | str = "cuda") -> torch.Tensor:
     """Sign words computed by the device hash (int32 tensor holding the uint32 bits)."""

@@ -171,3 +171,32 @@ def test_linear_workspace_size():
     assert lib.lwl_bfht_linear_forward_workspace_size(255, 768, 768, 32768) == partial
     partial = (14 * 2 * 300 * 4 + 255) // 256 * 256
     assert lib.lwl_bfht_linear_forward_workspace_size(300, 1000, 450, 32768) == partial + 19 * 32 * 1024
+
+@pytest.mark.parametrize(
+    "args,code,msg",
+    [
+        # (dtype, tokens, in_features, latent_size, out_features, layers)
+        ((2, 4096, 768, 32768, 3072, 3), N.LWL_OK, ""),
+        ((2, 4096, 3072, 32768, 768, 3), N.LWL_OK, ""),
+        ((2, 0, 768, 32768, 3072, 3), N.LWL_OK, ""),
+        ((0, 16, 768, 32768, 3072, 3), N.LWL_ERR_UNSUPPORTED, "bfloat16"),     # fp32: grad_weight in HBM
+        ((2, 16, 520, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "in_features"),    # > 4 row tiles per block
+        ((2, 16, 776, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "in_features"),    # in % 16 != 0
+        ((2, 16, 768, 8192, 64, 3), N.LWL_ERR_UNSUPPORTED, "block 2^15"),      # block 2^13
+        ((2, 16, 768, 32768, 64, 0), N.LWL_ERR_INVALID, "layers must be 1, 2, or 3"),
+        ((2, 1 << 20, 1024, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "2^30"),
+    ],
+)
+def test_linear_backward_latent_validation(args, code, msg):
+    lib = N.lib()
+    assert lib.lwl_bfht_check_linear_backward_latent(*args) == code
+    if msg:
+        assert msg in lib.lwl_last_error().decode()
+
+
+def test_linear_backward_latent_workspace_size():
+    # 216 partial rows of 32768 floats (72 blocks x 3 token ranges), x in 48 column tiles x 128
+    # token steps of 1 KiB, g transposed to 3072 rows of 4096 tokens
+    lib = N.lib()
+    assert lib.lwl_bfht_linear_backward_latent_workspace_size(4096, 768, 3072, 32768) == (
+        216 * 32768 * 4 + 48 * 128 * 1024 + 3072 * 4096 * 2)
