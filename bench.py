@@ -352,6 +352,15 @@ def extra_configs(abi, steps, warmup, only):
                 lin[f"{inf}x{outf}"] = {"error": f"{type(exc).__name__}: {exc}"}
         res["c4_linear_bwd"] = lin
 
+    # weight cache of the nanoGPT GPT-2-small recipe (examples/nanogpt: 48 matrices, latent ratio 0.01,
+    # 2 layers, seeds 1000+i, float32 latents, bf16 cache): grouped prepare / flush (one C-ABI call each)
+    # vs the per-module loop (generate, scale, cast; cast, backward, scale, accumulate per module)
+    if want("c6_cache"):
+        try:
+            res["c6_cache"] = cache_bench(abi, torch)
+        except Exception as exc:  # noqa: BLE001
+            res["c6_cache"] = {"error": f"{type(exc).__name__}: {exc}"}
+
     # config 5: 12-layer GPT-2-small linear stack (qkv, proj, fc, fc-proj per layer = 48 matrices,
     # latents of 32768 bf16, seeds 100+i), forward only, fused vs dense on materialized weights
     if want("c5_stack"):
@@ -413,6 +422,82 @@ def stack_bench(abi, torch):
         except Exception as exc:  # noqa: BLE001
             row["error"] = f"{type(exc).__name__}: {exc}"
         out[f"tokens_{tokens}"] = row
+    return out
+
+
+def cache_bench(abi, torch):
+    N = abi.N
+    lib = abi.lib
+    mats = []
+    for layer in range(12):
+        for j, (inf, outf) in enumerate(GPT2_SHAPES):
+            size = inf * outf
+            n = max(1, round(size * 0.01))
+            torch.manual_seed(1000 + 4 * layer + j)
+            lat = (torch.randn(n) * 0.02).cuda()
+            mats.append({"lat": lat, "size": size, "seed": 1000 + 4 * layer + j, "n": n,
+                         "w32": torch.empty(size, device="cuda"),
+                         "wbf": torch.empty(size, dtype=torch.bfloat16, device="cuda"),
+                         "wbf2": torch.empty(size, dtype=torch.bfloat16, device="cuda"),
+                         "gw": (torch.randn(size, generator=torch.Generator().manual_seed(j)) * 1e-3).to(
+                             torch.bfloat16).cuda(),
+                         "gl": torch.zeros(n, device="cuda"), "gl2": torch.zeros(n, device="cuda"),
+                         "tmp": torch.empty(n, device="cuda")})
+    for m in mats:
+        m["bws"] = abi.bwd_ws(m["n"], m["size"], 0, m["size"], "cuda")
+        m["g32"] = torch.empty(m["size"], device="cuda")
+
+    def jobs(fwd):
+        arr = (N.WeightJob * len(mats))()
+        for j, m in zip(arr, mats):
+            j.latent = m["lat"].data_ptr()
+            j.weight = m["wbf"].data_ptr()
+            j.grad_weight = m["gw"].data_ptr()
+            j.grad_latent = m["gl"].data_ptr()
+            j.latent_size, j.size, j.layers, j.seed = m["n"], m["size"], 2, m["seed"]
+            j.latent_dtype, j.weight_dtype, j.weight_scale, j.accumulate = 0, 2, 1.0, int(not fwd)
+        return arr
+
+    fj, bj = jobs(True), jobs(False)
+    ws_bytes = lib.lwl_bfht_flush_weight_grads_workspace_size(bj, len(mats))
+    gws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+
+    def grouped_prepare():
+        N.check(lib.lwl_bfht_materialize_weights(fj, len(mats), abi.stream()))
+
+    def per_module_prepare():
+        for m in mats:
+            abi.forward(m["lat"], m["w32"], m["size"], 2, m["seed"], 0, m["size"])
+            torch.mul(m["w32"], 1.0, out=m["w32"])
+            m["wbf2"].copy_(m["w32"])
+
+    def grouped_flush():
+        N.check(lib.lwl_bfht_flush_weight_grads(bj, len(mats), gws.data_ptr(), ws_bytes, abi.stream()))
+
+    def per_module_flush():
+        for m in mats:
+            m["g32"].copy_(m["gw"])
+            abi.backward(m["g32"], m["tmp"], m["size"], 2, m["seed"], 0, m["size"], m["bws"])
+            torch.mul(m["tmp"], 1.0, out=m["tmp"])
+            m["gl2"].add_(m["tmp"])
+
+    out = {"matrices": len(mats), "params": sum(m["size"] for m in mats),
+           "latent_params": sum(m["n"] for m in mats), "flush_workspace_MiB": ws_bytes / 2**20}
+    fwd_bytes = sum(m["size"] * 2 + m["n"] * 4 for m in mats)
+    bwd_bytes = sum(m["size"] * 2 + m["n"] * 8 for m in mats)
+    for name, fn, nbytes in (("prepare_grouped", grouped_prepare, fwd_bytes),
+                             ("prepare_per_module", per_module_prepare, None),
+                             ("flush_grouped", grouped_flush, bwd_bytes),
+                             ("flush_per_module", per_module_flush, None)):
+        sec = time_graph(torch, fn, 10, 2)
+        out[name + "_ms"] = round(sec * 1e3, 4)
+        if nbytes:
+            out[name + "_algo_GBs"] = nbytes / sec / 1e9
+    out["prepare_speedup"] = out["prepare_per_module_ms"] / out["prepare_grouped_ms"]
+    out["flush_speedup"] = out["flush_per_module_ms"] / out["flush_grouped_ms"]
+    # the two paths agree bit for bit (same roundings; flush accumulated the same steps)
+    out["prepare_bit_identical"] = all(torch.equal(m["wbf"], m["wbf2"]) for m in mats)
+    out["flush_bit_identical"] = all(torch.equal(m["gl"], m["gl2"]) for m in mats)
     return out
 
 

@@ -152,6 +152,49 @@ int lwl_bfht_linear_backward_latent(const void* grad_out, const void* input, int
 int lwl_bfht_check_linear_backward_latent(int dtype, int64_t tokens, int64_t in_features,
                                           int64_t latent_size, int64_t out_features, int64_t layers);
 
+/* ---------------------------------------------------------------- weight cache, grouped
+ * Replaces the per-module loops of prepare_block_fht_weight_cache and
+ * flush_block_fht_weight_cache (reference latent_weight_lab/block_fht.py:560-569
+ * over materialize_weight_cache :503-512 and flush_weight_cache_to_latent_grad
+ * :514-557, each one ext.forward / ext.backward call, csrc/block_fht_ext_cuda.cu:516-622):
+ * every job is one module's generator over the whole weight [0, size), and all
+ * jobs run in a few launches.  T is the latent dtype, W the weight dtype:
+ *
+ *   materialize  weight[i] = W(T(T(y[i]) * weight_scale))
+ *                (torch: (generator() * weight_scale).to(W))
+ *   flush        r = T(T(adjoint(T(grad_weight))) * weight_scale)
+ *                grad_latent = accumulate ? T(grad_latent + r) : r
+ *                (torch: weight_scale * block_fht_grad_latent(latent,
+ *                 grad_weight.to(T)), then latent.grad.add_ or assignment)
+ *
+ * Each block runs the code of the per-module call, so the results are
+ * bit-identical to it.  Jobs take latents of length <= 32768 (blocks up to
+ * 2^15); bfloat16 latents of block 2^15 need W = bfloat16.  Destinations must
+ * not overlap.  Gains, modulation and residual weights stay with the caller.
+ * The flush workspace holds every job's per-block float32 partial rows.
+ */
+typedef struct lwl_bfht_weight_job {
+  const void* latent;      /* [latent_size], latent_dtype (materialize) */
+  void* weight;            /* [size], weight_dtype (materialize: written) */
+  const void* grad_weight; /* [size], weight_dtype (flush: read) */
+  void* grad_latent;       /* [latent_size], latent_dtype (flush: written, read when accumulate) */
+  int64_t latent_size;
+  int64_t size;            /* in_features * out_features */
+  int64_t layers;
+  int64_t seed;
+  int32_t latent_dtype;
+  int32_t weight_dtype;
+  double weight_scale;
+  int32_t accumulate;      /* flush: add into grad_latent instead of overwriting it */
+} lwl_bfht_weight_job;
+
+/* Host-only check of count jobs for materialize (forward != 0) or flush. */
+int lwl_bfht_check_weight_jobs(const lwl_bfht_weight_job* jobs, int64_t count, int forward);
+int lwl_bfht_materialize_weights(const lwl_bfht_weight_job* jobs, int64_t count, void* stream);
+size_t lwl_bfht_flush_weight_grads_workspace_size(const lwl_bfht_weight_job* jobs, int64_t count);
+int lwl_bfht_flush_weight_grads(const lwl_bfht_weight_job* jobs, int64_t count, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- sign words
  * Parity probe for the device hash (reference device functions
  * csrc/block_fht_ext_cuda.cu:27-43; Python twin block_fht.py:36-52):

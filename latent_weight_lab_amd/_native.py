@@ -31,6 +31,25 @@ LWL_ERR_HIP = -4
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 
+class WeightJob(ctypes.Structure):
+    """``lwl_bfht_weight_job``: one module's whole weight in a grouped
+    materialize / flush call."""
+    _fields_ = [
+        ("latent", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p),
+        ("grad_weight", ctypes.c_void_p),
+        ("grad_latent", ctypes.c_void_p),
+        ("latent_size", ctypes.c_int64),
+        ("size", ctypes.c_int64),
+        ("layers", ctypes.c_int64),
+        ("seed", ctypes.c_int64),
+        ("latent_dtype", ctypes.c_int32),
+        ("weight_dtype", ctypes.c_int32),
+        ("weight_scale", ctypes.c_double),
+        ("accumulate", ctypes.c_int32),
+    ]
+
+
 class BlockFHTArgumentError(ValueError, RuntimeError):
     """Invalid argument.  The reference raises ValueError from its Python
     checks and RuntimeError from its extension's TORCH_CHECKs; this is both."""
@@ -49,6 +68,7 @@ def library_path() -> Path:
 def _bind(lib) -> None:
     i64, i32, sz, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p
     dbl, u32p = ctypes.c_double, ctypes.POINTER(ctypes.c_uint32)
+    jobp = ctypes.POINTER(WeightJob)
     sigs = {
         "lwl_last_error": (ctypes.c_char_p, []),
         "lwl_abi_version": (i32, []),
@@ -64,6 +84,10 @@ def _bind(lib) -> None:
         "lwl_bfht_linear_backward_latent": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, dbl, vp, vp, sz, vp]),
         "lwl_bfht_check_linear_backward_latent": (i32, [i32, i64, i64, i64, i64, i64]),
         "lwl_bfht_sign_words": (i32, [i64, i64, i64, i64, i64, u32p, vp]),
+        "lwl_bfht_check_weight_jobs": (i32, [jobp, i64, i32]),
+        "lwl_bfht_materialize_weights": (i32, [jobp, i64, vp]),
+        "lwl_bfht_flush_weight_grads_workspace_size": (sz, [jobp, i64]),
+        "lwl_bfht_flush_weight_grads": (i32, [jobp, i64, vp, sz, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)

@@ -255,7 +255,10 @@ class BlockFHTLinear(nn.Module):
     @property
     def weight(self) -> torch.Tensor:
         """The generated weight with every option applied (reference ``block_fht.py:444-462``)."""
-        weight = self.generator() * self.weight_scale
+        return self._finish_weight(self.generator() * self.weight_scale)
+
+    def _finish_weight(self, weight: torch.Tensor) -> torch.Tensor:
+        """Every option after ``generator() * weight_scale`` (flat, latent dtype)."""
         if self.modulation_alpha != 0.0:
             weight = weight + self.modulation_alpha * self._modulation_offset()
         weight = weight.view(self.out_features, self.in_features)
@@ -318,49 +321,144 @@ class BlockFHTLinear(nn.Module):
         if self._cached_weight is None:
             return
         if self._cached_weight.grad is not None:
-            latent = self.generator.latent
-            grad_weight = self._cached_weight.grad.to(dtype=latent.dtype)
-            cached = self._cached_weight.detach().to(dtype=latent.dtype)
-            generated_grad = grad_weight
-            for gain, dim, view in ((self.output_gain, 1, (-1, 1)), (self.input_gain, 0, (1, -1))):
-                if gain is None:
-                    continue
-                g = gain.detach().to(dtype=latent.dtype)
-                if torch.any(g == 0):
-                    which = "output" if dim == 1 else "input"
-                    raise RuntimeError(f"cannot flush a cached BlockFHT weight with a zero {which} gain")
-                gain_grad = (grad_weight * (cached / g.view(*view))).sum(dim=dim).to(dtype=gain.dtype)
-                if gain.grad is None:
-                    gain.grad = gain_grad
-                else:
-                    gain.grad.add_(gain_grad)
-                generated_grad = generated_grad * g.view(*view)
-            generated_grad = generated_grad.reshape(-1)
-            if self.residual_base_weight is not None:
-                generated_grad = generated_grad * self.residual_base_scale
-            grad_latent = self.weight_scale * block_fht_grad_latent(latent, generated_grad, self.generator.size,
-                                                                    self.generator.layers, self.generator.seed)
-            if self.modulation_alpha != 0.0:
-                grad_latent = grad_latent + 2.0 * self.modulation_alpha * latent * generated_grad.sum()
-            if latent.grad is None:
-                latent.grad = grad_latent
-            else:
-                latent.grad.add_(grad_latent)
+            g = self.generator
+            generated_grad = self._generated_weight_grad()
+            grad_latent = self.weight_scale * block_fht_grad_latent(g.latent, generated_grad, g.size, g.layers, g.seed)
+            self._add_latent_grad(grad_latent, generated_grad)
         self._cached_weight = None
+
+    def _generated_weight_grad(self) -> torch.Tensor:
+        """Gradient of the cached weight with respect to the generated one (flat,
+        latent dtype); accumulates the gains' gradients on the way."""
+        latent = self.generator.latent
+        grad_weight = self._cached_weight.grad.to(dtype=latent.dtype)
+        cached = self._cached_weight.detach().to(dtype=latent.dtype)
+        generated_grad = grad_weight
+        for gain, dim, view in ((self.output_gain, 1, (-1, 1)), (self.input_gain, 0, (1, -1))):
+            if gain is None:
+                continue
+            gd = gain.detach().to(dtype=latent.dtype)
+            if torch.any(gd == 0):
+                which = "output" if dim == 1 else "input"
+                raise RuntimeError(f"cannot flush a cached BlockFHT weight with a zero {which} gain")
+            gain_grad = (grad_weight * (cached / gd.view(*view))).sum(dim=dim).to(dtype=gain.dtype)
+            if gain.grad is None:
+                gain.grad = gain_grad
+            else:
+                gain.grad.add_(gain_grad)
+            generated_grad = generated_grad * gd.view(*view)
+        generated_grad = generated_grad.reshape(-1)
+        if self.residual_base_weight is not None:
+            generated_grad = generated_grad * self.residual_base_scale
+        return generated_grad
+
+    def _add_latent_grad(self, grad_latent: torch.Tensor, generated_grad: torch.Tensor) -> None:
+        latent = self.generator.latent
+        if self.modulation_alpha != 0.0:
+            grad_latent = grad_latent + 2.0 * self.modulation_alpha * latent * generated_grad.sum()
+        if latent.grad is None:
+            latent.grad = grad_latent
+        else:
+            latent.grad.add_(grad_latent)
+
+    def _cache_needs_torch_epilogue(self) -> bool:
+        # options applied in torch around the grouped kernels (the plain case
+        # scales, casts and accumulates inside them)
+        return self.modulation_alpha != 0.0 or self.output_gain is not None or self.input_gain is not None
+
+
+def _cacheable(module: "BlockFHTLinear") -> bool:
+    return (module.residual_base_weight is None and module.spectral_core is None
+            and module._cached_weight is None)
 
 
 def prepare_block_fht_weight_cache(model: nn.Module, dtype: torch.dtype | None = None) -> None:
-    """Materialize every BlockFHTLinear's weight once (reference ``block_fht.py:560-563``)."""
+    """Materialize every BlockFHTLinear's weight once (reference ``block_fht.py:560-563``).
+
+    The generators run together in a few grouped launches (``ops.materialize_weights``);
+    a module the grouped kernels do not take (blocks above 2^15, a bfloat16 latent of
+    block 2^15 cached in another dtype) materializes on its own.  The cached weights
+    are bit-identical either way.
+    """
+    grouped, specs = [], []
     for module in model.modules():
-        if isinstance(module, BlockFHTLinear):
+        if not isinstance(module, BlockFHTLinear) or not _cacheable(module):
+            continue
+        g = module.generator
+        latent = g.latent
+        plain = not module._cache_needs_torch_epilogue()
+        # the kernel's output dtype: the cache dtype when it finishes the weight
+        wdtype = (dtype or latent.dtype) if plain else latent.dtype
+        if ops.weight_job_supported(latent, g.size, g.layers, wdtype):
+            grouped.append((module, plain))
+            specs.append((latent, g.size, g.layers, g.seed, module.weight_scale, wdtype))
+        else:
             module.materialize_weight_cache(dtype=dtype)
+    if not specs:
+        return
+    with torch.no_grad():
+        weights = ops.materialize_weights(specs)
+        for (module, plain), w in zip(grouped, weights):
+            if not plain:
+                w = module._finish_weight(w)
+                if dtype is not None:
+                    w = w.to(dtype=dtype)
+            module._cached_weight = w.view(module.out_features, module.in_features).detach().requires_grad_(True)
 
 
 def flush_block_fht_weight_cache(model: nn.Module) -> None:
-    """Reference ``block_fht.py:566-569``."""
+    """Project every cached weight's gradient onto its latent and drop the caches
+    (reference ``block_fht.py:566-569``).
+
+    All generators' adjoints run in a few grouped launches (``ops.flush_weight_grads``),
+    which also scale by weight_scale and add into ``latent.grad``; gains and
+    modulation are applied in torch around them, as in the per-module flush.
+    """
+    grouped, specs, targets = [], [], set()
     for module in model.modules():
-        if isinstance(module, BlockFHTLinear):
+        if not isinstance(module, BlockFHTLinear) or module._cached_weight is None:
+            continue
+        cached = module._cached_weight
+        if cached.grad is None:
+            module._cached_weight = None
+            continue
+        g = module.generator
+        latent = g.latent
+        plain = not module._cache_needs_torch_epilogue()
+        if plain:
+            source = cached.grad.contiguous().reshape(-1)
+            supported = ops.weight_job_supported(latent, g.size, g.layers, source.dtype, source)
+        else:
+            # the source is the generated-weight gradient in the latent dtype
+            supported = ops.weight_job_supported(latent, g.size, g.layers, latent.dtype)
+        if not supported:
             module.flush_weight_cache_to_latent_grad()
+            continue
+        if not plain:
+            source = module._generated_weight_grad()
+        into = None
+        if (plain and latent.grad is not None and latent.grad.is_contiguous() and latent.grad.dtype == latent.dtype
+                and id(latent) not in targets):
+            into = latent.grad  # the kernel adds in place (a latent shared by modules: the first only)
+        targets.add(id(latent))
+        grouped.append((module, plain, source, into))
+        specs.append((latent, source, g.size, g.layers, g.seed, module.weight_scale, into))
+    if not specs:
+        return
+    with torch.no_grad():
+        results = ops.flush_weight_grads(specs)
+    for (module, plain, source, into), r in zip(grouped, results):
+        latent = module.generator.latent
+        if into is not None:
+            pass  # added in place
+        elif plain:
+            if latent.grad is None:
+                latent.grad = r
+            else:
+                latent.grad.add_(r)
+        else:
+            module._add_latent_grad(r, source)
+        module._cached_weight = None
 
 
 def suspend_block_fht_weight_cache(model: nn.Module) -> list[tuple[BlockFHTLinear, torch.Tensor]]:

@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "bfht_launch.h"
 
@@ -209,6 +210,56 @@ int check_workspace(size_t need, const void* ws, size_t have) {
   return LWL_OK;
 }
 
+// Grouped weight-cache jobs (block_fht.py:503-569): each job is the whole
+// weight of one module, with the per-module call's checks.
+int check_weight_jobs(const lwl_bfht_weight_job* jobs, int64_t count, bool fwd, std::vector<lwl::WeightJob>* out) {
+  if (count < 0) return fail(LWL_ERR_INVALID, "job count must be non-negative");
+  if (count > 0 && !jobs) return fail(LWL_ERR_INVALID, "jobs must be non-null");
+  std::vector<lwl::WeightJob> v((size_t)count);
+  for (int64_t i = 0; i < count; ++i) {
+    const lwl_bfht_weight_job& j = jobs[i];
+    int rc = check_common(j.latent_dtype, j.latent_size, j.size, j.layers, 0, j.size);
+    if (rc) return fail(rc, "job %lld: %s", (long long)i, g_last_error.c_str());
+    if (!valid_dtype(j.weight_dtype))
+      return fail(LWL_ERR_UNSUPPORTED, "job %lld: weight dtype code %d is not float32, float16 or bfloat16",
+                  (long long)i, j.weight_dtype);
+    if (fwd ? (!j.latent || !j.weight) : (!j.grad_weight || !j.grad_latent))
+      return fail(LWL_ERR_INVALID, "job %lld: %s must be non-null", (long long)i,
+                  fwd ? "latent and weight" : "grad_weight and grad_latent");
+    lwl::WeightJob w{};
+    w.latent = j.latent;
+    w.weight = j.weight;
+    w.grad_weight = j.grad_weight;
+    w.grad_latent = j.grad_latent;
+    w.n = j.latent_size;
+    w.size = j.size;
+    w.layers = (int)j.layers;
+    w.seed32 = fold_seed(j.seed);
+    w.ldtype = j.latent_dtype;
+    w.wdtype = j.weight_dtype;
+    w.scale = (float)j.weight_scale;
+    w.accumulate = j.accumulate != 0;
+    const char* why = nullptr;
+    if (!lwl::grouped_job_supported(w, fwd, &why)) return fail(LWL_ERR_UNSUPPORTED, "job %lld: %s", (long long)i, why);
+    v[(size_t)i] = w;
+  }
+  // destinations pairwise disjoint (one launch writes them all)
+  auto esize = [](int d) { return d == LWL_DTYPE_F32 ? 4 : 2; };
+  for (int64_t a = 0; a < count; ++a)
+    for (int64_t b = a + 1; b < count; ++b) {
+      const auto& x = v[(size_t)a];
+      const auto& y = v[(size_t)b];
+      const uintptr_t x0 = (uintptr_t)(fwd ? x.weight : x.grad_latent);
+      const uintptr_t y0 = (uintptr_t)(fwd ? y.weight : y.grad_latent);
+      const uintptr_t x1 = x0 + (uintptr_t)(fwd ? x.size * esize(x.wdtype) : x.n * esize(x.ldtype));
+      const uintptr_t y1 = y0 + (uintptr_t)(fwd ? y.size * esize(y.wdtype) : y.n * esize(y.ldtype));
+      if (x0 < y1 && y0 < x1)
+        return fail(LWL_ERR_INVALID, "jobs %lld and %lld write overlapping memory", (long long)a, (long long)b);
+    }
+  if (out) *out = std::move(v);
+  return LWL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -337,6 +388,36 @@ int lwl_bfht_linear_backward_latent(const void* grad_out, const void* input, int
   a.grad_latent = grad_latent;
   a.work = workspace;
   return hip_status(lwl::launch_linear_bwd(a, (hipStream_t)stream), "lwl_bfht_linear_backward_latent");
+}
+
+int lwl_bfht_check_weight_jobs(const lwl_bfht_weight_job* jobs, int64_t count, int forward) {
+  const int rc = check_weight_jobs(jobs, count, forward != 0, nullptr);
+  return rc ? rc : ok();
+}
+
+int lwl_bfht_materialize_weights(const lwl_bfht_weight_job* jobs, int64_t count, void* stream) {
+  std::vector<lwl::WeightJob> v;
+  const int rc = check_weight_jobs(jobs, count, true, &v);
+  if (rc) return rc;
+  return hip_status(lwl::launch_grouped(v.data(), count, nullptr, (hipStream_t)stream, true),
+                    "lwl_bfht_materialize_weights");
+}
+
+size_t lwl_bfht_flush_weight_grads_workspace_size(const lwl_bfht_weight_job* jobs, int64_t count) {
+  std::vector<lwl::WeightJob> v;
+  if (check_weight_jobs(jobs, count, false, &v)) return 0;
+  return lwl::grouped_workspace_bytes(v.data(), count);
+}
+
+int lwl_bfht_flush_weight_grads(const lwl_bfht_weight_job* jobs, int64_t count, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  std::vector<lwl::WeightJob> v;
+  int rc = check_weight_jobs(jobs, count, false, &v);
+  if (rc) return rc;
+  rc = check_workspace(lwl::grouped_workspace_bytes(v.data(), count), workspace, workspace_bytes);
+  if (rc) return rc;
+  return hip_status(lwl::launch_grouped(v.data(), count, workspace, (hipStream_t)stream, false),
+                    "lwl_bfht_flush_weight_grads");
 }
 
 int lwl_bfht_sign_words(int64_t seed, int64_t block, int64_t layer, int64_t first_word,

@@ -65,6 +65,15 @@ __device__ __forceinline__ T from_f32(float v) {
 
 __device__ __forceinline__ int lds_index(int p) { return p + (p >> 5); }
 
+// Job of workgroup `wg` in a grouped launch (uniform across the workgroup):
+// the table's prefix sums count workgroups, so each workgroup serves one job.
+template <class Table>
+__device__ __forceinline__ int group_job(const Table& g, int wg) {
+  int j = 0;
+  while (j + 1 < g.count && wg >= g.prefix[j + 1]) ++j;
+  return j;
+}
+
 // Index of the element that thread t holds in register r for bit group
 // [lo, lo + nb) of an LB-bit index space, with 2^LE registers per thread.
 // Register bits below nb walk the group; the remaining register bits pick one

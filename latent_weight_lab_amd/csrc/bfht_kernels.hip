@@ -54,17 +54,16 @@ __device__ __forceinline__ float inv_sqrt_block() {
 
 // ---------------------------------------------------------------- whole block
 
-template <int LB, class T>
-__global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd(const T* __restrict__ latent,
-                                                             T* __restrict__ out, int n,
-                                                             int64_t first_block, int64_t nblocks,
-                                                             int64_t start, int64_t stop,
-                                                             uint32_t seed32, int layers) {
+// Forward of block slot `slot` (block first_block + slot of one generator) by
+// thread group gi of the workgroup; every thread of the workgroup calls it
+// (barriers inside), threads of an inactive slot (slot >= nblocks) included.
+template <int LB, class T, class Store>
+__device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Store out, int n,
+                                               int64_t first_block, int64_t slot, int64_t nblocks, int64_t start,
+                                               int64_t stop, uint32_t seed32, int layers, float* smem) {
   using Gm = Geo<LB>;
-  __shared__ float smem[Gm::LDS_FLOATS];
   const int gi = threadIdx.x >> Gm::LT;
   const int t = threadIdx.x & (Gm::TB - 1);
-  const int64_t slot = (int64_t)blockIdx.x * Gm::G + gi;
   const bool active = slot < nblocks;
   const int64_t block = first_block + (active ? slot : 0);
   float* lds = smem + (Gm::NG > 1 ? gi * Gm::PADDED : 0);
@@ -115,14 +114,14 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd(const T* __restric
 #pragma unroll
     for (int k = 0; k < Gm::E; ++k) {
       const int p = k * Gm::TB + t;
-      if (p >= lo && p < hi) out[base + p - start] = from_f32<T>(lds[Gm::coal(t, k)]);
+      if (p >= lo && p < hi) out(base + p - start, lds[Gm::coal(t, k)]);
     }
   } else {
     if (!active) return;
 #pragma unroll
     for (int r = 0; r < Gm::E; ++r) {
       const int p = p0 + r;
-      if (p >= lo && p < hi) out[base + p - start] = from_f32<T>(v[r]);
+      if (p >= lo && p < hi) out(base + p - start, v[r]);
     }
   }
 }
@@ -130,19 +129,14 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd(const T* __restric
 // Backward: adjoint chain D_0 H D_1 ... H D_L on grad scattered into the block
 // frame.  Writes partial[slot * n + p] (float32) for p < n, or the final
 // gradient in T when `direct` (a single block).
-template <int LB, class T>
-__global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restrict__ grad,
-                                                             float* __restrict__ partial,
-                                                             T* __restrict__ grad_latent, int n,
-                                                             int64_t first_block, int64_t nblocks,
-                                                             int64_t start, int64_t stop,
-                                                             uint32_t seed32, int layers,
-                                                             int direct) {
+template <int LB, class T, class Load>
+__device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ partial,
+                                               T* __restrict__ grad_latent, int n, int64_t first_block,
+                                               int64_t slot, int64_t nblocks, int64_t start, int64_t stop,
+                                               uint32_t seed32, int layers, int direct, float* smem) {
   using Gm = Geo<LB>;
-  __shared__ float smem[Gm::LDS_FLOATS];
   const int gi = threadIdx.x >> Gm::LT;
   const int t = threadIdx.x & (Gm::TB - 1);
-  const int64_t slot = (int64_t)blockIdx.x * Gm::G + gi;
   const bool active = slot < nblocks;
   const int64_t block = first_block + (active ? slot : 0);
   float* lds = smem + (Gm::NG > 1 ? gi * Gm::PADDED : 0);
@@ -159,7 +153,7 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
 #pragma unroll
     for (int k = 0; k < Gm::E; ++k) {
       const int p = k * Gm::TB + t;
-      lds[Gm::coal(t, k)] = (active && p >= lo && p < hi) ? to_f32(grad[base + p - start]) : 0.0f;
+      lds[Gm::coal(t, k)] = (active && p >= lo && p < hi) ? grad(base + p - start) : 0.0f;
     }
     __syncthreads();
 #pragma unroll
@@ -168,7 +162,7 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
 #pragma unroll
     for (int r = 0; r < Gm::E; ++r) {
       const int p = p0 + r;
-      v[r] = (active && p >= lo && p < hi) ? to_f32(grad[base + p - start]) : 0.0f;
+      v[r] = (active && p >= lo && p < hi) ? grad(base + p - start) : 0.0f;
     }
   }
   const float scale = inv_sqrt_block<LB>();
@@ -214,6 +208,97 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
   }
 }
 
+// Element access of the per-generator launches: the slice in the latent dtype.
+template <class T>
+struct SliceStore {
+  T* out;
+  __device__ void operator()(int64_t i, float v) const { out[i] = from_f32<T>(v); }
+};
+template <class T>
+struct SliceLoad {
+  const T* g;
+  __device__ float operator()(int64_t i) const { return to_f32(g[i]); }
+};
+
+template <int LB, class T>
+__global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd(const T* __restrict__ latent, T* __restrict__ out,
+                                                             int n, int64_t first_block, int64_t nblocks,
+                                                             int64_t start, int64_t stop, uint32_t seed32,
+                                                             int layers) {
+  __shared__ float smem[Geo<LB>::LDS_FLOATS];
+  const int64_t slot = (int64_t)blockIdx.x * Geo<LB>::G + (threadIdx.x >> Geo<LB>::LT);
+  block_fwd_slot<LB, T>(latent, SliceStore<T>{out}, n, first_block, slot, nblocks, start, stop, seed32, layers,
+                        smem);
+}
+
+template <int LB, class T>
+__global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restrict__ grad,
+                                                             float* __restrict__ partial,
+                                                             T* __restrict__ grad_latent, int n,
+                                                             int64_t first_block, int64_t nblocks, int64_t start,
+                                                             int64_t stop, uint32_t seed32, int layers,
+                                                             int direct) {
+  __shared__ float smem[Geo<LB>::LDS_FLOATS];
+  const int64_t slot = (int64_t)blockIdx.x * Geo<LB>::G + (threadIdx.x >> Geo<LB>::LT);
+  block_bwd_slot<LB, T>(SliceLoad<T>{grad}, partial, grad_latent, n, first_block, slot, nblocks, start, stop,
+                        seed32, layers, direct, smem);
+}
+
+// ---------------------------------------------------------------- grouped
+
+// Element access of the grouped weight jobs.  Store: the generator value in the
+// latent dtype T, times the weight scale rounded to T again, then cast to the
+// weight dtype.  Load: the weight gradient cast to T first.
+template <class T>
+__device__ __forceinline__ float round_to(float v) {
+  return to_f32(from_f32<T>(v));
+}
+
+template <class T>
+struct WeightStore {
+  void* out;
+  int code;
+  float scale;
+  __device__ void operator()(int64_t i, float v) const {
+    const float y = round_to<T>(round_to<T>(v) * scale);
+    if (code == kF32) static_cast<float*>(out)[i] = y;
+    else if (code == kF16) static_cast<f16*>(out)[i] = from_f32<f16>(y);
+    else static_cast<bf16*>(out)[i] = from_f32<bf16>(y);
+  }
+};
+template <class T>
+struct WeightGradLoad {
+  const void* g;
+  int code;
+  __device__ float operator()(int64_t i) const {
+    float v;
+    if (code == kF32) v = static_cast<const float*>(g)[i];
+    else if (code == kF16) v = to_f32(static_cast<const f16*>(g)[i]);
+    else v = to_f32(static_cast<const bf16*>(g)[i]);
+    return round_to<T>(v);
+  }
+};
+
+template <int LB, class T>
+__global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd_grouped(const GroupTable g) {
+  __shared__ float smem[Geo<LB>::LDS_FLOATS];
+  const int j = group_job(g, (int)blockIdx.x);
+  const GroupJob& jb = g.job[j];
+  const int64_t slot = (int64_t)(blockIdx.x - g.prefix[j]) * Geo<LB>::G + (threadIdx.x >> Geo<LB>::LT);
+  block_fwd_slot<LB, T>(static_cast<const T*>(jb.src), WeightStore<T>{jb.dst, jb.wdtype, jb.scale}, jb.n, 0, slot,
+                        jb.nblocks, 0, jb.size, jb.seed32, jb.layers, smem);
+}
+
+template <int LB, class T>
+__global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd_grouped(const GroupTable g) {
+  __shared__ float smem[Geo<LB>::LDS_FLOATS];
+  const int j = group_job(g, (int)blockIdx.x);
+  const GroupJob& jb = g.job[j];
+  const int64_t slot = (int64_t)(blockIdx.x - g.prefix[j]) * Geo<LB>::G + (threadIdx.x >> Geo<LB>::LT);
+  block_bwd_slot<LB, T>(WeightGradLoad<T>{jb.src, jb.wdtype}, jb.part, static_cast<T*>(nullptr), jb.n, 0, slot,
+                        jb.nblocks, 0, jb.size, jb.seed32, jb.layers, 0, smem);
+}
+
 // grad_latent[p] = sum_b part[b * stride + p], blocks in order.
 // Fixed-order sum of the per-block float32 partial rows: grad[p] = sum over b
 // of part[b * stride + p].  Each workgroup owns 128 columns (2 per lane); wave
@@ -226,13 +311,13 @@ constexpr int kRedWaves = 8;
 constexpr int kRedCols = 128;
 constexpr int kRedDepth = 16;
 
-template <class T, bool kPairs>
-__global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_blocks(const float* __restrict__ part,
-                                                                     int64_t nblocks, int64_t stride, int n,
-                                                                     T* __restrict__ grad_latent) {
-  __shared__ float sums[kRedWaves][2][64];
+// Column pair c0, c0 + 1 of the sum; every thread of the workgroup calls it,
+// and wave 0 returns true with the totals.
+template <bool kPairs>
+__device__ __forceinline__ bool reduce_columns(const float* __restrict__ part, int64_t nblocks, int64_t stride,
+                                               int n, int c0, float (&sums)[kRedWaves][2][64], float& t0,
+                                               float& t1) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int c0 = blockIdx.x * kRedCols + 2 * lane;
   const bool has0 = c0 < n, has1 = c0 + 1 < n;
   float a0 = 0.0f, a1 = 0.0f;
   auto row = [&](int64_t b) -> float2 {
@@ -259,15 +344,54 @@ __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_blocks(const float
   sums[wave][0][lane] = a0;
   sums[wave][1][lane] = a1;
   __syncthreads();
-  if (wave != 0) return;
-  float t0 = 0.0f, t1 = 0.0f;
+  if (wave != 0) return false;
+  t0 = 0.0f;
+  t1 = 0.0f;
 #pragma unroll
   for (int w = 0; w < kRedWaves; ++w) {
     t0 += sums[w][0][lane];
     t1 += sums[w][1][lane];
   }
-  if (has0) grad_latent[c0] = from_f32<T>(t0);
-  if (has1) grad_latent[c0 + 1] = from_f32<T>(t1);
+  return true;
+}
+
+template <class T, bool kPairs>
+__global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_blocks(const float* __restrict__ part,
+                                                                     int64_t nblocks, int64_t stride, int n,
+                                                                     T* __restrict__ grad_latent) {
+  __shared__ float sums[kRedWaves][2][64];
+  const int c0 = blockIdx.x * kRedCols + 2 * (threadIdx.x & 63);
+  float t0, t1;
+  if (!reduce_columns<kPairs>(part, nblocks, stride, n, c0, sums, t0, t1)) return;
+  if (c0 < n) grad_latent[c0] = from_f32<T>(t0);
+  if (c0 + 1 < n) grad_latent[c0 + 1] = from_f32<T>(t1);
+}
+
+// Grouped block sums with the flush epilogue: r = T(T(sum) * scale), added to
+// the destination in T when the job accumulates.
+template <class T>
+__device__ __forceinline__ void grad_store(T* dst, int i, float sum, float scale, int accumulate) {
+  float r = round_to<T>(round_to<T>(sum) * scale);
+  if (accumulate) r = to_f32(dst[i]) + r;
+  dst[i] = from_f32<T>(r);
+}
+
+template <class T>
+__global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_grouped(const GroupTable g) {
+  static_assert(kGroupReduceCols == kRedCols, "grouped prefix counts reduce tiles");
+  __shared__ float sums[kRedWaves][2][64];
+  const int j = group_job(g, (int)blockIdx.x);
+  const GroupJob& jb = g.job[j];
+  const int n = jb.n;
+  const int c0 = (blockIdx.x - g.prefix[j]) * kRedCols + 2 * (threadIdx.x & 63);
+  float t0, t1;
+  // 8-byte row loads need even row strides (part is 256-byte aligned)
+  const bool done = (n % 2 == 0) ? reduce_columns<true>(jb.part, jb.nblocks, n, n, c0, sums, t0, t1)
+                                 : reduce_columns<false>(jb.part, jb.nblocks, n, n, c0, sums, t0, t1);
+  if (!done) return;
+  T* dst = static_cast<T*>(jb.dst);
+  if (c0 < n) grad_store<T>(dst, c0, t0, jb.scale, jb.accumulate);
+  if (c0 + 1 < n) grad_store<T>(dst, c0 + 1, t1, jb.scale, jb.accumulate);
 }
 
 template <class T>
@@ -577,6 +701,55 @@ static hipError_t run_typed(const BfhtArgs& a, hipStream_t s, bool fwd) {
   if (a.log_block <= kTileLog)
     return dispatch_block<T>(a.log_block, fwd, a, s, std::make_integer_sequence<int, kTileLog + 1>{});
   return run_tiles<T>(a, s, fwd);
+}
+
+int group_slots_per_wg(int log_block) {
+  // Geo<LB>::G: blocks of 2^LB that one workgroup transforms together
+  const int tb = 1 << (log_block - (log_block < 5 ? log_block : 5));
+  return (tb < 256 ? 256 : tb) / tb;
+}
+
+template <int LB, class T>
+static hipError_t launch_block_grouped_lb(const GroupTable& g, hipStream_t s, bool fwd) {
+  if (group_slots_per_wg(LB) != Geo<LB>::G) return hipErrorInvalidValue;  // the planner's prefix unit
+  const dim3 grid((unsigned)g.prefix[g.count]), block(Geo<LB>::WG);
+  if (fwd)
+    hipLaunchKernelGGL((bfht_block_fwd_grouped<LB, T>), grid, block, 0, s, g);
+  else
+    hipLaunchKernelGGL((bfht_block_bwd_grouped<LB, T>), grid, block, 0, s, g);
+  return hipGetLastError();
+}
+
+template <class T, int... LBs>
+static hipError_t dispatch_grouped(const GroupTable& g, int LB, hipStream_t s, bool fwd,
+                                   std::integer_sequence<int, LBs...>) {
+  using Fn = hipError_t (*)(const GroupTable&, hipStream_t, bool);
+  static const Fn table[] = {&launch_block_grouped_lb<LBs, T>...};
+  return table[LB](g, s, fwd);
+}
+
+hipError_t launch_block_grouped(const GroupTable& g, int dtype, int log_block, hipStream_t s, bool fwd) {
+  if (g.count <= 0 || g.prefix[g.count] == 0) return hipSuccess;
+  if (log_block < 0 || log_block > kTileLog) return hipErrorInvalidValue;
+  const auto seq = std::make_integer_sequence<int, kTileLog + 1>{};
+  switch (dtype) {
+    case kF32: return dispatch_grouped<float>(g, log_block, s, fwd, seq);
+    case kF16: return dispatch_grouped<f16>(g, log_block, s, fwd, seq);
+    case kBF16: return dispatch_grouped<bf16>(g, log_block, s, fwd, seq);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_reduce_grouped(const GroupTable& g, int dtype, hipStream_t s) {
+  if (g.count <= 0 || g.prefix[g.count] == 0) return hipSuccess;
+  const dim3 grid((unsigned)g.prefix[g.count]), block(64 * kRedWaves);
+  switch (dtype) {
+    case kF32: hipLaunchKernelGGL((bfht_reduce_grouped<float>), grid, block, 0, s, g); break;
+    case kF16: hipLaunchKernelGGL((bfht_reduce_grouped<f16>), grid, block, 0, s, g); break;
+    case kBF16: hipLaunchKernelGGL((bfht_reduce_grouped<bf16>), grid, block, 0, s, g); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_bfht(const BfhtArgs& a, hipStream_t s, bool forward) {

@@ -96,4 +96,60 @@ hipError_t launch_linear_bwd(const LinearBwdArgs& a, hipStream_t s);
 hipError_t launch_block_sum(const float* part, int64_t rows, int64_t stride, int64_t n, void* dst, int dtype,
                             hipStream_t s);
 
+// Grouped whole-weight generation and its adjoint: the weight-cache prepare and
+// flush of many generators (one per BlockFHTLinear) in a few launches
+// (bfht_grouped.cpp plans them).  Each job is one generator over [0, size):
+//   forward   dst[i] = W(T(T(gen[i]) * scale))                   (weight dtype W)
+//   backward  r = T(T(adjoint(T(src))) * scale); dst = accumulate ? T(dst + r) : r
+// with T the latent dtype, i.e. the roundings of the per-generator launch
+// followed by torch's `* weight_scale`, `.to(dtype)` and `grad.add_`.
+constexpr int kGroupMaxJobs = 32;
+struct GroupJob {
+  const void* src;   // forward: latent [n]; backward: grad of the weight [size] (weight dtype)
+  void* dst;         // forward: weight [size] (weight dtype); backward: grad_latent [n]
+  float* part;       // backward: nblocks partial rows of n floats
+  int64_t size;
+  int32_t n;
+  int32_t nblocks;   // ceil(size / B)
+  uint32_t seed32;
+  int32_t layers;
+  int32_t wdtype;    // weight dtype code
+  int32_t accumulate;
+  float scale;
+};
+// Passed by value; prefix[j] = first workgroup of job j, prefix[count] = grid.
+struct GroupTable {
+  int32_t count;
+  int32_t prefix[kGroupMaxJobs + 1];
+  GroupJob job[kGroupMaxJobs];
+};
+// Whole-block jobs (B <= 2^15) of one latent dtype and block size.
+int group_slots_per_wg(int log_block);
+hipError_t launch_block_grouped(const GroupTable& g, int dtype, int log_block, hipStream_t s, bool fwd);
+// bfloat16 jobs of block 2^15 and one layer count on the matrix cores.
+hipError_t launch_mfma15_grouped(const GroupTable& g, int layers, hipStream_t s, bool fwd);
+// Block sums of backward jobs of one latent dtype (prefix in 128-column tiles).
+constexpr int kGroupReduceCols = 128;
+hipError_t launch_reduce_grouped(const GroupTable& g, int dtype, hipStream_t s);
+
+// One generator of a grouped call (validated by the C ABI).
+struct WeightJob {
+  const void* latent;       // [n], ldtype
+  void* weight;             // forward: [size], wdtype
+  const void* grad_weight;  // backward: [size], wdtype
+  void* grad_latent;        // backward: [n], ldtype
+  int64_t n, size;
+  int layers;
+  uint32_t seed32;
+  int ldtype, wdtype;
+  float scale;
+  int accumulate;
+};
+constexpr int64_t kGroupMaxGrid = ((int64_t)1 << 31) - 1;  // workgroups of one grouped launch
+// Whether the grouped kernels take the job (else *why says what is missing).
+bool grouped_job_supported(const WeightJob& j, bool fwd, const char** why);
+// Backward workspace: every job's partial rows, each 256-byte aligned.
+size_t grouped_workspace_bytes(const WeightJob* jobs, int64_t count);
+hipError_t launch_grouped(const WeightJob* jobs, int64_t count, void* work, hipStream_t s, bool fwd);
+
 }  // namespace lwl

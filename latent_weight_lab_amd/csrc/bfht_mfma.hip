@@ -105,6 +105,96 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
   write_partial_row<L, kWhole>(acc, nw, x, lds, partial + slot * (int64_t)n, n, 1.0f);
 }
 
+// ---------------------------------------------------------------- grouped
+
+// The 8 bf16 of a chunk times `scale`, rounded to bf16 (torch's bf16 * scalar).
+__device__ __forceinline__ u32x4 scale_chunk(u32x4 v, float scale) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    v[k] = pk(__uint_as_float(v[k] << 16) * scale, __uint_as_float(v[k] & 0xffff0000u) * scale);
+  return v;
+}
+
+// Whole weight of each job (positions [0, size)): the chain of bfht_mfma15_fwd,
+// the bf16 output times the job's weight scale.
+template <int L>
+__global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd_grouped(const GroupTable g) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  const int j = group_job(g, (int)blockIdx.x);
+  const GroupJob& jb = g.job[j];
+  const int64_t block = (int64_t)blockIdx.x - g.prefix[j];
+  const Ctx x = make_ctx(jb.seed32, block);
+  u32x4 src[kTiles][2];
+  load_latent(x, static_cast<const __bf16*>(jb.src), jb.n, src);
+  f32x16 acc[kTiles];
+  uint32_t nw[4];
+  run_chain<L>(acc, x, lds, src, [](int i) { return i; }, nw);
+  u32x4* stage = reinterpret_cast<u32x4*>(lds + (L & 1) * kXBufBytes);
+  stage_output<L>(acc, nw, x, stage);
+  __syncthreads();
+  const int64_t base = block * kB;
+  const int hi = jb.size - base < kB ? (int)(jb.size - base) : kB;
+  __bf16* oblk = static_cast<__bf16*>(jb.dst) + base;
+  const bool full = hi == kB && (((uintptr_t)oblk & 15) == 0);
+  const auto out_r = rsrc(full ? (const void*)oblk : jb.dst, full ? (uint32_t)(kB * 2) : 0u);
+  uint16_t* oblk16 = reinterpret_cast<uint16_t*>(oblk);
+  const float scale = jb.scale;
+  constexpr int kPer = kChunks / kThreads;
+  u32x4 v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = i * kThreads + (int)threadIdx.x;
+    v[i] = stage[stage_slot(c)];
+    if (scale != 1.0f) v[i] = scale_chunk(v[i], scale);
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int p = (i * kThreads + (int)threadIdx.x) * 8;
+    if (full) {
+      __builtin_amdgcn_raw_buffer_store_b128(v[i], out_r, p * 2, 0, kStreamStore);
+    } else if (p < hi) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (p + e < hi) oblk16[p + e] = (uint16_t)(v[i][e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
+// Per-block partial rows of each job's whole-weight gradient (bf16 weight
+// gradient, as bfht_mfma15_bwd), into the job's partial rows.
+template <int L>
+__global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd_grouped(const GroupTable g) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  const int j = group_job(g, (int)blockIdx.x);
+  const GroupJob& jb = g.job[j];
+  const int64_t slot = (int64_t)blockIdx.x - g.prefix[j];
+  const Ctx x = make_ctx(jb.seed32, slot);
+  const int64_t base = slot * kB;
+  const int hi = jb.size - base < kB ? (int)(jb.size - base) : kB;
+  const __bf16* gblk = static_cast<const __bf16*>(jb.src) + base;
+  const bool full = hi == kB && (((uintptr_t)gblk & 15) == 0);
+  const auto g_r = rsrc(full ? (const void*)gblk : jb.src, full ? (uint32_t)(kB * 2) : 0u);
+  const uint16_t* gblk16 = reinterpret_cast<const uint16_t*>(gblk);
+  u32x4 src[kTiles][2];
+  load_source(
+      x,
+      [&](int p) -> u32x4 {
+        if (full) return __builtin_amdgcn_raw_buffer_load_b128(g_r, p * 2, 0, 0);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (p < hi) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (p + e < hi) v[e >> 1] |= (uint32_t)gblk16[p + e] << (16 * (e & 1));
+        }
+        return v;
+      },
+      src);
+  f32x16 acc[kTiles];
+  uint32_t nw[4];
+  run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
+  write_partial_row<L, false>(acc, nw, x, lds, jb.part + slot * (int64_t)jb.n, jb.n, 1.0f);
+}
+
 }  // namespace
 }  // namespace mfma15
 
@@ -144,6 +234,25 @@ hipError_t launch_mfma15_shape(const BfhtArgs& a, hipStream_t s, bool fwd) {
 }
 
 }  // namespace
+
+hipError_t launch_mfma15_grouped(const GroupTable& g, int layers, hipStream_t s, bool fwd) {
+  using namespace mfma15;
+  if (g.count <= 0 || g.prefix[g.count] == 0) return hipSuccess;
+  const dim3 grid((unsigned)g.prefix[g.count]), block(kThreads);
+#define LWL_GROUPED(L)                                                       \
+  if (fwd)                                                                   \
+    hipLaunchKernelGGL((bfht_mfma15_fwd_grouped<L>), grid, block, 0, s, g); \
+  else                                                                       \
+    hipLaunchKernelGGL((bfht_mfma15_bwd_grouped<L>), grid, block, 0, s, g)
+  switch (layers) {
+    case 1: LWL_GROUPED(1); break;
+    case 2: LWL_GROUPED(2); break;
+    case 3: LWL_GROUPED(3); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef LWL_GROUPED
+  return hipGetLastError();
+}
 
 hipError_t launch_mfma15(const BfhtArgs& a, hipStream_t s, bool fwd) {
   using namespace mfma15;

@@ -139,6 +139,114 @@ def linear_backward_latent(grad2d: torch.Tensor, x2d: torch.Tensor, latent: torc
     return grad_latent
 
 
+def _weight_job(latent: torch.Tensor, size: int, layers: int, seed: int, weight_scale: float,
+                weight_dtype: torch.dtype) -> N.WeightJob:
+    j = N.WeightJob()
+    j.latent = latent.data_ptr()
+    j.latent_size = latent.numel()
+    j.size = int(size)
+    j.layers = int(layers)
+    j.seed = int(seed)
+    j.latent_dtype = N.dtype_code(latent.dtype)
+    j.weight_dtype = N.dtype_code(weight_dtype)
+    j.weight_scale = float(weight_scale)
+    return j
+
+
+def _job_array(jobs: list) -> ctypes.Array:
+    return (N.WeightJob * max(1, len(jobs)))(*jobs)
+
+
+def weight_job_supported(latent: torch.Tensor, size: int, layers: int, weight_dtype: torch.dtype,
+                         grad_weight: torch.Tensor | None = None) -> bool:
+    """Whether the grouped weight-cache kernels take this generator (host-only check;
+    the pointers are not dereferenced).  Without ``grad_weight`` the materialize
+    side is checked, with it the flush side."""
+    if not latent.is_cuda or latent.dtype not in N.DTYPE_CODES or weight_dtype not in N.DTYPE_CODES:
+        return False
+    if not latent.is_contiguous():
+        return False
+    j = _weight_job(latent, size, layers, 0, 1.0, weight_dtype)
+    if grad_weight is None:
+        j.weight = j.latent
+        forward = 1
+    else:
+        if not grad_weight.is_cuda or not grad_weight.is_contiguous() or grad_weight.dtype != weight_dtype:
+            return False
+        j.grad_weight = grad_weight.data_ptr()
+        j.grad_latent = j.latent
+        forward = 0
+    return N.lib().lwl_bfht_check_weight_jobs(_job_array([j]), 1, forward) == N.LWL_OK
+
+
+def materialize_weights(specs: list[tuple]) -> list[torch.Tensor]:
+    """Generate whole weights of many generators in a few launches (the per-module
+    ``materialize_weight_cache`` calls of the reference's ``prepare_block_fht_weight_cache``,
+    ``block_fht.py:503-563``).
+
+    ``specs``: ``(latent, size, layers, seed, weight_scale, weight_dtype)`` per generator.
+    Returns flat weights equal to ``(generate(latent) * weight_scale).to(weight_dtype)``.
+    """
+    if not specs:
+        return []
+    dev = N.require_cuda(*[s[0] for s in specs])
+    jobs, outs, keep = [], [], []
+    for latent, size, layers, seed, weight_scale, weight_dtype in specs:
+        latent = latent.detach().contiguous()
+        out = torch.empty(int(size), dtype=weight_dtype, device=dev)
+        j = _weight_job(latent, size, layers, seed, weight_scale, weight_dtype)
+        j.weight = out.data_ptr()
+        jobs.append(j)
+        outs.append(out)
+        keep.append(latent)
+    L = N.lib()
+    arr = _job_array(jobs)
+    with _device_guard(dev):
+        N.check(L.lwl_bfht_materialize_weights(arr, len(jobs), N.stream_ptr(dev)))
+    return outs
+
+
+def flush_weight_grads(specs: list[tuple]) -> list[torch.Tensor]:
+    """Project many weight gradients back onto their latents in a few launches (the
+    per-module ``flush_weight_cache_to_latent_grad`` calls of the reference's
+    ``flush_block_fht_weight_cache``, ``block_fht.py:514-569``).
+
+    ``specs``: ``(latent, grad_weight, size, layers, seed, weight_scale, into)`` per
+    generator; ``into`` is None or a contiguous tensor of the latent's shape and dtype
+    that the result is added to in place (``latent.grad.add_``).  Returns, per spec,
+    ``into`` or a new tensor holding ``weight_scale * block_fht_grad_latent(latent,
+    grad_weight.to(latent.dtype), ...)``.
+    """
+    if not specs:
+        return []
+    dev = N.require_cuda(*[s[1] for s in specs])
+    jobs, outs, keep = [], [], []
+    for latent, grad_weight, size, layers, seed, weight_scale, into in specs:
+        grad_weight = grad_weight.detach().contiguous()
+        if grad_weight.numel() != size:
+            raise N.BlockFHTArgumentError(f"grad_weight has {grad_weight.numel()} elements, size is {size}")
+        if into is None:
+            out = torch.empty(latent.numel(), dtype=latent.dtype, device=dev)
+        else:
+            if into.dtype != latent.dtype or into.numel() != latent.numel() or not into.is_contiguous():
+                raise N.BlockFHTArgumentError("accumulation target must be a contiguous tensor like the latent")
+            out = into
+        j = _weight_job(latent, size, layers, seed, weight_scale, grad_weight.dtype)
+        j.grad_weight = grad_weight.data_ptr()
+        j.grad_latent = out.data_ptr()
+        j.accumulate = int(into is not None)
+        jobs.append(j)
+        outs.append(out)
+        keep.append(grad_weight)
+    L = N.lib()
+    arr = _job_array(jobs)
+    with _device_guard(dev):
+        ws_ptr, ws_size, ws = N.workspace(L.lwl_bfht_flush_weight_grads_workspace_size(arr, len(jobs)), dev)
+        N.check(L.lwl_bfht_flush_weight_grads(arr, len(jobs), ws_ptr, ws_size, N.stream_ptr(dev)))
+    del ws, keep
+    return outs
+
+
 def sign_words(seed: int, block: int, layer: int, nwords: int, first_word: int = 0,
                device: torch.device | str = "cuda") -> torch.Tensor:
     """Sign words computed by the device hash (int32 tensor holding the uint32 bits)."""

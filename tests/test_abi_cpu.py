@@ -200,3 +200,77 @@ def test_linear_backward_latent_workspace_size():
     lib = N.lib()
     assert lib.lwl_bfht_linear_backward_latent_workspace_size(4096, 768, 3072, 32768) == (
         216 * 32768 * 4 + 48 * 128 * 1024 + 3072 * 4096 * 2)
+
+
+def weight_job(n, size, ld=0, wd=0, layers=2, ptr=0x10000, **kw):
+    j = N.WeightJob()
+    j.latent = j.weight = j.grad_weight = j.grad_latent = ptr
+    j.latent_size, j.size, j.layers, j.seed = n, size, layers, 1
+    j.latent_dtype, j.weight_dtype, j.weight_scale = ld, wd, 1.0
+    for k, v in kw.items():
+        setattr(j, k, v)
+    return j
+
+
+def check_jobs(jobs, forward=1):
+    arr = (N.WeightJob * max(1, len(jobs)))(*jobs)
+    rc = N.lib().lwl_bfht_check_weight_jobs(arr, len(jobs), forward)
+    return rc, N.lib().lwl_last_error().decode()
+
+
+def test_weight_job_struct_matches_header():
+    # ctypes mirror of lwl_bfht_weight_job: 4 pointers, 4 int64, 2 int32, double, int32
+    assert N.WeightJob.weight_scale.offset == 72 and N.WeightJob.accumulate.offset == 80
+    assert ctypes_sizeof(N.WeightJob) == 88
+
+
+def ctypes_sizeof(t):
+    import ctypes
+
+    return ctypes.sizeof(t)
+
+
+@pytest.mark.parametrize(
+    "jobs, forward, code, msg",
+    [
+        ([], 1, N.LWL_OK, ""),
+        ([weight_job(23593, 768 * 3072, ld=0, wd=2)], 1, N.LWL_OK, ""),
+        ([weight_job(32768, 1 << 20, ld=2, wd=2)], 0, N.LWL_OK, ""),
+        ([weight_job(32769, 1 << 20)], 1, N.LWL_ERR_UNSUPPORTED, "blocks up to 2^15"),
+        # bf16 latent of block 2^15 (matrix cores) cached as float32: per-module path
+        ([weight_job(32768, 1 << 20, ld=2, wd=0)], 1, N.LWL_ERR_UNSUPPORTED, "need a bfloat16 weight"),
+        # ... unless the source is not 16-byte aligned (the per-module call then uses the block kernel)
+        ([weight_job(32768, 1 << 20, ld=2, wd=0, ptr=0x10002)], 1, N.LWL_OK, ""),
+        ([weight_job(100, 1000, layers=4)], 1, N.LWL_ERR_INVALID, "layers must be 1, 2, or 3"),
+        ([weight_job(100, 1000, wd=7)], 1, N.LWL_ERR_UNSUPPORTED, "weight dtype code 7"),
+        ([weight_job(100, 0)], 1, N.LWL_ERR_INVALID, "size must be positive"),
+        ([weight_job(100, 1000, weight=None)], 1, N.LWL_ERR_INVALID, "latent and weight must be non-null"),
+        ([weight_job(100, 1000, grad_latent=None)], 0, N.LWL_ERR_INVALID, "grad_weight and grad_latent"),
+        # destinations: weights [0x10000, +4000) and [0x10f00, ...) overlap
+        ([weight_job(100, 1000), weight_job(100, 1000, weight=0x10f00)], 1, N.LWL_ERR_INVALID,
+         "jobs 0 and 1 write overlapping memory"),
+        ([weight_job(100, 1000), weight_job(100, 1000, weight=0x10000 + 4000)], 1, N.LWL_OK, ""),
+        # flush destinations are the latent gradients (100 floats)
+        ([weight_job(100, 1000), weight_job(100, 1000, grad_latent=0x10000 + 396)], 0, N.LWL_ERR_INVALID,
+         "overlapping"),
+    ],
+)
+def test_weight_job_validation(jobs, forward, code, msg):
+    rc, err = check_jobs(jobs, forward)
+    assert rc == code, err
+    assert msg in err
+
+
+def test_flush_workspace_size():
+    jobs = [weight_job(23593, 768 * 3072, ptr=1 << 20), weight_job(5898, 768 * 768, ptr=2 << 20),
+            weight_job(3, 7, ptr=3 << 20)]
+    arr = (N.WeightJob * 3)(*jobs)
+    got = N.lib().lwl_bfht_flush_weight_grads_workspace_size(arr, 3)
+
+    def al(v):
+        return (v + 255) // 256 * 256
+
+    # one float32 partial row of n per block, per job, 256-byte aligned
+    assert got == al(72 * 23593 * 4) + al(72 * 5898 * 4) + al(2 * 3 * 4)
+    bad = (N.WeightJob * 1)(weight_job(40000, 100))
+    assert N.lib().lwl_bfht_flush_weight_grads_workspace_size(bad, 1) == 0

@@ -1,0 +1,192 @@
+"""GPU parity of the grouped weight cache: prepare / flush of many BlockFHTLinear
+modules in a few launches (reference latent_weight_lab/block_fht.py:503-569, whose
+loops call ext.forward / ext.backward once per module).
+
+The grouped kernels run every block with the code of the per-module launch, and
+fold in torch's ``* weight_scale``, ``.to(dtype)`` and ``latent.grad.add_`` with
+the same roundings, so the bar is bit-identity (``torch.equal``) with the
+per-module path; one job per dtype is also checked against the C oracle
+(float32 1e-5, bf16 / fp16 1e-2 relative L2, as the per-module tests).
+"""
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from conftest import gpu_available
+from latent_weight_lab_amd import (BlockFHTLinear, block_fht_grad_latent, flush_block_fht_weight_cache,
+                                   prepare_block_fht_weight_cache)
+from latent_weight_lab_amd import ops
+from oracle import c_oracle
+from oracle import oracle as O
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
+
+F32, F16, BF16 = torch.float32, torch.float16, torch.bfloat16
+
+# (latent size, size, layers, seed, weight_scale, latent dtype, weight dtype)
+JOBS = [
+    (23593, 768 * 3072, 2, 1000, 1.0, F32, BF16),     # GPT-2 MLP at latent ratio 0.01: block 2^15, fp32 latent
+    (5898, 768 * 768, 2, 1001, 0.25, F32, BF16),      # block 2^13, one block per workgroup
+    (17694, 768 * 2304, 3, 1002, 1.0, F32, F32),      # fp32 cache
+    (32768, 1024 * 1024, 3, 7, 0.5, BF16, BF16),      # bf16 block 2^15: matrix cores, scaled
+    (20000, 300 * 1000, 2, 8, 1.0, BF16, BF16),       # matrix cores, padded latent, partial last block
+    (3000, 64 * 500, 1, 9, 2.0, F16, F32),            # fp16 latent, block 2^12 (2 blocks per workgroup)
+    (10, 7 * 33, 3, -4, 1.0, F32, F16),               # block 2^4 (256 blocks per workgroup), partial
+    (1, 5, 2, 3, 1.5, F32, F32),                      # one-element latent, block 2^0
+    (4096, 4096, 3, 11, 1.0, BF16, F32),              # bf16 latent, block 2^12, fp32 cache
+]
+
+
+def make_latent(n, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(n, generator=g) * 0.02).to(dtype).cuda()
+
+
+def per_module_weight(latent, size, layers, seed, ws, wdtype):
+    return (ops.forward(latent, size, layers, seed, 0, size) * ws).to(wdtype)
+
+
+def test_materialize_matches_per_module_bitwise():
+    latents = [make_latent(n, ld, i) for i, (n, _, _, _, _, ld, _) in enumerate(JOBS)]
+    specs = [(lat, size, layers, seed, ws, wd) for lat, (_, size, layers, seed, ws, _, wd) in zip(latents, JOBS)]
+    got = ops.materialize_weights(specs)
+    torch.cuda.synchronize()
+    for spec, w in zip(specs, got):
+        want = per_module_weight(*spec)
+        assert w.dtype == want.dtype and w.shape == want.shape
+        assert torch.equal(w, want), spec[1:]
+
+
+@pytest.mark.parametrize("ld,tol", [(F32, 1e-5), (BF16, 1e-2), (F16, 1e-2)])
+def test_materialize_matches_oracle(ld, tol):
+    n, size, layers, seed, ws = 30000, 200 * 700, 3, 17, 0.5
+    lat = make_latent(n, ld, 5)
+    (w,) = ops.materialize_weights([(lat, size, layers, seed, ws, ld)])
+    want = ws * c_oracle.forward(lat.double().cpu().numpy(), size, layers, seed, 0, size)
+    assert O.rel_l2(w.double().cpu().numpy(), want) < tol
+
+
+def test_flush_matches_per_module_bitwise():
+    latents = [make_latent(n, ld, 50 + i) for i, (n, _, _, _, _, ld, _) in enumerate(JOBS)]
+    grads = []
+    for i, (n, size, *_rest, wd) in enumerate(JOBS):
+        g = torch.Generator().manual_seed(100 + i)
+        grads.append(torch.randn(size, generator=g).to(wd).cuda())
+    # half the jobs add into an existing gradient
+    intos = [None if i % 2 else (torch.randn(lat.numel()) * 0.1).to(lat.dtype).cuda()
+             for i, lat in enumerate(latents)]
+    before = [None if t is None else t.clone() for t in intos]
+    specs = [(lat, gw, size, layers, seed, ws, into)
+             for lat, gw, into, (_, size, layers, seed, ws, _, _) in zip(latents, grads, intos, JOBS)]
+    got = ops.flush_weight_grads(specs)
+    torch.cuda.synchronize()
+    for i, ((lat, gw, size, layers, seed, ws, into), r) in enumerate(zip(specs, got)):
+        want = ws * block_fht_grad_latent(lat, gw.to(lat.dtype), size, layers, seed)
+        if before[i] is not None:
+            want = before[i].add_(want)
+            assert r.data_ptr() == into.data_ptr()
+        assert r.dtype == lat.dtype
+        assert torch.equal(r, want), JOBS[i]
+
+
+@pytest.mark.parametrize("ld,tol", [(F32, 1e-5), (BF16, 1e-2)])
+def test_flush_matches_oracle(ld, tol):
+    n, size, layers, seed, ws = 30000, 200 * 700, 2, 23, 2.0
+    lat = make_latent(n, ld, 6)
+    gw = torch.randn(size, generator=torch.Generator().manual_seed(7)).to(ld).cuda()
+    (r,) = ops.flush_weight_grads([(lat, gw, size, layers, seed, ws, None)])
+    want = ws * c_oracle.backward(gw.double().cpu().numpy(), n, size, layers, seed, 0, size)
+    assert O.rel_l2(r.double().cpu().numpy(), want) < tol
+
+
+def test_more_jobs_than_one_table():
+    # 40 generators: the planner splits them over two launch tables
+    specs, lats = [], []
+    for i in range(40):
+        n = 100 + 37 * i
+        lat = make_latent(n, F32, 200 + i)
+        lats.append(lat)
+        specs.append((lat, 3 * n + i, 1 + i % 3, i, 1.0, F32))
+    got = ops.materialize_weights(specs)
+    grads = [torch.randn_like(w) for w in got]
+    flushed = ops.flush_weight_grads([(lat, g, s[1], s[2], s[3], 1.0, None)
+                                      for lat, g, s in zip(lats, grads, specs)])
+    torch.cuda.synchronize()
+    for s, w, g, r in zip(specs, got, grads, flushed):
+        assert torch.equal(w, per_module_weight(*s))
+        assert torch.equal(r, block_fht_grad_latent(s[0], g, s[1], s[2], s[3]))
+
+
+class Net(torch.nn.Module):
+    """Modules of every cache kind: plain fp32 latents (grouped, cast to bf16),
+    gains and modulation (grouped with torch epilogues), a residual base (never
+    cached), and a latent above 2^15 (per-module tile path)."""
+
+    def __init__(self):
+        super().__init__()
+        self.qkv = BlockFHTLinear(768, 2304, latent_ratio=0.01, layers=2, seed=1, weight_scale=0.5)
+        self.fc = BlockFHTLinear(768, 3072, latent_ratio=0.01, layers=2, seed=2)
+        self.proj = BlockFHTLinear(3072, 768, latent_ratio=0.01, layers=2, seed=3, output_gain=True,
+                                   input_gain=True)
+        self.mod = BlockFHTLinear(256, 512, latent_ratio=0.05, layers=3, seed=4, modulation_alpha=0.1)
+        self.res = BlockFHTLinear(256, 256, latent_ratio=0.05, layers=1, seed=5, residual_base_scale=0.5)
+        self.big = BlockFHTLinear(1024, 1024, latent_dim=50000, layers=2, seed=6)
+
+    def forward(self, x, y, z):
+        h = self.qkv(x).float().sum() + self.fc(x).float().sum() * 0.5
+        h = h + self.proj(y).float().pow(2).sum() * 1e-3
+        h = h + self.mod(z).float().sum() + self.res(z).float().sum() + self.big(
+            torch.cat([z, z, z, z], dim=-1)).float().sum()
+        return h
+
+
+def per_module_prepare(model, dtype):
+    for m in model.modules():
+        if isinstance(m, BlockFHTLinear):
+            m.materialize_weight_cache(dtype=dtype)
+
+
+def per_module_flush(model):
+    for m in model.modules():
+        if isinstance(m, BlockFHTLinear):
+            m.flush_weight_cache_to_latent_grad()
+
+
+@pytest.mark.parametrize("cache_dtype", [BF16, None])
+def test_model_prepare_flush_matches_per_module(cache_dtype):
+    torch.manual_seed(0)
+    a = Net().cuda()
+    with torch.no_grad():
+        for m in a.modules():
+            if isinstance(m, BlockFHTLinear) and m.output_gain is not None:
+                m.output_gain.uniform_(0.5, 1.5)
+                m.input_gain.uniform_(0.5, 1.5)
+    b = copy.deepcopy(a)
+    x = torch.randn(8, 768, device="cuda")
+    y = torch.randn(8, 3072, device="cuda")
+    z = torch.randn(8, 256, device="cuda")
+    # a: grouped helpers; b: the per-module loop; two microbatches each, the
+    # second flush adding into the gradients of the first
+    for step in range(2):
+        prepare_block_fht_weight_cache(a, dtype=cache_dtype)
+        per_module_prepare(b, cache_dtype)
+        for (na, ma), (nb, mb) in zip(a.named_modules(), b.named_modules()):
+            if isinstance(ma, BlockFHTLinear):
+                assert (ma._cached_weight is None) == (mb._cached_weight is None), na
+                if ma._cached_weight is not None:
+                    assert torch.equal(ma._cached_weight, mb._cached_weight), na
+        cast = (lambda t: t.to(cache_dtype)) if cache_dtype is not None else (lambda t: t)
+        a(cast(x), cast(y), cast(z)).backward()
+        b(cast(x), cast(y), cast(z)).backward()
+        flush_block_fht_weight_cache(a)
+        per_module_flush(b)
+        for (na, pa), (nb, pb) in zip(a.named_parameters(), b.named_parameters()):
+            assert (pa.grad is None) == (pb.grad is None), na
+            if pa.grad is not None:
+                assert torch.equal(pa.grad, pb.grad), (step, na)
+    for m in a.modules():
+        if isinstance(m, BlockFHTLinear):
+            assert m._cached_weight is None
