@@ -361,6 +361,14 @@ def extra_configs(abi, steps, warmup, only):
         except Exception as exc:  # noqa: BLE001
             res["c6_cache"] = {"error": f"{type(exc).__name__}: {exc}"}
 
+    # many small generators (nanoGPT HeadwiseLinear / GroupedInputLinear): one training step (forward +
+    # backward) of all heads batched into one grouped generation vs head by head
+    if want("c7_heads"):
+        try:
+            res["c7_heads"] = heads_bench(torch)
+        except Exception as exc:  # noqa: BLE001
+            res["c7_heads"] = {"error": f"{type(exc).__name__}: {exc}"}
+
     # config 5: 12-layer GPT-2-small linear stack (qkv, proj, fc, fc-proj per layer = 48 matrices,
     # latents of 32768 bf16, seeds 100+i), forward only, fused vs dense on materialized weights
     if want("c5_stack"):
@@ -422,6 +430,43 @@ def stack_bench(abi, torch):
         except Exception as exc:  # noqa: BLE001
             row["error"] = f"{type(exc).__name__}: {exc}"
         out[f"tokens_{tokens}"] = row
+    return out
+
+
+def heads_bench(torch):
+    from latent_weight_lab_amd import BlockFHTLinear, block_fht_grouped_input_linear, block_fht_headwise_linear
+
+    out = {}
+    cases = {
+        # attention k projection per head (attn.c_attn.k_headwise): 12 x (768 -> 64), latent 492, block 2^9
+        "headwise_12x768x64": (block_fht_headwise_linear, 12, 768, 64, 768),
+        # MLP c_proj in 4 input groups (mlp.c_proj grouped): 4 x (768 -> 768), latent 5898, block 2^13
+        "grouped_input_4x768x768": (block_fht_grouped_input_linear, 4, 768, 768, 4 * 768),
+    }
+    for name, (fn, nh, inf, outf, xin) in cases.items():
+        torch.manual_seed(0)
+        heads = [BlockFHTLinear(inf, outf, latent_ratio=0.01, layers=2, seed=1000 + i).cuda() for i in range(nh)]
+        x = torch.randn(8 * 1024, xin, device="cuda").to(torch.bfloat16).requires_grad_(True)
+
+        def per_head():
+            if fn is block_fht_headwise_linear:
+                y = torch.cat([h(x) for h in heads], dim=-1)
+            else:
+                pieces = x.split(inf, dim=-1)
+                y = heads[0](pieces[0])
+                for p, h in zip(pieces[1:], heads[1:]):
+                    y = y + h(p)
+            y.float().sum().backward()
+
+        def batched():
+            fn(x, heads).float().sum().backward()
+
+        row = {"tokens": 8 * 1024, "heads": nh, "latent": heads[0].generator.latent.numel()}
+        for tag, f in (("batched", batched), ("per_head", per_head)):
+            row[tag + "_ms"] = round(time_eager(torch, f, 20, 3) * 1e3, 4)
+        row["speedup"] = row["per_head_ms"] / row["batched_ms"]
+        out[name] = row
+        del heads, x
     return out
 
 

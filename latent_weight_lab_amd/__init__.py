@@ -20,11 +20,14 @@ from .block_fht import (
     signs_for,
     suspend_block_fht_weight_cache,
 )
+from .batched import block_fht_grouped_input_linear, block_fht_headwise_linear
 
 __all__ = [
     "BlockFHT",
     "BlockFHTLinear",
     "block_fht_grad_latent",
+    "block_fht_grouped_input_linear",
+    "block_fht_headwise_linear",
     "block_fht_linear_forward",
     "block_fht_slice",
     "flush_block_fht_weight_cache",

@@ -179,31 +179,40 @@ def weight_job_supported(latent: torch.Tensor, size: int, layers: int, weight_dt
     return N.lib().lwl_bfht_check_weight_jobs(_job_array([j]), 1, forward) == N.LWL_OK
 
 
-def materialize_weights(specs: list[tuple]) -> list[torch.Tensor]:
+def materialize_weights(specs: list[tuple], outs: list[torch.Tensor] | None = None) -> list[torch.Tensor]:
     """Generate whole weights of many generators in a few launches (the per-module
     ``materialize_weight_cache`` calls of the reference's ``prepare_block_fht_weight_cache``,
     ``block_fht.py:503-563``).
 
     ``specs``: ``(latent, size, layers, seed, weight_scale, weight_dtype)`` per generator.
-    Returns flat weights equal to ``(generate(latent) * weight_scale).to(weight_dtype)``.
+    Returns flat weights equal to ``(generate(latent) * weight_scale).to(weight_dtype)``,
+    written into ``outs`` (contiguous, ``size`` elements of ``weight_dtype`` each) when given.
     """
     if not specs:
         return []
     dev = N.require_cuda(*[s[0] for s in specs])
-    jobs, outs, keep = [], [], []
-    for latent, size, layers, seed, weight_scale, weight_dtype in specs:
+    if outs is not None and len(outs) != len(specs):
+        raise N.BlockFHTArgumentError("outs must match specs")
+    jobs, result, keep = [], [], []
+    for i, (latent, size, layers, seed, weight_scale, weight_dtype) in enumerate(specs):
         latent = latent.detach().contiguous()
-        out = torch.empty(int(size), dtype=weight_dtype, device=dev)
+        if outs is None:
+            out = torch.empty(int(size), dtype=weight_dtype, device=dev)
+        else:
+            out = outs[i]
+            if (out.dtype != weight_dtype or out.numel() != int(size) or not out.is_contiguous()
+                    or out.device != dev):
+                raise N.BlockFHTArgumentError(f"output {i} must be a contiguous {weight_dtype} tensor of {size}")
         j = _weight_job(latent, size, layers, seed, weight_scale, weight_dtype)
         j.weight = out.data_ptr()
         jobs.append(j)
-        outs.append(out)
+        result.append(out)
         keep.append(latent)
     L = N.lib()
     arr = _job_array(jobs)
     with _device_guard(dev):
         N.check(L.lwl_bfht_materialize_weights(arr, len(jobs), N.stream_ptr(dev)))
-    return outs
+    return result
 
 
 def flush_weight_grads(specs: list[tuple]) -> list[torch.Tensor]:

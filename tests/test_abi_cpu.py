@@ -274,3 +274,13 @@ def test_flush_workspace_size():
     assert got == al(72 * 23593 * 4) + al(72 * 5898 * 4) + al(2 * 3 * 4)
     bad = (N.WeightJob * 1)(weight_job(40000, 100))
     assert N.lib().lwl_bfht_flush_weight_grads_workspace_size(bad, 1) == 0
+
+
+def test_batched_linears_fail_loudly_on_cpu():
+    from latent_weight_lab_amd import BlockFHTLinear, block_fht_grouped_input_linear, block_fht_headwise_linear
+
+    heads = [BlockFHTLinear(8, 4, latent_dim=8, layers=1, seed=i) for i in range(2)]
+    with pytest.raises(RuntimeError, match="GPU only"):
+        block_fht_headwise_linear(torch.zeros(3, 8), heads)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        block_fht_grouped_input_linear(torch.zeros(3, 16), heads)
