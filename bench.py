@@ -369,6 +369,14 @@ def extra_configs(abi, steps, warmup, only):
         except Exception as exc:  # noqa: BLE001
             res["c7_heads"] = {"error": f"{type(exc).__name__}: {exc}"}
 
+    # signed activation FHT (nanoGPT FixedFHTMix) on 8192 bf16 rows: one launch vs the reference's
+    # torch loop (pad, sign, log2(P) reshape/clone butterfly stages, scale, sign, slice) on this GPU
+    if want("c8_mix"):
+        try:
+            res["c8_mix"] = mix_bench(torch)
+        except Exception as exc:  # noqa: BLE001
+            res["c8_mix"] = {"error": f"{type(exc).__name__}: {exc}"}
+
     # config 5: 12-layer GPT-2-small linear stack (qkv, proj, fc, fc-proj per layer = 48 matrices,
     # latents of 32768 bf16, seeds 100+i), forward only, fused vs dense on materialized weights
     if want("c5_stack"):
@@ -431,6 +439,44 @@ def stack_bench(abi, torch):
             row["error"] = f"{type(exc).__name__}: {exc}"
         out[f"tokens_{tokens}"] = row
     return out
+
+
+def mix_bench(torch):
+    from latent_weight_lab_amd import ops
+
+    def torch_mix(x, signs):  # the reference's FixedFHTMix.forward, op for op
+        features = x.shape[-1]
+        padded = signs.numel()
+        if padded != features:
+            x = torch.nn.functional.pad(x, (0, padded - features))
+        out = x * signs.to(dtype=x.dtype)
+        step = 1
+        while step < padded:
+            shape = out.shape
+            out = out.reshape(*shape[:-1], -1, 2, step)
+            first = out[..., 0, :].clone()
+            second = out[..., 1, :].clone()
+            out[..., 0, :] = first + second
+            out[..., 1, :] = first - second
+            out = out.reshape(shape)
+            step *= 2
+        out = out / math.sqrt(padded)
+        return (out * signs.to(dtype=x.dtype))[..., :features]
+
+    res = {}
+    for features in (768, 3072):
+        padded = 1 << (features - 1).bit_length()
+        signs = (torch.randint(0, 2, (padded,), generator=torch.Generator().manual_seed(1),
+                               dtype=torch.float32) * 2.0 - 1.0).cuda()
+        x = torch.randn(8192, features, device="cuda").to(torch.bfloat16)
+        out = torch.empty_like(x)
+        nbytes = 2 * x.numel() * 2
+        k = time_graph(torch, lambda: ops.fht_mix(x, signs, out=out), 50, 5)
+        t = time_graph(torch, lambda: torch_mix(x, signs), 10, 2)
+        res[f"8192x{features}"] = {"kernel_ms": round(k * 1e3, 5), "kernel_algo_GBs": nbytes / k / 1e9,
+                                   "kernel_hbm_frac": nbytes / k / 1e9 / HBM_PEAK_GBS,
+                                   "torch_reference_ms": round(t * 1e3, 4), "speedup": t / k}
+    return res
 
 
 def heads_bench(torch):

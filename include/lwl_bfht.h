@@ -195,6 +195,24 @@ size_t lwl_bfht_flush_weight_grads_workspace_size(const lwl_bfht_weight_job* job
 int lwl_bfht_flush_weight_grads(const lwl_bfht_weight_job* jobs, int64_t count, void* workspace,
                                 size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------- signed activation FHT
+ * Replaces FixedFHTMix.forward (reference examples/nanogpt/model.py:200-218,
+ * normalized_fht_last_dim :180-197), a torch loop of log2(P) reshape/clone
+ * stages.  For each of `rows` rows of `features` values (row-major, contiguous):
+ *
+ *   out[row] = (S H S pad(x[row]))[:features]
+ *
+ * P = next power of two >= features (<= 32768), pad appends zeros, S =
+ * diag(signs) with signs[P] = ±1.0f (the module's buffer, on the device), H the
+ * Sylvester Walsh-Hadamard transform divided by sqrt(P).  float32 arithmetic,
+ * one rounding to `dtype` at the end.  S H S is symmetric, so the backward is
+ * the same call on the output gradient.  out may equal x (in place).
+ */
+int lwl_fht_mix(const void* x, int dtype, int64_t rows, int64_t features, const float* signs, void* out,
+                void* stream);
+/* Host-only argument check of lwl_fht_mix. */
+int lwl_fht_check_mix(int dtype, int64_t rows, int64_t features);
+
 /* ---------------------------------------------------------------- sign words
  * Parity probe for the device hash (reference device functions
  * csrc/block_fht_ext_cuda.cu:27-43; Python twin block_fht.py:36-52):

@@ -21,15 +21,18 @@ from .block_fht import (
     suspend_block_fht_weight_cache,
 )
 from .batched import block_fht_grouped_input_linear, block_fht_headwise_linear
+from .mix import FixedFHTMix, fixed_fht_mix
 
 __all__ = [
     "BlockFHT",
     "BlockFHTLinear",
+    "FixedFHTMix",
     "block_fht_grad_latent",
     "block_fht_grouped_input_linear",
     "block_fht_headwise_linear",
     "block_fht_linear_forward",
     "block_fht_slice",
+    "fixed_fht_mix",
     "flush_block_fht_weight_cache",
     "lowbias32",
     "next_power_of_two",

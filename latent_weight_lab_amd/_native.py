@@ -88,6 +88,8 @@ def _bind(lib) -> None:
         "lwl_bfht_materialize_weights": (i32, [jobp, i64, vp]),
         "lwl_bfht_flush_weight_grads_workspace_size": (sz, [jobp, i64]),
         "lwl_bfht_flush_weight_grads": (i32, [jobp, i64, vp, sz, vp]),
+        "lwl_fht_mix": (i32, [vp, i32, i64, i64, vp, vp, vp]),
+        "lwl_fht_check_mix": (i32, [i32, i64, i64]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)

@@ -420,6 +420,28 @@ int lwl_bfht_flush_weight_grads(const lwl_bfht_weight_job* jobs, int64_t count, 
                     "lwl_bfht_flush_weight_grads");
 }
 
+int lwl_fht_check_mix(int dtype, int64_t rows, int64_t features) {
+  if (!valid_dtype(dtype))
+    return fail(LWL_ERR_UNSUPPORTED, "FHT mix supports float32, float16 and bfloat16 (dtype code %d)", dtype);
+  if (rows < 0) return fail(LWL_ERR_INVALID, "rows must be non-negative");
+  if (features <= 0) return fail(LWL_ERR_INVALID, "features must be positive");
+  if (features > ((int64_t)1 << lwl::kWholeBlockMaxLog))
+    return fail(LWL_ERR_UNSUPPORTED, "FHT mix supports up to 32768 features (got %lld)", (long long)features);
+  if (rows > ((int64_t)1 << 40)) return fail(LWL_ERR_UNSUPPORTED, "too many rows");
+  return ok();
+}
+
+int lwl_fht_mix(const void* x, int dtype, int64_t rows, int64_t features, const float* signs, void* out,
+                void* stream) {
+  const int rc = lwl_fht_check_mix(dtype, rows, features);
+  if (rc) return rc;
+  if (rows == 0) return ok();
+  if (!x || !signs || !out) return fail(LWL_ERR_INVALID, "x, signs and out must be non-null");
+  return hip_status(lwl::launch_fht_mix(dtype, x, out, signs, rows, features, log2_pow2_ceil(features),
+                                        (hipStream_t)stream),
+                    "lwl_fht_mix");
+}
+
 int lwl_bfht_sign_words(int64_t seed, int64_t block, int64_t layer, int64_t first_word,
                         int64_t nwords, uint32_t* out, void* stream) {
   if (nwords < 0 || first_word < 0 || (nwords > 0 && !out))

@@ -156,4 +156,79 @@ __device__ __forceinline__ void fht_unnormalized(float (&v)[1 << LE], float* lds
   }
 }
 
+// Full unnormalized transform of an LB-bit block held in the coalesced layout
+// (thread t, register r holds position r * 2^(LB-LE) + t, so a warp's lanes
+// touch consecutive positions for every register), left in the same layout.
+// The registers already span the top LE bits, so the transform starts there and
+// needs one LDS exchange per remaining group of up to 5 bits plus one back to
+// the coalesced layout.  All threads of the workgroup must call it.
+template <int LB, int LE>
+__device__ __forceinline__ void fht_coalesced(float (&v)[1 << LE], float* lds, int t) {
+  constexpr int E = 1 << LE;
+  constexpr int TOP = LB - LE;  // position bits [TOP, LB) are the register bits
+  butterflies<E>(v, LE);
+  if constexpr (TOP > 0) {
+    constexpr int NR = (TOP + 4) / 5;
+    int lo_cur = TOP, nb_cur = LE;
+#pragma unroll
+    for (int g = 0; g < NR; ++g) {
+      const int lo = 5 * g, nb = (TOP - lo < 5) ? TOP - lo : 5;
+      const int wb = group_base<LB, LE>(t, lo_cur, nb_cur);
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, lo_cur, nb_cur)] = v[r];
+      __syncthreads();
+      const int rb = group_base<LB, LE>(t, lo, nb);
+#pragma unroll
+      for (int r = 0; r < E; ++r) v[r] = lds[group_lds<LB, LE>(rb, r, lo, nb)];
+      butterflies<E>(v, nb);
+      lo_cur = lo;
+      nb_cur = nb;
+    }
+    const int wb = group_base<LB, LE>(t, lo_cur, nb_cur);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, lo_cur, nb_cur)] = v[r];
+    __syncthreads();
+    const int rb = group_base<LB, LE>(t, TOP, LE);
+#pragma unroll
+    for (int r = 0; r < E; ++r) v[r] = lds[group_lds<LB, LE>(rb, r, TOP, LE)];
+  }
+}
+
+// Geometry of the whole-block VALU kernels: a block of 2^LB values is held by
+// TB threads with E = 2^LE values each (contiguous runs: thread t holds
+// positions t*E .. t*E+E-1); a workgroup of WG threads holds G blocks, each
+// with its own lds_index-padded LDS copy for the group exchanges.
+template <int LB>
+struct Geo {
+  static constexpr int LE = LB < 5 ? LB : 5;  // log2 elements per thread
+  static constexpr int E = 1 << LE;
+  static constexpr int LT = LB - LE;          // log2 threads per block
+  static constexpr int TB = 1 << LT;
+  static constexpr int WG = TB < 256 ? 256 : TB;
+  static constexpr int G = WG / TB;           // blocks per workgroup
+  static constexpr int B = 1 << LB;
+  static constexpr int NG = (LB + 4) / 5;
+  static constexpr int PADDED = B + (B >> 5);
+  static constexpr int LDS_FLOATS = NG > 1 ? G * PADDED : 1;
+  // padded LDS index of position k * TB + t (coalesced order) and of t * E + r
+  // (a thread's own run), written so that the compiler sees a per-thread base
+  // plus a constant per k or r
+  __device__ static int coal(int t, int k) {
+    if constexpr (TB % 32 == 0) return t + (t >> 5) + k * (TB + TB / 32);
+    else return lds_index(k * TB + t);
+  }
+  __device__ static int own(int t, int r) {
+    if constexpr (E == 32) return t * 33 + r;
+    else return lds_index(t * E + r);
+  }
+};
+
+template <int LB>
+__device__ __forceinline__ float inv_sqrt_block() {
+  // 2^(-LB/2), exact for even LB
+  return (LB & 1) ? 0.70710678118654752440f / (float)(1 << (LB >> 1)) : 1.0f / (float)(1 << (LB >> 1));
+}
+
 }  // namespace lwl

@@ -21,37 +21,6 @@
 
 namespace lwl {
 
-template <int LB>
-struct Geo {
-  static constexpr int LE = LB < 5 ? LB : 5;  // log2 elements per thread
-  static constexpr int E = 1 << LE;
-  static constexpr int LT = LB - LE;          // log2 threads per block
-  static constexpr int TB = 1 << LT;
-  static constexpr int WG = TB < 256 ? 256 : TB;
-  static constexpr int G = WG / TB;           // blocks per workgroup
-  static constexpr int B = 1 << LB;
-  static constexpr int NG = (LB + 4) / 5;
-  static constexpr int PADDED = B + (B >> 5);
-  static constexpr int LDS_FLOATS = NG > 1 ? G * PADDED : 1;
-  // padded LDS index of position k * TB + t (coalesced order) and of t * E + r
-  // (a thread's own run), written so that the compiler sees a per-thread base
-  // plus a constant per k or r
-  __device__ static int coal(int t, int k) {
-    if constexpr (TB % 32 == 0) return t + (t >> 5) + k * (TB + TB / 32);
-    else return lds_index(k * TB + t);
-  }
-  __device__ static int own(int t, int r) {
-    if constexpr (E == 32) return t * 33 + r;
-    else return lds_index(t * E + r);
-  }
-};
-
-template <int LB>
-__device__ __forceinline__ float inv_sqrt_block() {
-  // 2^(-LB/2), exact for even LB
-  return (LB & 1) ? 0.70710678118654752440f / (float)(1 << (LB >> 1)) : 1.0f / (float)(1 << (LB >> 1));
-}
-
 // ---------------------------------------------------------------- whole block
 
 // Forward of block slot `slot` (block first_block + slot of one generator) by

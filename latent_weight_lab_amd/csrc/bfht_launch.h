@@ -152,4 +152,9 @@ bool grouped_job_supported(const WeightJob& j, bool fwd, const char** why);
 size_t grouped_workspace_bytes(const WeightJob* jobs, int64_t count);
 hipError_t launch_grouped(const WeightJob* jobs, int64_t count, void* work, hipStream_t s, bool fwd);
 
+// Signed activation FHT of `rows` rows of `features` values (bfht_mix.hip):
+// out = (S H S pad(x))[:features] per row, H of order 2^log_size, S = diag(signs).
+hipError_t launch_fht_mix(int dtype, const void* x, void* out, const float* signs, int64_t rows, int64_t features,
+                          int log_size, hipStream_t s);
+
 }  // namespace lwl

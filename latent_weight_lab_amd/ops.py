@@ -266,3 +266,28 @@ def sign_words(seed: int, block: int, layer: int, nwords: int, first_word: int =
                                             ctypes.cast(out.data_ptr(), ctypes.POINTER(ctypes.c_uint32)),
                                             N.stream_ptr(device)))
     return out
+
+
+def fht_mix(x: torch.Tensor, signs: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``(S H S pad(x))[..., :features]`` over the last dimension (``FixedFHTMix.forward``,
+    reference ``examples/nanogpt/model.py:200-218``); ``signs`` holds ±1 for the padded
+    length.  ``out`` may be ``x`` (in place)."""
+    dev = N.require_cuda(x, signs)
+    features = int(x.shape[-1])
+    padded = next_power_of_two(features)
+    if signs.numel() != padded:
+        raise N.BlockFHTArgumentError(f"signs must hold {padded} values for {features} features")
+    signs = signs.detach().to(dtype=torch.float32).contiguous()
+    x = x.contiguous()
+    rows = x.numel() // features if features else 0
+    code = N.dtype_code(x.dtype)
+    L = N.lib()
+    N.check(L.lwl_fht_check_mix(code, rows, features))
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+        raise N.BlockFHTArgumentError("out must be a contiguous tensor like x")
+    with _device_guard(dev):
+        N.check(L.lwl_fht_mix(x.data_ptr(), code, rows, features, signs.data_ptr(), out.data_ptr(),
+                              N.stream_ptr(dev)))
+    return out

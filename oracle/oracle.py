@@ -15,6 +15,7 @@ It restates, in numpy, the semantics of the reference path:
 * ``slice_backward``                 — the adjoint that ``block_fht.py:180-196`` obtains
   by autograd and ``block_fht_ext_cuda.cu:185-223`` computes explicitly
 * ``linear_forward``                 — ``block_fht.py:251-288`` fallback branch
+* ``fixed_fht_mix``                  — ``examples/nanogpt/model.py:200-218`` (``FixedFHTMix``)
 
 and, for the CPU baseline, ``torch_port_slice`` — an op-for-op restatement of
 ``block_fht_slice_torch`` in torch CPU ops (per-block Python loop, reshape
@@ -35,6 +36,8 @@ How each function is pinned (tests/test_oracle.py):
   finite differences, slice == full[start:stop].
 * ``linear_forward``: golden vectors, and equality with a dense matmul on the
   materialized weight.
+* ``fixed_fht_mix``: the dense product ``diag(s) H diag(s)`` with the closed-form
+  H on the padded input, involution and Parseval at power-of-two widths.
 """
 from __future__ import annotations
 
@@ -196,6 +199,20 @@ def linear_forward(x: np.ndarray, latent: np.ndarray, out_features: int, layers:
     w = materialize_weight(latent, in_features, out_features, layers, seed, dtype) * dtype(weight_scale)
     flat = x.reshape(-1, in_features).astype(dtype)
     return (flat @ w.T).reshape(*x.shape[:-1], out_features)
+
+
+def fixed_fht_mix(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """``FixedFHTMix.forward`` (``examples/nanogpt/model.py:200-218``): zero-pad the
+    last dimension to ``P = next_power_of_two(features)``, multiply by the ±1
+    ``signs`` [P], ``normalized_fht_last_dim`` (``model.py:180-197``, the same
+    transform as ``fht_normalized``), multiply by ``signs`` again, keep the first
+    ``features`` values."""
+    features = x.shape[-1]
+    padded = next_power_of_two(features)
+    xp = np.zeros(x.shape[:-1] + (padded,), dtype=np.float64)
+    xp[..., :features] = x
+    y = fht_normalized(xp * signs) * signs
+    return y[..., :features]
 
 
 def rel_l2(got, want) -> float:

@@ -284,3 +284,20 @@ def test_batched_linears_fail_loudly_on_cpu():
         block_fht_headwise_linear(torch.zeros(3, 8), heads)
     with pytest.raises(RuntimeError, match="GPU only"):
         block_fht_grouped_input_linear(torch.zeros(3, 16), heads)
+
+
+@pytest.mark.parametrize(
+    "args, code, msg",
+    [
+        ((0, 10, 768), N.LWL_OK, ""),
+        ((2, 0, 32768), N.LWL_OK, ""),
+        ((0, 10, 32769), N.LWL_ERR_UNSUPPORTED, "up to 32768 features"),
+        ((0, -1, 8), N.LWL_ERR_INVALID, "rows must be non-negative"),
+        ((0, 1, 0), N.LWL_ERR_INVALID, "features must be positive"),
+        ((5, 1, 8), N.LWL_ERR_UNSUPPORTED, "dtype code 5"),
+    ],
+)
+def test_fht_mix_validation(args, code, msg):
+    rc = N.lib().lwl_fht_check_mix(*args)
+    assert rc == code
+    assert msg in N.lib().lwl_last_error().decode()

@@ -218,3 +218,30 @@ def test_torch_port_matches_oracle():
     y.square().sum().backward()
     want = O.slice_backward(2 * y.detach().numpy(), 200, 1500, 3, 77, 255, 1290)
     np.testing.assert_allclose(lat_t.grad.numpy(), want, atol=1e-10)
+
+
+# ---------------------------------------------------------------- signed activation FHT
+
+@pytest.mark.parametrize("features", [1, 5, 8, 100, 256])
+def test_fixed_fht_mix_equals_dense_signed_hadamard(features):
+    rng = np.random.default_rng(features)
+    P = O.next_power_of_two(features)
+    signs = rng.integers(0, 2, P) * 2.0 - 1.0
+    x = rng.standard_normal((4, features))
+    M = np.diag(signs) @ sylvester(P) @ np.diag(signs)
+    xp = np.zeros((4, P))
+    xp[:, :features] = x
+    want = (xp @ M.T)[:, :features]
+    np.testing.assert_allclose(O.fixed_fht_mix(x, signs), want, rtol=1e-12, atol=1e-12)
+
+
+def test_fixed_fht_mix_involution_and_parseval():
+    rng = np.random.default_rng(3)
+    signs = rng.integers(0, 2, 1024) * 2.0 - 1.0
+    x = rng.standard_normal((3, 1024))
+    y = O.fixed_fht_mix(x, signs)
+    np.testing.assert_allclose(np.linalg.norm(y, axis=1), np.linalg.norm(x, axis=1), rtol=1e-12)
+    np.testing.assert_allclose(O.fixed_fht_mix(y, signs), x, rtol=1e-10, atol=1e-12)
+    # a single sign multiply is not an involution: the check would catch that mistake
+    once = O.fht_normalized(x * signs)
+    assert np.abs(O.fht_normalized(once * signs) - x).max() > 1e-3
