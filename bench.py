@@ -294,7 +294,7 @@ def extra_configs(abi, steps, warmup, only):
 
     # config 4: fused linear at GPT-2-small MLP shapes vs dense bf16 GEMM on the materialized weight
     if want("c4_linear"):
-        from latent_weight_lab_amd import block_fht_slice
+        from latent_weight_lab_amd import block_fht_linear_forward, block_fht_slice
 
         lin = {}
         for inf, outf in ((768, 3072), (3072, 768)):
@@ -309,9 +309,15 @@ def extra_configs(abi, steps, warmup, only):
                 flops = 2 * 4096 * inf * outf
                 fused = time_graph(torch, lambda: abi.linear(x, latent, out, outf, 3, 3, 1.0, ws), 50, 5)
                 dense = time_graph(torch, lambda: torch.nn.functional.linear(x, w), 50, 5)
-                lin[f"{inf}x{outf}"] = {"fused_ms": round(fused * 1e3, 4), "dense_gemm_ms": round(dense * 1e3, 4),
+                with torch.no_grad():  # the default route: generate W once (one launch), then the GEMM
+                    auto = time_graph(torch, lambda: block_fht_linear_forward(x, latent, outf, 3, 3), 50, 5)
+                lin[f"{inf}x{outf}"] = {"block_fht_linear_forward_ms": round(auto * 1e3, 4),
+                                        "auto_over_dense": auto / dense,
+                                        "fused_kernel_ms": round(fused * 1e3, 4),
+                                        "dense_gemm_ms": round(dense * 1e3, 4),
                                         "fused_over_dense": fused / dense,
-                                        "fused_tokens_per_s": 4096 / fused,
+                                        "tokens_per_s": 4096 / auto,
+                                        "TFLOPs": flops / auto / 1e12,
                                         "fused_TFLOPs": flops / fused / 1e12,
                                         "dense_TFLOPs": flops / dense / 1e12}
                 del latent, x, out, ws, w
@@ -388,7 +394,7 @@ GPT2_SHAPES = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
 
 
 def stack_bench(abi, torch):
-    from latent_weight_lab_amd import block_fht_slice
+    from latent_weight_lab_amd import block_fht_linear_forward, block_fht_slice
 
     mats = []
     for layer in range(12):
@@ -410,6 +416,24 @@ def stack_bench(abi, torch):
                 for (inf, outf, lat, seed), o, ws in zip(mats, outs, wss):
                     abi.linear(xs[inf], lat, o, outf, 3, seed, 1.0, ws)
 
+            def auto_stack():
+                with torch.no_grad():
+                    for (inf, outf, lat, seed), o in zip(mats, outs):
+                        block_fht_linear_forward(xs[inf], lat, outf, 3, seed)
+
+            sec = time_graph(torch, auto_stack, 5, 2)
+            row["block_fht_linear_forward_ms"] = sec * 1e3
+            row["block_fht_linear_forward_tokens_per_s"] = tokens / sec
+            if tokens == 1:
+                # all 48 weights regenerated in one grouped launch (what a model-wide refresh of
+                # materialized weights costs, e.g. once per optimizer step)
+                from latent_weight_lab_amd import ops as lwl_ops
+
+                specs = [(lat, inf * outf, 3, seed, 1.0, torch.bfloat16) for inf, outf, lat, seed in mats]
+                wbufs = [torch.empty(inf * outf, dtype=torch.bfloat16, device="cuda") for inf, outf, _, _ in mats]
+                out["grouped_regenerate_all_ms"] = time_graph(
+                    torch, lambda: lwl_ops.materialize_weights(specs, wbufs), 5, 2) * 1e3
+                del wbufs
             torch.cuda.synchronize()
             base = torch.cuda.memory_allocated()
             torch.cuda.reset_peak_memory_stats()

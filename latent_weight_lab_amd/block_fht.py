@@ -91,23 +91,43 @@ def block_fht_grad_latent(latent: torch.Tensor, grad_out: torch.Tensor, size: in
 
 
 def block_fht_linear_forward(input: torch.Tensor, latent: torch.Tensor, out_features: int, layers: int, seed: int,
-                             weight_scale: float = 1.0) -> torch.Tensor:
+                             weight_scale: float = 1.0, fused: bool | None = None) -> torch.Tensor:
     """``input @ (weight_scale * W)^T`` with ``W = BlockFHT(latent)[: in*out].view(out, in)``
-    (reference ``block_fht.py:251-288``).  The fused kernel generates W on chip;
-    shapes it does not take fall back, as in the reference, to generating W
-    with the HIP forward and calling ``F.linear`` on the GPU."""
+    (reference ``block_fht.py:251-288``).
+
+    Two routes compute it.  The fused kernel (``fused=True``, bf16 latents of block
+    2^15 with ``in_features % 8 == 0``, 528..5120) generates W on chip for every
+    token range and never stores it.  The default generates W once into a transient
+    buffer (one launch, ``weight_scale`` folded in) and calls ``F.linear`` — the
+    reference's own route at these shapes (its fused gate, ``:263-273``, needs
+    ``B <= 16384`` and ``B % in == 0``).  On MI355X the second is faster at every
+    batch size measured (1 to 8192 tokens, GPT-2 shapes): the fused kernel
+    regenerates each block per token range and streams x once per block, while
+    the transient W costs ~1 µs of HBM traffic and the GEMM runs on hipBLASLt.
+    With autograd recording and a latent that requires grad, W comes from the
+    differentiable ``block_fht_slice``, as in the reference's fallback.
+    """
     if input.dim() < 2:
         raise ValueError("input must have at least 2 dimensions")
     in_features = int(input.shape[-1])
+    out_features = int(out_features)
     flat = input.reshape(-1, in_features)
     _native.require_cuda(flat, latent)
-    if ops.linear_supported(in_features, int(out_features), latent, flat):
-        out = ops.linear_forward(flat, latent, int(out_features), int(layers), int(seed), float(weight_scale))
-    else:
-        size = in_features * int(out_features)
-        weight = block_fht_slice(latent, size, int(layers), int(seed), 0, size).view(int(out_features), in_features)
+    size = in_features * out_features
+    if fused and ops.linear_supported(in_features, out_features, latent, flat):
+        out = ops.linear_forward(flat, latent, out_features, int(layers), int(seed), float(weight_scale))
+    elif torch.is_grad_enabled() and latent.requires_grad:
+        weight = block_fht_slice(latent, size, int(layers), int(seed), 0, size).view(out_features, in_features)
         out = F.linear(flat.contiguous(), weight * float(weight_scale))
-    return out.reshape(*input.shape[:-1], int(out_features))
+    else:
+        with torch.no_grad():
+            if ops.weight_job_supported(latent, size, int(layers), latent.dtype):
+                (weight,) = ops.materialize_weights([(latent, size, int(layers), int(seed), float(weight_scale),
+                                                      latent.dtype)])
+            else:
+                weight = block_fht_slice(latent, size, int(layers), int(seed), 0, size) * float(weight_scale)
+        out = F.linear(flat.contiguous(), weight.view(out_features, in_features))
+    return out.reshape(*input.shape[:-1], out_features)
 
 
 class _BlockFHTLinearFn(torch.autograd.Function):

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from conftest import decode_array, gpu_available
-from latent_weight_lab_amd import BlockFHTLinear, block_fht_linear_forward
+from latent_weight_lab_amd import BlockFHTLinear, block_fht_grad_latent, block_fht_linear_forward, block_fht_slice
 from latent_weight_lab_amd import ops
 from oracle import c_oracle
 from oracle import oracle as O
@@ -51,15 +51,18 @@ def test_fused_linear_matches_oracle(tokens, in_f, out_f, n, layers, seed, scale
     x = torch.randn(tokens, in_f, generator=g).to(torch.bfloat16)
     xd, ld = x.cuda(), latent.cuda()
     assert ops.linear_supported(in_f, out_f, ld, xd), "fused kernel should take this shape"
-    got = block_fht_linear_forward(xd, ld, out_f, layers, seed, weight_scale=scale)
+    got = block_fht_linear_forward(xd, ld, out_f, layers, seed, weight_scale=scale, fused=True)
     torch.cuda.synchronize()
     assert got.shape == (tokens, out_f) and got.dtype == torch.bfloat16
     want = oracle_linear(x, latent, out_f, layers, seed, scale)
     err = O.rel_l2(got.double().cpu().numpy(), want)
     assert err < 1e-2, err
     # deterministic: no atomics, the straddling rows are summed in a fixed order
-    again = block_fht_linear_forward(xd, ld, out_f, layers, seed, weight_scale=scale)
+    again = block_fht_linear_forward(xd, ld, out_f, layers, seed, weight_scale=scale, fused=True)
     assert torch.equal(got, again)
+    # the default route (generate once, then a GEMM) agrees within the bf16 bar
+    auto = block_fht_linear_forward(xd, ld, out_f, layers, seed, weight_scale=scale)
+    assert O.rel_l2(auto.double().cpu().numpy(), want) < 1e-2
 
 
 def test_fused_linear_3d_input_and_module():
@@ -71,6 +74,31 @@ def test_fused_linear_3d_input_and_module():
         dense = torch.nn.functional.linear(x.float(), lin.weight.float())
     assert fused.shape == (2, 5, 3072)
     assert O.rel_l2(fused.double().cpu().numpy(), dense.double().cpu().numpy()) < 1e-2
+
+
+def test_default_route_generates_weight_once_bitwise():
+    # generate + GEMM: W equals the slice forward times weight_scale, rounded as the
+    # reference's fallback (bf16 * scale in bf16), and the product is F.linear's
+    g = torch.Generator().manual_seed(8)
+    latent = torch.randn(32768, generator=g).to(torch.bfloat16).cuda()
+    x = torch.randn(37, 768, generator=g).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        got = block_fht_linear_forward(x, latent, 2304, 3, 5, weight_scale=0.5)
+        w = block_fht_slice(latent, 768 * 2304, 3, 5, 0, 768 * 2304).view(2304, 768) * 0.5
+        want = torch.nn.functional.linear(x, w)
+    assert torch.equal(got, want)
+
+
+def test_default_route_is_differentiable_in_the_latent():
+    latent = torch.randn(4096, device="cuda", requires_grad=True)
+    x = torch.randn(5, 64, device="cuda", requires_grad=True)
+    y = block_fht_linear_forward(x, latent, 48, 2, 13, weight_scale=0.5)
+    y.square().sum().backward()
+    assert latent.grad is not None and x.grad is not None
+    w = block_fht_slice(latent.detach(), 64 * 48, 2, 13, 0, 64 * 48).view(48, 64) * 0.5
+    gy = 2 * (x.detach() @ w.t())
+    want = 0.5 * block_fht_grad_latent(latent.detach(), (gy.t() @ x.detach()).reshape(-1), 64 * 48, 2, 13)
+    assert O.rel_l2(latent.grad.double().cpu().numpy(), want.double().cpu().numpy()) < 1e-5
 
 
 def test_unsupported_shapes_fall_back_to_generated_weight():
