@@ -107,6 +107,11 @@ def block_fht_linear_forward(input: torch.Tensor, latent: torch.Tensor, out_feat
     With autograd recording and a latent that requires grad, W comes from the
     differentiable ``block_fht_slice``, as in the reference's fallback.
     """
+    return _generated_linear(input, latent, out_features, layers, seed, weight_scale, None, fused)
+
+
+def _generated_linear(input, latent, out_features, layers, seed, weight_scale, bias, fused):
+    # block_fht_linear_forward, with an optional bias added by the GEMM's epilogue
     if input.dim() < 2:
         raise ValueError("input must have at least 2 dimensions")
     in_features = int(input.shape[-1])
@@ -116,9 +121,11 @@ def block_fht_linear_forward(input: torch.Tensor, latent: torch.Tensor, out_feat
     size = in_features * out_features
     if fused and ops.linear_supported(in_features, out_features, latent, flat):
         out = ops.linear_forward(flat, latent, out_features, int(layers), int(seed), float(weight_scale))
+        if bias is not None:
+            out = out + bias
     elif torch.is_grad_enabled() and latent.requires_grad:
         weight = block_fht_slice(latent, size, int(layers), int(seed), 0, size).view(out_features, in_features)
-        out = F.linear(flat.contiguous(), weight * float(weight_scale))
+        out = F.linear(flat.contiguous(), weight * float(weight_scale), bias)
     else:
         with torch.no_grad():
             if ops.weight_job_supported(latent, size, int(layers), latent.dtype):
@@ -126,7 +133,7 @@ def block_fht_linear_forward(input: torch.Tensor, latent: torch.Tensor, out_feat
                                                       latent.dtype)])
             else:
                 weight = block_fht_slice(latent, size, int(layers), int(seed), 0, size) * float(weight_scale)
-        out = F.linear(flat.contiguous(), weight.view(out_features, in_features))
+        out = F.linear(flat.contiguous(), weight.view(out_features, in_features), bias)
     return out.reshape(*input.shape[:-1], out_features)
 
 
@@ -309,12 +316,17 @@ class BlockFHTLinear(nn.Module):
                                        self.fused_latent_grad)
 
     def forward_fused(self, input: torch.Tensor, weight_scale: float = 1.0) -> torch.Tensor:
-        """Inference forward without materializing W (reference ``block_fht.py:482-501``)."""
+        """Inference forward (reference ``block_fht.py:482-501``): W generated once into a
+        transient buffer, then one GEMM that also adds the bias when no modulation or
+        residual term comes between; otherwise the reference's sequence of terms."""
         if self.output_gain is not None or self.input_gain is not None or self.spectral_core is not None:
             return F.linear(input, self.weight.to(dtype=input.dtype), self.bias)
         g = self.generator
-        out = block_fht_linear_forward(input, g.latent, self.out_features, g.layers, g.seed,
-                                       weight_scale=weight_scale * self.weight_scale)
+        scale = weight_scale * self.weight_scale
+        if self.modulation_alpha == 0.0 and self.residual_base_weight is None:
+            # the bias rides in the GEMM's epilogue
+            return _generated_linear(input, g.latent, self.out_features, g.layers, g.seed, scale, self.bias, None)
+        out = block_fht_linear_forward(input, g.latent, self.out_features, g.layers, g.seed, weight_scale=scale)
         if self.modulation_alpha != 0.0:
             modulation = self.modulation_alpha * self._modulation_offset()
             out = out + modulation.to(dtype=out.dtype) * input.sum(dim=-1, keepdim=True)

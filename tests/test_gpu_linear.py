@@ -121,3 +121,28 @@ def test_linear_golden_vectors(golden):
                                        weight_scale=case["weight_scale"])
         want = decode_array(case["out"])
         assert O.rel_l2(got.double().cpu().numpy().reshape(-1), want) < 1e-5
+
+
+@pytest.mark.parametrize("opts", [
+    dict(bias=True),
+    dict(bias=True, modulation_alpha=0.3),
+    dict(bias=True, residual_base_scale=0.5),
+    dict(bias=False, output_gain=True, input_gain=True),
+])
+def test_forward_fused_matches_materialized(opts):
+    # reference tests/test_block_fht.py:196-199 and tests/test_block_fht_cuda.py:43-98:
+    # forward_fused == F.linear(x, weight, bias) for every option
+    torch.manual_seed(1)
+    lin = BlockFHTLinear(96, 40, latent_dim=1000, layers=2, seed=5, weight_scale=0.7, **opts).cuda()
+    with torch.no_grad():
+        if lin.bias is not None:
+            lin.bias.normal_()
+        for gain in (lin.output_gain, lin.input_gain):
+            if gain is not None:
+                gain.uniform_(0.5, 1.5)
+        x = torch.randn(3, 7, 96, device="cuda")
+        got = lin.forward_fused(x)
+        want = torch.nn.functional.linear(x.double(), lin.weight.double(),
+                                          None if lin.bias is None else lin.bias.double())
+    assert got.shape == (3, 7, 40)
+    assert O.rel_l2(got.double().cpu().numpy(), want.cpu().numpy()) < 1e-5
