@@ -1,0 +1,385 @@
+// Whole-block VALU transforms (blocks of 2^0 .. 2^15 held in registers with
+// LDS exchanges), shared by the per-generator kernels (bfht_kernels.hip) and
+// the grouped weight-cache kernels (bfht_grouped_kernels.hip).
+#pragma once
+
+#include "bfht_device.h"
+#include "bfht_launch.h"
+
+namespace lwl {
+
+// Element loads / stores through a raw buffer resource: element index i of the
+// buffer; indices past the end read 0 / are dropped by the buffer range check,
+// and negative indices are sent to the out-of-range offset 2^31 explicitly (the
+// check covers only the per-lane offset, and a wrapped offset near 2^32 must
+// never reach it).  Buffers stay below 2 GiB.  The resource must be uniform
+// across the wave (a divergent one costs a loop over its distinct values).
+constexpr uint32_t kOobOffset = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(bytes < 0x80000000ull ? bytes : 0x80000000ull), 0x00020000);
+}
+template <class T>
+__device__ __forceinline__ int buf_offset(int i) {
+  return (int)(i < 0 ? kOobOffset : (uint32_t)i * (uint32_t)sizeof(T));
+}
+template <class T>
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, buf_offset<T>(i), 0, 0));
+  } else {
+    const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, buf_offset<T>(i), 0, 0);
+    return to_f32(__builtin_bit_cast(T, h));
+  }
+}
+template <class T>
+__device__ __forceinline__ void buf_store(float v, __amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, buf_offset<T>(i), 0, 1 | 16);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), r, buf_offset<T>(i), 0,
+                                          1 | 16);
+  }
+}
+
+// ---------------------------------------------------------------- whole block
+
+// Blocks of up to 2^5 (one thread holds a whole block, no LDS).
+template <int LB, class T, class Store>
+__device__ __forceinline__ void block_fwd_small(const T* __restrict__ latent, Store out, int n, int64_t first_block,
+                                                int64_t slot, int64_t nblocks, int64_t start, int64_t stop,
+                                                uint32_t seed32, int layers) {
+  using Gm = Geo<LB>;
+  static_assert(Gm::TB == 1, "one thread per block");
+  const bool active = slot < nblocks;
+  const int64_t block = first_block + (active ? slot : 0);
+  const uint32_t bkey = block_key(seed32, block);
+  float v[Gm::E];
+  {
+    const uint32_t w = sign_word(bkey, layer_key(0), 0u);
+    const auto lat_r = tile_rsrc(latent, (uint64_t)n * sizeof(T));  // positions >= n read 0
+#pragma unroll
+    for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(buf_load<T>(lat_r, r), w, r);
+  }
+  const float scale = inv_sqrt_block<LB>();
+  for (int layer = 0; layer < layers; ++layer) {
+    butterflies<Gm::E>(v, Gm::LE);
+    const uint32_t w = sign_word(bkey, layer_key(layer + 1), 0u);
+#pragma unroll
+    for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(v[r], w, r) * scale;
+  }
+  if (!active) return;
+  const int64_t base = block * Gm::B;
+  const int64_t lo = start - base > 0 ? start - base : 0;
+  const int64_t hi = stop - base < Gm::B ? stop - base : Gm::B;
+#pragma unroll
+  for (int r = 0; r < Gm::E; ++r)
+    if (r >= lo && r < hi) out.at(base + r - start, v[r]);
+}
+
+template <int LB, class T, class Load>
+__device__ __forceinline__ void block_bwd_small(Load grad, float* __restrict__ partial, int64_t stride,
+                                                T* __restrict__ grad_latent, int n, int64_t first_block, int64_t slot,
+                                                int64_t nblocks, int64_t start, int64_t stop, uint32_t seed32,
+                                                int layers, int direct) {
+  using Gm = Geo<LB>;
+  static_assert(Gm::TB == 1, "one thread per block");
+  const bool active = slot < nblocks;
+  const int64_t block = first_block + (active ? slot : 0);
+  const uint32_t bkey = block_key(seed32, block);
+  const int64_t base = block * Gm::B;
+  const int64_t lo = start - base > 0 ? start - base : 0;
+  const int64_t hi = stop - base < Gm::B ? stop - base : Gm::B;
+  // every lane is a different block: element loads from a valid index (the
+  // slice's first element stands in for positions outside it), then a select
+  float v[Gm::E];
+#pragma unroll
+  for (int r = 0; r < Gm::E; ++r) {
+    const bool valid = active && r >= lo && r < hi;
+    const float x = grad.at(valid ? base + r - start : 0);
+    v[r] = valid ? x : 0.0f;
+  }
+  const float scale = inv_sqrt_block<LB>();
+  for (int layer = layers - 1; layer >= 0; --layer) {
+    const uint32_t w = sign_word(bkey, layer_key(layer + 1), 0u);
+#pragma unroll
+    for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(v[r], w, r);
+    butterflies<Gm::E>(v, Gm::LE);
+#pragma unroll
+    for (int r = 0; r < Gm::E; ++r) v[r] *= scale;
+  }
+  if (!active) return;
+  const uint32_t w0 = sign_word(bkey, layer_key(0), 0u);
+#pragma unroll
+  for (int r = 0; r < Gm::E; ++r) {
+    if (r < n) {
+      const float g = signed_by(v[r], w0, r);
+      if (direct)
+        grad_latent[r] = from_f32<T>(g);
+      else
+        partial[slot * stride + r] = g;
+    }
+  }
+}
+
+// Blocks of 2^6 .. 2^15: 32 values per thread.  The transform is a sequence of
+// bit groups — the top group (position bits LB-5 .. LB-1, which the registers
+// of the coalesced layout span: register r of thread t holds position
+// r * TB + t) and groups of up to 5 bits from bit 0 up — with one LDS exchange
+// between consecutive groups.  Even layers run the groups in that order, odd
+// layers in reverse, so a layer boundary needs no exchange: the sign layer
+// between them is applied in whatever layout the data is in, from a table of
+// the block's sign words in LDS (hashed once per block, one word per thread and
+// layer).  The block is read and written in the coalesced layout (or, after an
+// odd number of layers, in the last group's layout when that keeps 32
+// consecutive positions per half wave).
+template <int LB>
+struct BlockSeq {
+  static constexpr int TOP = LB - 5;
+  static constexpr int N = 1 + (TOP + 4) / 5;  // groups
+  __host__ __device__ static constexpr int lo(int g) { return g == 0 ? TOP : 5 * (g - 1); }
+  __host__ __device__ static constexpr int nb(int g) {
+    return g == 0 ? 5 : (TOP - 5 * (g - 1) < 5 ? TOP - 5 * (g - 1) : 5);
+  }
+  // the last group's layout stores 32 consecutive positions per half wave
+  static constexpr bool kLastStores = lo(N - 1) >= 5;
+};
+
+constexpr int kSignTableLayers = 4;  // layers 0..3
+
+template <int LB>
+struct BlockLds {
+  using Gm = Geo<LB>;
+  // per block: the padded exchange buffer, then the sign-word table
+  static constexpr int FLOATS = Gm::NG > 1 ? Gm::G * (Gm::PADDED + kSignTableLayers * Gm::TB) : 1;
+  __device__ static float* data(float* smem, int gi) { return smem + gi * Gm::PADDED; }
+  __device__ static uint32_t* table(float* smem, int gi) {
+    return reinterpret_cast<uint32_t*>(smem + Gm::G * Gm::PADDED) + gi * kSignTableLayers * Gm::TB;
+  }
+};
+
+// Register exchange from group layout (lo_a, nb_a) to (lo_b, nb_b) through LDS.
+template <int LB>
+__device__ __forceinline__ void exchange(float (&v)[32], float* lds, int t, int lo_a, int nb_a, int lo_b, int nb_b) {
+  const int wb = group_base<LB, 5>(t, lo_a, nb_a);
+  __syncthreads();  // earlier reads of the buffer are done
+#pragma unroll
+  for (int r = 0; r < 32; ++r) lds[group_lds<LB, 5>(wb, r, lo_a, nb_a)] = v[r];
+  __syncthreads();
+  const int rb = group_base<LB, 5>(t, lo_b, nb_b);
+#pragma unroll
+  for (int r = 0; r < 32; ++r) v[r] = lds[group_lds<LB, 5>(rb, r, lo_b, nb_b)];
+}
+
+// v[r] *= ±scale by the sign bit of its position in layout (lo, nb): word p >> 5
+// of the layer's table, bit p & 31 (set: +).  Position = per-thread base OR a
+// per-register constant (disjoint bits), so word index and bit split the same way.
+template <int LB>
+__device__ __forceinline__ void sign_scale(float (&v)[32], const uint32_t* words, int t, int lo, int nb,
+                                           float scale) {
+  const int base = group_pos<LB, 5>(t, 0, lo, nb);
+  const uint32_t pos = __float_as_uint(scale), neg = pos ^ 0x80000000u;
+#pragma unroll
+  for (int r = 0; r < 32; ++r) {
+    const int c = group_pos<LB, 5>(0, r, lo, nb);
+    const uint32_t w = words[(base >> 5) + (c >> 5)];
+    const int bit = (base & 31) | (c & 31);
+    const uint32_t m = (uint32_t)((int32_t)(w << (31 - bit)) >> 31);
+    v[r] *= __uint_as_float((m & pos) | (~m & neg));
+  }
+}
+
+// One layer's transform (unnormalized), groups forward (even layers: top first,
+// ending in the last group's layout) or reversed (odd layers).
+template <int LB>
+__device__ __forceinline__ void layer_fht(float (&v)[32], float* lds, int t, bool reversed) {
+  using S = BlockSeq<LB>;
+  if (!reversed) {
+    butterflies<32>(v, S::nb(0));
+#pragma unroll
+    for (int g = 1; g < S::N; ++g) {
+      exchange<LB>(v, lds, t, S::lo(g - 1), S::nb(g - 1), S::lo(g), S::nb(g));
+      butterflies<32>(v, S::nb(g));
+    }
+  } else {
+    butterflies<32>(v, S::nb(S::N - 1));
+#pragma unroll
+    for (int g = S::N - 2; g >= 0; --g) {
+      exchange<LB>(v, lds, t, S::lo(g + 1), S::nb(g + 1), S::lo(g), S::nb(g));
+      butterflies<32>(v, S::nb(g));
+    }
+  }
+}
+
+template <int LB>
+__device__ __forceinline__ void fill_sign_table(uint32_t* tab, uint32_t bkey, int t, int layers) {
+  for (int l = 0; l <= layers; ++l) tab[l * Geo<LB>::TB + t] = sign_word(bkey, layer_key(l), (uint32_t)t);
+}
+
+// Forward of block slot `slot` (block first_block + slot of one generator) by
+// thread group gi of the workgroup; every thread of the workgroup calls it
+// (barriers inside), threads of an inactive slot (slot >= nblocks) included.
+template <int LB, class T, class Store>
+__device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Store out, int n,
+                                               int64_t first_block, int64_t slot, int64_t nblocks, int64_t start,
+                                               int64_t stop, uint32_t seed32, int layers, float* smem) {
+  using Gm = Geo<LB>;
+  using S = BlockSeq<LB>;
+  if constexpr (Gm::NG <= 1) {  // B <= 2^5
+    block_fwd_small<LB, T>(latent, out, n, first_block, slot, nblocks, start, stop, seed32, layers);
+  } else {
+    const int gi = threadIdx.x >> Gm::LT;
+    const int t = threadIdx.x & (Gm::TB - 1);
+    const bool active = slot < nblocks;
+    const int64_t block = first_block + (active ? slot : 0);
+    float* lds = BlockLds<LB>::data(smem, gi);
+    uint32_t* tab = BlockLds<LB>::table(smem, gi);
+    fill_sign_table<LB>(tab, block_key(seed32, block), t, layers);
+    // coalesced layout: register r of thread t holds position r * TB + t;
+    // positions >= n read 0 (buffer range)
+    const auto lat_r = tile_rsrc(latent, (uint64_t)n * sizeof(T));
+    float v[32];
+#pragma unroll
+    for (int r = 0; r < 32; ++r) v[r] = buf_load<T>(lat_r, r * Gm::TB + t);
+    __syncthreads();  // the sign table is complete
+    sign_scale<LB>(v, tab, t, S::lo(0), S::nb(0), 1.0f);
+    const float scale = inv_sqrt_block<LB>();
+    for (int layer = 0; layer < layers; ++layer) {
+      const bool odd = layer & 1;
+      layer_fht<LB>(v, lds, t, odd);
+      if (odd)
+        sign_scale<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(0), S::nb(0), scale);
+      else
+        sign_scale<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(S::N - 1), S::nb(S::N - 1), scale);
+    }
+    // store from the layout the last layer ended in
+    const int64_t base = block * Gm::B;
+    const int64_t lo = start - base > 0 ? start - base : 0;
+    const int64_t hi = stop - base < Gm::B ? stop - base : Gm::B;
+    auto store = [&](int glo, int gnb) {
+      if (!active) return;
+      const int pb = group_pos<LB, 5>(t, 0, glo, gnb);
+      if constexpr (Gm::TB >= 64) {
+        // one block per wave: a uniform buffer resource over the block's range,
+        // positions outside [lo, hi) dropped by its range check
+        const auto out_r = out.range(base + lo - start, hi - lo);
+#pragma unroll
+        for (int r = 0; r < 32; ++r) out(out_r, pb + group_pos<LB, 5>(0, r, glo, gnb) - (int)lo, v[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+          const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
+          if (p >= lo && p < hi) out.at(base + p - start, v[r]);
+        }
+      }
+    };
+    if (!(layers & 1)) {
+      store(S::lo(0), S::nb(0));
+    } else if constexpr (S::kLastStores) {
+      store(S::lo(S::N - 1), S::nb(S::N - 1));
+    } else {
+      exchange<LB>(v, lds, t, S::lo(S::N - 1), S::nb(S::N - 1), S::lo(0), S::nb(0));
+      store(S::lo(0), S::nb(0));
+    }
+  }
+}
+
+// Backward: adjoint chain D_0 H D_1 ... H D_L on grad scattered into the block.
+// Writes partial[slot * stride + p] (float32) for p < n, or the final gradient
+// in T when `direct` (a single block).
+template <int LB, class T, class Load>
+__device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ partial, int64_t stride,
+                                               T* __restrict__ grad_latent, int n, int64_t first_block, int64_t slot,
+                                               int64_t nblocks, int64_t start, int64_t stop, uint32_t seed32,
+                                               int layers, int direct, float* smem) {
+  using Gm = Geo<LB>;
+  using S = BlockSeq<LB>;
+  if constexpr (Gm::NG <= 1) {  // B <= 2^5
+    block_bwd_small<LB, T>(grad, partial, stride, grad_latent, n, first_block, slot, nblocks, start, stop, seed32,
+                           layers, direct);
+  } else {
+    const int gi = threadIdx.x >> Gm::LT;
+    const int t = threadIdx.x & (Gm::TB - 1);
+    const bool active = slot < nblocks;
+    const int64_t block = first_block + (active ? slot : 0);
+    float* lds = BlockLds<LB>::data(smem, gi);
+    uint32_t* tab = BlockLds<LB>::table(smem, gi);
+    fill_sign_table<LB>(tab, block_key(seed32, block), t, layers);
+    const int64_t base = block * Gm::B;
+    const int64_t lo = start - base > 0 ? start - base : 0;
+    const int64_t hi = stop - base < Gm::B ? stop - base : Gm::B;
+    // positions outside [lo, hi), and every position of an inactive slot, read 0
+    float v[32];
+    if constexpr (Gm::TB >= 64) {
+      const auto g_r = grad.range(base + lo - start, active ? hi - lo : 0);
+#pragma unroll
+      for (int r = 0; r < 32; ++r) v[r] = grad(g_r, r * Gm::TB + t - (int)lo);
+    } else {
+      // several blocks per wave: element loads from a valid index (the slice's
+      // first element stands in for positions outside it), then a select
+#pragma unroll
+      for (int r = 0; r < 32; ++r) {
+        const int p = r * Gm::TB + t;
+        const bool valid = active && p >= lo && p < hi;
+        const float x = grad.at(valid ? base + p - start : 0);
+        v[r] = valid ? x : 0.0f;
+      }
+    }
+    __syncthreads();  // the sign table is complete
+    sign_scale<LB>(v, tab + layers * Gm::TB, t, S::lo(0), S::nb(0), 1.0f);
+    const float scale = inv_sqrt_block<LB>();
+    for (int i = 0; i < layers; ++i) {
+      const bool odd = i & 1;
+      layer_fht<LB>(v, lds, t, odd);
+      const uint32_t* words = tab + (layers - 1 - i) * Gm::TB;
+      if (odd)
+        sign_scale<LB>(v, words, t, S::lo(0), S::nb(0), scale);
+      else
+        sign_scale<LB>(v, words, t, S::lo(S::N - 1), S::nb(S::N - 1), scale);
+    }
+    auto write = [&](int glo, int gnb) {
+      if (!active) return;
+      const int pb = group_pos<LB, 5>(t, 0, glo, gnb);
+      if constexpr (Gm::TB >= 64) {
+        // one block per wave: uniform resources, positions >= n dropped
+        const auto d_r = direct ? tile_rsrc(grad_latent, (uint64_t)n * sizeof(T))
+                                : tile_rsrc(partial + slot * stride, (uint64_t)n * 4);
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+          const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
+          if (direct)
+            buf_store<T>(v[r], d_r, p);
+          else
+            buf_store<float>(v[r], d_r, p);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+          const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
+          if (p < n) {
+            if (direct)
+              grad_latent[p] = from_f32<T>(v[r]);
+            else
+              partial[slot * stride + p] = v[r];
+          }
+        }
+      }
+    };
+    if (!(layers & 1)) {
+      write(S::lo(0), S::nb(0));
+    } else if constexpr (S::kLastStores) {
+      write(S::lo(S::N - 1), S::nb(S::N - 1));
+    } else {
+      exchange<LB>(v, lds, t, S::lo(S::N - 1), S::nb(S::N - 1), S::lo(0), S::nb(0));
+      write(S::lo(0), S::nb(0));
+    }
+  }
+}
+
+// Rounding of a float32 value to T and back.
+template <class T>
+__device__ __forceinline__ float round_to(float v) {
+  return to_f32(from_f32<T>(v));
+}
+
+}  // namespace lwl

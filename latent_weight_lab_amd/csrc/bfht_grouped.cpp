@@ -7,7 +7,8 @@
 // one ext.forward / ext.backward call per module).  Jobs are sorted into
 // classes that one kernel instantiation serves — (matrix-core chain, layer
 // count) for bfloat16 blocks of 2^15 that the per-module call would run on the
-// matrix cores, (element type, block size) for every other whole block — and
+// matrix cores, (latent type, weight type, block size) for every other whole
+// block — and
 // each class runs in launches of up to kGroupMaxJobs jobs.  Every block runs
 // exactly the code of its per-module launch, so the results are bit-identical
 // to the per-module path followed by torch's scale, cast and accumulate.
@@ -32,10 +33,12 @@ int log2_ceil(int64_t v) {
 struct ClassKey {
   bool mfma;
   int dtype;
+  int wdtype;  // VALU classes only (a template parameter there)
   int log_block;
   int layers;  // matrix-core classes only (a template parameter there)
   bool operator==(const ClassKey& o) const {
-    return mfma == o.mfma && dtype == o.dtype && log_block == o.log_block && layers == o.layers;
+    return mfma == o.mfma && dtype == o.dtype && wdtype == o.wdtype && log_block == o.log_block &&
+           layers == o.layers;
   }
 };
 
@@ -45,8 +48,13 @@ ClassKey class_of(const WeightJob& j, bool fwd) {
   // 16-byte aligned source (latent, or the weight gradient in the backward)
   const void* src = fwd ? j.latent : j.grad_weight;
   const bool mfma = j.ldtype == kBF16 && lb == 15 && (uintptr_t)src % 16 == 0;
-  return ClassKey{mfma, j.ldtype, lb, mfma ? j.layers : 0};
+  return ClassKey{mfma, j.ldtype, mfma ? kBF16 : j.wdtype, lb, mfma ? j.layers : 0};
 }
+
+// Partial rows of the backward are 128-byte aligned: n rounded up to 32 floats.
+int64_t row_stride(const WeightJob& j) { return (j.n + 31) / 32 * 32; }
+
+size_t partial_bytes(const WeightJob& j);
 
 int64_t blocks_of(const WeightJob& j) {
   const int64_t B = (int64_t)1 << log2_ceil(j.n);
@@ -60,6 +68,8 @@ int64_t workgroups_of(const ClassKey& k, const WeightJob& j) {
   return (blocks_of(j) + g - 1) / g;
 }
 
+size_t partial_bytes(const WeightJob& j) { return align_up((size_t)blocks_of(j) * (size_t)row_stride(j) * 4); }
+
 GroupJob device_job(const WeightJob& j, bool fwd, float* part) {
   GroupJob d{};
   d.src = fwd ? j.latent : j.grad_weight;
@@ -67,6 +77,7 @@ GroupJob device_job(const WeightJob& j, bool fwd, float* part) {
   d.part = part;
   d.size = j.size;
   d.n = (int32_t)j.n;
+  d.stride = (int32_t)row_stride(j);
   d.nblocks = (int32_t)blocks_of(j);
   d.seed32 = j.seed32;
   d.layers = j.layers;
@@ -121,7 +132,7 @@ bool grouped_job_supported(const WeightJob& j, bool fwd, const char** why) {
 
 size_t grouped_workspace_bytes(const WeightJob* jobs, int64_t count) {
   size_t total = 0;
-  for (int64_t i = 0; i < count; ++i) total += align_up((size_t)blocks_of(jobs[i]) * (size_t)jobs[i].n * 4);
+  for (int64_t i = 0; i < count; ++i) total += partial_bytes(jobs[i]);
   return total;
 }
 
@@ -133,7 +144,7 @@ hipError_t launch_grouped(const WeightJob* jobs, int64_t count, void* work, hipS
     float* part = nullptr;
     if (!fwd) {
       part = reinterpret_cast<float*>(static_cast<char*>(work) + off);
-      off += align_up((size_t)blocks_of(jobs[i]) * (size_t)jobs[i].n * 4);
+      off += partial_bytes(jobs[i]);
     }
     djobs[i] = device_job(jobs[i], fwd, part);
     keys[i] = class_of(jobs[i], fwd);
@@ -153,7 +164,7 @@ hipError_t launch_grouped(const WeightJob* jobs, int64_t count, void* work, hipS
         idx, djobs, [&](int m) { return workgroups_of(k, jobs[m]); },
         [&](const GroupTable& t) {
           return k.mfma ? launch_mfma15_grouped(t, k.layers, s, fwd)
-                        : launch_block_grouped(t, k.dtype, k.log_block, s, fwd);
+                        : launch_block_grouped(t, k.dtype, k.wdtype, k.log_block, s, fwd);
         });
     if (e != hipSuccess) return e;
   }

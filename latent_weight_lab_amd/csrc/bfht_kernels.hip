@@ -16,312 +16,31 @@
 //
 // Reference semantics: latent_weight_lab/block_fht.py:84-109 (forward),
 // csrc/block_fht_ext_cuda.cu:185-223 and :568-622 (backward).
-#include "bfht_device.h"
-#include "bfht_launch.h"
+#include "bfht_block.h"
 
 namespace lwl {
 
-// ---------------------------------------------------------------- whole block
-
-// Blocks of up to 2^5 (one thread holds a whole block, no LDS).
-template <int LB, class T, class Store>
-__device__ __forceinline__ void block_fwd_small(const T* __restrict__ latent, Store out, int n, int64_t first_block,
-                                                int64_t slot, int64_t nblocks, int64_t start, int64_t stop,
-                                                uint32_t seed32, int layers) {
-  using Gm = Geo<LB>;
-  static_assert(Gm::TB == 1, "one thread per block");
-  const bool active = slot < nblocks;
-  const int64_t block = first_block + (active ? slot : 0);
-  const uint32_t bkey = block_key(seed32, block);
-  float v[Gm::E];
-  {
-    const uint32_t w = sign_word(bkey, layer_key(0), 0u);
-#pragma unroll
-    for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(r < n ? to_f32(latent[r]) : 0.0f, w, r);
-  }
-  const float scale = inv_sqrt_block<LB>();
-  for (int layer = 0; layer < layers; ++layer) {
-    butterflies<Gm::E>(v, Gm::LE);
-    const uint32_t w = sign_word(bkey, layer_key(layer + 1), 0u);
-#pragma unroll
-    for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(v[r], w, r) * scale;
-  }
-  if (!active) return;
-  const int64_t base = block * Gm::B;
-#pragma unroll
-  for (int r = 0; r < Gm::E; ++r)
-    if (base + r >= start && base + r < stop) out(base + r - start, v[r]);
-}
-
-template <int LB, class T, class Load>
-__device__ __forceinline__ void block_bwd_small(Load grad, float* __restrict__ partial, T* __restrict__ grad_latent,
-                                                int n, int64_t first_block, int64_t slot, int64_t nblocks,
-                                                int64_t start, int64_t stop, uint32_t seed32, int layers,
-                                                int direct) {
-  using Gm = Geo<LB>;
-  static_assert(Gm::TB == 1, "one thread per block");
-  const bool active = slot < nblocks;
-  const int64_t block = first_block + (active ? slot : 0);
-  const uint32_t bkey = block_key(seed32, block);
-  const int64_t base = block * Gm::B;
-  float v[Gm::E];
-#pragma unroll
-  for (int r = 0; r < Gm::E; ++r)
-    v[r] = (active && base + r >= start && base + r < stop) ? grad(base + r - start) : 0.0f;
-  const float scale = inv_sqrt_block<LB>();
-  for (int layer = layers - 1; layer >= 0; --layer) {
-    const uint32_t w = sign_word(bkey, layer_key(layer + 1), 0u);
-#pragma unroll
-    for (int r = 0; r < Gm::E; ++r) v[r] = signed_by(v[r], w, r);
-    butterflies<Gm::E>(v, Gm::LE);
-#pragma unroll
-    for (int r = 0; r < Gm::E; ++r) v[r] *= scale;
-  }
-  if (!active) return;
-  const uint32_t w0 = sign_word(bkey, layer_key(0), 0u);
-#pragma unroll
-  for (int r = 0; r < Gm::E; ++r) {
-    if (r < n) {
-      const float g = signed_by(v[r], w0, r);
-      if (direct)
-        grad_latent[r] = from_f32<T>(g);
-      else
-        partial[slot * (int64_t)n + r] = g;
-    }
-  }
-}
-
-// Blocks of 2^6 .. 2^15: 32 values per thread.  The transform is a sequence of
-// bit groups — the top group (position bits LB-5 .. LB-1, which the registers
-// of the coalesced layout span: register r of thread t holds position
-// r * TB + t) and groups of up to 5 bits from bit 0 up — with one LDS exchange
-// between consecutive groups.  Even layers run the groups in that order, odd
-// layers in reverse, so a layer boundary needs no exchange: the sign layer
-// between them is applied in whatever layout the data is in, from a table of
-// the block's sign words in LDS (hashed once per block, one word per thread and
-// layer).  The block is read and written in the coalesced layout (or, after an
-// odd number of layers, in the last group's layout when that keeps 32
-// consecutive positions per half wave).
-template <int LB>
-struct BlockSeq {
-  static constexpr int TOP = LB - 5;
-  static constexpr int N = 1 + (TOP + 4) / 5;  // groups
-  __host__ __device__ static constexpr int lo(int g) { return g == 0 ? TOP : 5 * (g - 1); }
-  __host__ __device__ static constexpr int nb(int g) {
-    return g == 0 ? 5 : (TOP - 5 * (g - 1) < 5 ? TOP - 5 * (g - 1) : 5);
-  }
-  // the last group's layout stores 32 consecutive positions per half wave
-  static constexpr bool kLastStores = lo(N - 1) >= 5;
-};
-
-constexpr int kSignTableLayers = 4;  // layers 0..3
-
-template <int LB>
-struct BlockLds {
-  using Gm = Geo<LB>;
-  // per block: the padded exchange buffer, then the sign-word table
-  static constexpr int FLOATS = Gm::NG > 1 ? Gm::G * (Gm::PADDED + kSignTableLayers * Gm::TB) : 1;
-  __device__ static float* data(float* smem, int gi) { return smem + gi * Gm::PADDED; }
-  __device__ static uint32_t* table(float* smem, int gi) {
-    return reinterpret_cast<uint32_t*>(smem + Gm::G * Gm::PADDED) + gi * kSignTableLayers * Gm::TB;
-  }
-};
-
-// Register exchange from group layout (lo_a, nb_a) to (lo_b, nb_b) through LDS.
-template <int LB>
-__device__ __forceinline__ void exchange(float (&v)[32], float* lds, int t, int lo_a, int nb_a, int lo_b, int nb_b) {
-  const int wb = group_base<LB, 5>(t, lo_a, nb_a);
-  __syncthreads();  // earlier reads of the buffer are done
-#pragma unroll
-  for (int r = 0; r < 32; ++r) lds[group_lds<LB, 5>(wb, r, lo_a, nb_a)] = v[r];
-  __syncthreads();
-  const int rb = group_base<LB, 5>(t, lo_b, nb_b);
-#pragma unroll
-  for (int r = 0; r < 32; ++r) v[r] = lds[group_lds<LB, 5>(rb, r, lo_b, nb_b)];
-}
-
-// v[r] *= ±scale by the sign bit of its position in layout (lo, nb): word p >> 5
-// of the layer's table, bit p & 31 (set: +).  Position = per-thread base OR a
-// per-register constant (disjoint bits), so word index and bit split the same way.
-template <int LB>
-__device__ __forceinline__ void sign_scale(float (&v)[32], const uint32_t* words, int t, int lo, int nb,
-                                           float scale) {
-  const int base = group_pos<LB, 5>(t, 0, lo, nb);
-  const uint32_t pos = __float_as_uint(scale), neg = pos ^ 0x80000000u;
-#pragma unroll
-  for (int r = 0; r < 32; ++r) {
-    const int c = group_pos<LB, 5>(0, r, lo, nb);
-    const uint32_t w = words[(base >> 5) + (c >> 5)];
-    const int bit = (base & 31) | (c & 31);
-    const uint32_t m = (uint32_t)((int32_t)(w << (31 - bit)) >> 31);
-    v[r] *= __uint_as_float((m & pos) | (~m & neg));
-  }
-}
-
-// One layer's transform (unnormalized), groups forward (even layers: top first,
-// ending in the last group's layout) or reversed (odd layers).
-template <int LB>
-__device__ __forceinline__ void layer_fht(float (&v)[32], float* lds, int t, bool reversed) {
-  using S = BlockSeq<LB>;
-  if (!reversed) {
-    butterflies<32>(v, S::nb(0));
-#pragma unroll
-    for (int g = 1; g < S::N; ++g) {
-      exchange<LB>(v, lds, t, S::lo(g - 1), S::nb(g - 1), S::lo(g), S::nb(g));
-      butterflies<32>(v, S::nb(g));
-    }
-  } else {
-    butterflies<32>(v, S::nb(S::N - 1));
-#pragma unroll
-    for (int g = S::N - 2; g >= 0; --g) {
-      exchange<LB>(v, lds, t, S::lo(g + 1), S::nb(g + 1), S::lo(g), S::nb(g));
-      butterflies<32>(v, S::nb(g));
-    }
-  }
-}
-
-template <int LB>
-__device__ __forceinline__ void fill_sign_table(uint32_t* tab, uint32_t bkey, int t, int layers) {
-  for (int l = 0; l <= layers; ++l) tab[l * Geo<LB>::TB + t] = sign_word(bkey, layer_key(l), (uint32_t)t);
-}
-
-// Forward of block slot `slot` (block first_block + slot of one generator) by
-// thread group gi of the workgroup; every thread of the workgroup calls it
-// (barriers inside), threads of an inactive slot (slot >= nblocks) included.
-template <int LB, class T, class Store>
-__device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Store out, int n,
-                                               int64_t first_block, int64_t slot, int64_t nblocks, int64_t start,
-                                               int64_t stop, uint32_t seed32, int layers, float* smem) {
-  using Gm = Geo<LB>;
-  using S = BlockSeq<LB>;
-  if constexpr (Gm::NG <= 1) {  // B <= 2^5
-    block_fwd_small<LB, T>(latent, out, n, first_block, slot, nblocks, start, stop, seed32, layers);
-  } else {
-    const int gi = threadIdx.x >> Gm::LT;
-    const int t = threadIdx.x & (Gm::TB - 1);
-    const bool active = slot < nblocks;
-    const int64_t block = first_block + (active ? slot : 0);
-    float* lds = BlockLds<LB>::data(smem, gi);
-    uint32_t* tab = BlockLds<LB>::table(smem, gi);
-    fill_sign_table<LB>(tab, block_key(seed32, block), t, layers);
-    float v[32];
-#pragma unroll
-    for (int r = 0; r < 32; ++r) {
-      const int p = r * Gm::TB + t;
-      v[r] = p < n ? to_f32(latent[p]) : 0.0f;
-    }
-    __syncthreads();  // the sign table is complete
-    sign_scale<LB>(v, tab, t, S::lo(0), S::nb(0), 1.0f);
-    const float scale = inv_sqrt_block<LB>();
-    for (int layer = 0; layer < layers; ++layer) {
-      const bool odd = layer & 1;
-      layer_fht<LB>(v, lds, t, odd);
-      if (odd)
-        sign_scale<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(0), S::nb(0), scale);
-      else
-        sign_scale<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(S::N - 1), S::nb(S::N - 1), scale);
-    }
-    // store from the layout the last layer ended in
-    const int64_t base = block * Gm::B;
-    const int64_t lo = start - base > 0 ? start - base : 0;
-    const int64_t hi = stop - base < Gm::B ? stop - base : Gm::B;
-    auto store = [&](int glo, int gnb) {
-      if (!active) return;
-      const int pb = group_pos<LB, 5>(t, 0, glo, gnb);
-#pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
-        if (p >= lo && p < hi) out(base + p - start, v[r]);
-      }
-    };
-    if (!(layers & 1)) {
-      store(S::lo(0), S::nb(0));
-    } else if constexpr (S::kLastStores) {
-      store(S::lo(S::N - 1), S::nb(S::N - 1));
-    } else {
-      exchange<LB>(v, lds, t, S::lo(S::N - 1), S::nb(S::N - 1), S::lo(0), S::nb(0));
-      store(S::lo(0), S::nb(0));
-    }
-  }
-}
-
-// Backward: adjoint chain D_0 H D_1 ... H D_L on grad scattered into the block.
-// Writes partial[slot * n + p] (float32) for p < n, or the final gradient in T
-// when `direct` (a single block).
-template <int LB, class T, class Load>
-__device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ partial, T* __restrict__ grad_latent,
-                                               int n, int64_t first_block, int64_t slot, int64_t nblocks,
-                                               int64_t start, int64_t stop, uint32_t seed32, int layers, int direct,
-                                               float* smem) {
-  using Gm = Geo<LB>;
-  using S = BlockSeq<LB>;
-  if constexpr (Gm::NG <= 1) {  // B <= 2^5
-    block_bwd_small<LB, T>(grad, partial, grad_latent, n, first_block, slot, nblocks, start, stop, seed32, layers,
-                           direct);
-  } else {
-    const int gi = threadIdx.x >> Gm::LT;
-    const int t = threadIdx.x & (Gm::TB - 1);
-    const bool active = slot < nblocks;
-    const int64_t block = first_block + (active ? slot : 0);
-    float* lds = BlockLds<LB>::data(smem, gi);
-    uint32_t* tab = BlockLds<LB>::table(smem, gi);
-    fill_sign_table<LB>(tab, block_key(seed32, block), t, layers);
-    const int64_t base = block * Gm::B;
-    const int64_t lo = start - base > 0 ? start - base : 0;
-    const int64_t hi = stop - base < Gm::B ? stop - base : Gm::B;
-    float v[32];
-#pragma unroll
-    for (int r = 0; r < 32; ++r) {
-      const int p = r * Gm::TB + t;
-      v[r] = (active && p >= lo && p < hi) ? grad(base + p - start) : 0.0f;
-    }
-    __syncthreads();  // the sign table is complete
-    sign_scale<LB>(v, tab + layers * Gm::TB, t, S::lo(0), S::nb(0), 1.0f);
-    const float scale = inv_sqrt_block<LB>();
-    for (int i = 0; i < layers; ++i) {
-      const bool odd = i & 1;
-      layer_fht<LB>(v, lds, t, odd);
-      const uint32_t* words = tab + (layers - 1 - i) * Gm::TB;
-      if (odd)
-        sign_scale<LB>(v, words, t, S::lo(0), S::nb(0), scale);
-      else
-        sign_scale<LB>(v, words, t, S::lo(S::N - 1), S::nb(S::N - 1), scale);
-    }
-    auto write = [&](int glo, int gnb) {
-      if (!active) return;
-      const int pb = group_pos<LB, 5>(t, 0, glo, gnb);
-#pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
-        if (p < n) {
-          if (direct)
-            grad_latent[p] = from_f32<T>(v[r]);
-          else
-            partial[slot * (int64_t)n + p] = v[r];
-        }
-      }
-    };
-    if (!(layers & 1)) {
-      write(S::lo(0), S::nb(0));
-    } else if constexpr (S::kLastStores) {
-      write(S::lo(S::N - 1), S::nb(S::N - 1));
-    } else {
-      exchange<LB>(v, lds, t, S::lo(S::N - 1), S::nb(S::N - 1), S::lo(0), S::nb(0));
-      write(S::lo(0), S::nb(0));
-    }
-  }
-}
-
 // Element access of the per-generator launches: the slice in the latent dtype.
+// Element access of the per-generator launches: the slice in the latent dtype,
+// through a buffer resource over one block's range (`range` + call) or by
+// element index (`at`, for blocks that share a wave).
 template <class T>
 struct SliceStore {
   T* out;
-  __device__ void operator()(int64_t i, float v) const { out[i] = from_f32<T>(v); }
+  __device__ __amdgpu_buffer_rsrc_t range(int64_t first, int64_t count) const {
+    return tile_rsrc(out + first, (uint64_t)count * sizeof(T));
+  }
+  __device__ void operator()(__amdgpu_buffer_rsrc_t r, int i, float v) const { buf_store<T>(v, r, i); }
+  __device__ void at(int64_t i, float v) const { out[i] = from_f32<T>(v); }
 };
 template <class T>
 struct SliceLoad {
   const T* g;
-  __device__ float operator()(int64_t i) const { return to_f32(g[i]); }
+  __device__ __amdgpu_buffer_rsrc_t range(int64_t first, int64_t count) const {
+    return tile_rsrc(g + first, (uint64_t)count * sizeof(T));
+  }
+  __device__ float operator()(__amdgpu_buffer_rsrc_t r, int i) const { return buf_load<T>(r, i); }
+  __device__ float at(int64_t i) const { return to_f32(g[i]); }
 };
 
 template <int LB, class T>
@@ -344,63 +63,8 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
                                                              int direct) {
   __shared__ float smem[BlockLds<LB>::FLOATS];
   const int64_t slot = (int64_t)blockIdx.x * Geo<LB>::G + (threadIdx.x >> Geo<LB>::LT);
-  block_bwd_slot<LB, T>(SliceLoad<T>{grad}, partial, grad_latent, n, first_block, slot, nblocks, start, stop,
+  block_bwd_slot<LB, T>(SliceLoad<T>{grad}, partial, n, grad_latent, n, first_block, slot, nblocks, start, stop,
                         seed32, layers, direct, smem);
-}
-
-// ---------------------------------------------------------------- grouped
-
-// Element access of the grouped weight jobs.  Store: the generator value in the
-// latent dtype T, times the weight scale rounded to T again, then cast to the
-// weight dtype.  Load: the weight gradient cast to T first.
-template <class T>
-__device__ __forceinline__ float round_to(float v) {
-  return to_f32(from_f32<T>(v));
-}
-
-template <class T>
-struct WeightStore {
-  void* out;
-  int code;
-  float scale;
-  __device__ void operator()(int64_t i, float v) const {
-    const float y = round_to<T>(round_to<T>(v) * scale);
-    if (code == kF32) static_cast<float*>(out)[i] = y;
-    else if (code == kF16) static_cast<f16*>(out)[i] = from_f32<f16>(y);
-    else static_cast<bf16*>(out)[i] = from_f32<bf16>(y);
-  }
-};
-template <class T>
-struct WeightGradLoad {
-  const void* g;
-  int code;
-  __device__ float operator()(int64_t i) const {
-    float v;
-    if (code == kF32) v = static_cast<const float*>(g)[i];
-    else if (code == kF16) v = to_f32(static_cast<const f16*>(g)[i]);
-    else v = to_f32(static_cast<const bf16*>(g)[i]);
-    return round_to<T>(v);
-  }
-};
-
-template <int LB, class T>
-__global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_fwd_grouped(const GroupTable g) {
-  __shared__ float smem[BlockLds<LB>::FLOATS];
-  const int j = group_job(g, (int)blockIdx.x);
-  const GroupJob& jb = g.job[j];
-  const int64_t slot = (int64_t)(blockIdx.x - g.prefix[j]) * Geo<LB>::G + (threadIdx.x >> Geo<LB>::LT);
-  block_fwd_slot<LB, T>(static_cast<const T*>(jb.src), WeightStore<T>{jb.dst, jb.wdtype, jb.scale}, jb.n, 0, slot,
-                        jb.nblocks, 0, jb.size, jb.seed32, jb.layers, smem);
-}
-
-template <int LB, class T>
-__global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd_grouped(const GroupTable g) {
-  __shared__ float smem[BlockLds<LB>::FLOATS];
-  const int j = group_job(g, (int)blockIdx.x);
-  const GroupJob& jb = g.job[j];
-  const int64_t slot = (int64_t)(blockIdx.x - g.prefix[j]) * Geo<LB>::G + (threadIdx.x >> Geo<LB>::LT);
-  block_bwd_slot<LB, T>(WeightGradLoad<T>{jb.src, jb.wdtype}, jb.part, static_cast<T*>(nullptr), jb.n, 0, slot,
-                        jb.nblocks, 0, jb.size, jb.seed32, jb.layers, 0, smem);
 }
 
 // grad_latent[p] = sum_b part[b * stride + p], blocks in order.
@@ -490,8 +154,8 @@ __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_grouped(const Grou
   const int c0 = (blockIdx.x - g.prefix[j]) * kRedCols + 2 * (threadIdx.x & 63);
   float t0, t1;
   // 8-byte row loads need even row strides (part is 256-byte aligned)
-  const bool done = (n % 2 == 0) ? reduce_columns<true>(jb.part, jb.nblocks, n, n, c0, sums, t0, t1)
-                                 : reduce_columns<false>(jb.part, jb.nblocks, n, n, c0, sums, t0, t1);
+  const bool done = (jb.stride % 2 == 0) ? reduce_columns<true>(jb.part, jb.nblocks, jb.stride, n, c0, sums, t0, t1)
+                                         : reduce_columns<false>(jb.part, jb.nblocks, jb.stride, n, c0, sums, t0, t1);
   if (!done) return;
   T* dst = static_cast<T*>(jb.dst);
   if (c0 < n) grad_store<T>(dst, c0, t0, jb.scale, jb.accumulate);
@@ -562,32 +226,6 @@ __device__ __forceinline__ void tile_fht_bits(float* lds, int tid) {
     for (int r = 0; r < 32; ++r) lds[base + lds_index(group_pos<kTileLog, 5>(0, r, lo, nb))] = v[r];
   }
   __syncthreads();
-}
-
-// Element loads / stores through a raw buffer resource: element index i of the
-// buffer, out-of-range (including negative) indices read 0 / are dropped.  The
-// whole offset goes in the per-lane offset: the range check covers only that
-// part (a scalar offset is added after it).  Buffers stay below 2 GiB.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
-                                           (int)(bytes < 0x80000000ull ? bytes : 0x80000000ull), 0x00020000);
-}
-template <class T>
-__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, int i) {
-  if constexpr (sizeof(T) == 4) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, i * 4, 0, 0));
-  } else {
-    const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, i * 2, 0, 0);
-    return to_f32(__builtin_bit_cast(T, h));
-  }
-}
-template <class T>
-__device__ __forceinline__ void buf_store(float v, __amdgpu_buffer_rsrc_t r, int i) {
-  if constexpr (sizeof(T) == 4) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, i * 4, 0, 1 | 16);
-  } else {
-    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), r, i * 2, 0, 1 | 16);
-  }
 }
 
 // One pass of the tiled schedule (run_tiles).  A tile is 2^15 positions of one
@@ -805,43 +443,6 @@ static hipError_t run_typed(const BfhtArgs& a, hipStream_t s, bool fwd) {
   if (a.log_block <= kTileLog)
     return dispatch_block<T>(a.log_block, fwd, a, s, std::make_integer_sequence<int, kTileLog + 1>{});
   return run_tiles<T>(a, s, fwd);
-}
-
-int group_slots_per_wg(int log_block) {
-  // Geo<LB>::G: blocks of 2^LB that one workgroup transforms together
-  const int tb = 1 << (log_block - (log_block < 5 ? log_block : 5));
-  return (tb < 256 ? 256 : tb) / tb;
-}
-
-template <int LB, class T>
-static hipError_t launch_block_grouped_lb(const GroupTable& g, hipStream_t s, bool fwd) {
-  if (group_slots_per_wg(LB) != Geo<LB>::G) return hipErrorInvalidValue;  // the planner's prefix unit
-  const dim3 grid((unsigned)g.prefix[g.count]), block(Geo<LB>::WG);
-  if (fwd)
-    hipLaunchKernelGGL((bfht_block_fwd_grouped<LB, T>), grid, block, 0, s, g);
-  else
-    hipLaunchKernelGGL((bfht_block_bwd_grouped<LB, T>), grid, block, 0, s, g);
-  return hipGetLastError();
-}
-
-template <class T, int... LBs>
-static hipError_t dispatch_grouped(const GroupTable& g, int LB, hipStream_t s, bool fwd,
-                                   std::integer_sequence<int, LBs...>) {
-  using Fn = hipError_t (*)(const GroupTable&, hipStream_t, bool);
-  static const Fn table[] = {&launch_block_grouped_lb<LBs, T>...};
-  return table[LB](g, s, fwd);
-}
-
-hipError_t launch_block_grouped(const GroupTable& g, int dtype, int log_block, hipStream_t s, bool fwd) {
-  if (g.count <= 0 || g.prefix[g.count] == 0) return hipSuccess;
-  if (log_block < 0 || log_block > kTileLog) return hipErrorInvalidValue;
-  const auto seq = std::make_integer_sequence<int, kTileLog + 1>{};
-  switch (dtype) {
-    case kF32: return dispatch_grouped<float>(g, log_block, s, fwd, seq);
-    case kF16: return dispatch_grouped<f16>(g, log_block, s, fwd, seq);
-    case kBF16: return dispatch_grouped<bf16>(g, log_block, s, fwd, seq);
-  }
-  return hipErrorInvalidValue;
 }
 
 hipError_t launch_reduce_grouped(const GroupTable& g, int dtype, hipStream_t s) {

@@ -107,9 +107,10 @@ constexpr int kGroupMaxJobs = 32;
 struct GroupJob {
   const void* src;   // forward: latent [n]; backward: grad of the weight [size] (weight dtype)
   void* dst;         // forward: weight [size] (weight dtype); backward: grad_latent [n]
-  float* part;       // backward: nblocks partial rows of n floats
+  float* part;       // backward: nblocks partial rows of n floats, `stride` floats apart
   int64_t size;
   int32_t n;
+  int32_t stride;    // n rounded up to 32 (128-byte aligned rows)
   int32_t nblocks;   // ceil(size / B)
   uint32_t seed32;
   int32_t layers;
@@ -123,9 +124,11 @@ struct GroupTable {
   int32_t prefix[kGroupMaxJobs + 1];
   GroupJob job[kGroupMaxJobs];
 };
-// Whole-block jobs (B <= 2^15) of one latent dtype and block size.
+// Whole-block jobs (B <= 2^15) of one latent dtype, weight dtype and block size
+// (bfht_grouped_kernels.hip).
 int group_slots_per_wg(int log_block);
-hipError_t launch_block_grouped(const GroupTable& g, int dtype, int log_block, hipStream_t s, bool fwd);
+hipError_t launch_block_grouped(const GroupTable& g, int dtype, int wdtype, int log_block, hipStream_t s,
+                                bool fwd);
 // bfloat16 jobs of block 2^15 and one layer count on the matrix cores.
 hipError_t launch_mfma15_grouped(const GroupTable& g, int layers, hipStream_t s, bool fwd);
 // Block sums of backward jobs of one latent dtype (prefix in 128-column tiles).

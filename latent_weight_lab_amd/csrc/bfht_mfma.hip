@@ -192,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd_grouped(const GroupT
   f32x16 acc[kTiles];
   uint32_t nw[4];
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
-  write_partial_row<L, false>(acc, nw, x, lds, jb.part + slot * (int64_t)jb.n, jb.n, 1.0f);
+  write_partial_row<L, false>(acc, nw, x, lds, jb.part + slot * (int64_t)jb.stride, jb.n, 1.0f);
 }
 
 }  // namespace

@@ -270,8 +270,8 @@ def test_flush_workspace_size():
     def al(v):
         return (v + 255) // 256 * 256
 
-    # one float32 partial row of n per block, per job, 256-byte aligned
-    assert got == al(72 * 23593 * 4) + al(72 * 5898 * 4) + al(2 * 3 * 4)
+    # one float32 partial row per block, rows 128-byte aligned (n rounded up to 32), per job 256-byte aligned
+    assert got == al(72 * 23616 * 4) + al(72 * 5920 * 4) + al(2 * 32 * 4)
     bad = (N.WeightJob * 1)(weight_job(40000, 100))
     assert N.lib().lwl_bfht_flush_weight_grads_workspace_size(bad, 1) == 0
 
