@@ -88,10 +88,14 @@ __device__ __forceinline__ bool reduce_columns(const float* __restrict__ part, i
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool has0 = c0 < n, has1 = c0 + 1 < n;
   float a0 = 0.0f, a1 = 0.0f;
+  // columns past n read column 0 of the row (always valid) and are zeroed by a
+  // select: no branch around the loads, so kRedDepth of them are in flight
+  const int c0s = has0 ? c0 : 0, c1s = has1 ? c0 + 1 : 0;
   auto row = [&](int64_t b) -> float2 {
-    const float* r = part + b * stride + c0;
-    if (kPairs && has1) return *reinterpret_cast<const float2*>(r);
-    return float2{has0 ? r[0] : 0.0f, has1 ? r[1] : 0.0f};
+    const float* r = part + b * stride;
+    if (kPairs && has1) return *reinterpret_cast<const float2*>(r + c0);
+    const float x0 = r[c0s], x1 = r[c1s];
+    return float2{has0 ? x0 : 0.0f, has1 ? x1 : 0.0f};
   };
   int64_t b = wave;
   for (; b + (int64_t)kRedWaves * (kRedDepth - 1) < nblocks; b += (int64_t)kRedWaves * kRedDepth) {

@@ -43,13 +43,17 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_mix_rows(const T* x, T* out,
   for (int64_t rg = blockIdx.x; rg < groups; rg += gridDim.x) {
     const int64_t row = rg * Gm::G + gi;
     const bool active = row < rows;
-    const T* xr = x + row * features;
+    const T* xr = x + (active ? row : 0) * features;
     T* orow = out + row * features;
     float v[Gm::E];
+    // loads from a valid index (position 0 of the row stands in for the padding)
+    // and a select, so all E loads are in flight at once
 #pragma unroll
     for (int r = 0; r < Gm::E; ++r) {
       const int p = r * Gm::TB + t;
-      v[r] = flip((active && p < features) ? to_f32(xr[p]) : 0.0f, r);
+      const bool ok = active && p < features;
+      const float xv = to_f32(xr[ok ? p : 0]);
+      v[r] = flip(ok ? xv : 0.0f, r);
     }
     fht_coalesced<LB, Gm::LE>(v, lds, t);
     if (active) {
