@@ -171,22 +171,30 @@ __device__ __forceinline__ void exchange(float (&v)[32], float* lds, int t, int 
   for (int r = 0; r < 32; ++r) v[r] = lds[group_lds<LB, 5>(rb, r, lo_b, nb_b)];
 }
 
-// v[r] *= ±scale by the sign bit of its position in layout (lo, nb): word p >> 5
-// of the layer's table, bit p & 31 (set: +).  Position = per-thread base OR a
-// per-register constant (disjoint bits), so word index and bit split the same way.
+// Sign layer in layout (lo, nb): v[r] negated where the bit of its position is
+// clear (word p >> 5 of the layer's table, bit p & 31), as an XOR of the float's
+// sign bit.  Position = per-thread base OR a per-register constant (disjoint
+// bits), so word index and bit split the same way.  The 2^(-LB/2) of every layer
+// is applied once, at the end (transform_scale).
 template <int LB>
-__device__ __forceinline__ void sign_scale(float (&v)[32], const uint32_t* words, int t, int lo, int nb,
-                                           float scale) {
+__device__ __forceinline__ void sign_flip(float (&v)[32], const uint32_t* words, int t, int lo, int nb) {
   const int base = group_pos<LB, 5>(t, 0, lo, nb);
-  const uint32_t pos = __float_as_uint(scale), neg = pos ^ 0x80000000u;
 #pragma unroll
   for (int r = 0; r < 32; ++r) {
     const int c = group_pos<LB, 5>(0, r, lo, nb);
-    const uint32_t w = words[(base >> 5) + (c >> 5)];
+    const uint32_t w = ~words[(base >> 5) + (c >> 5)];
     const int bit = (base & 31) | (c & 31);
-    const uint32_t m = (uint32_t)((int32_t)(w << (31 - bit)) >> 31);
-    v[r] *= __uint_as_float((m & pos) | (~m & neg));
+    v[r] = __uint_as_float(__float_as_uint(v[r]) ^ ((w << (31 - bit)) & 0x80000000u));
   }
+}
+
+// 2^(-LB * layers / 2): the normalization of `layers` transforms of order 2^LB,
+// exact but for one rounding of 1/sqrt(2) when LB * layers is odd.
+template <int LB>
+__device__ __forceinline__ float transform_scale(int layers) {
+  const int e = LB * layers;
+  const float p2 = __builtin_ldexpf(1.0f, -(e >> 1));
+  return (e & 1) ? 0.70710678118654752440f * p2 : p2;
 }
 
 // One layer's transform (unnormalized), groups forward (even layers: top first,
@@ -242,16 +250,16 @@ __device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Sto
 #pragma unroll
     for (int r = 0; r < 32; ++r) v[r] = buf_load<T>(lat_r, r * Gm::TB + t);
     __syncthreads();  // the sign table is complete
-    sign_scale<LB>(v, tab, t, S::lo(0), S::nb(0), 1.0f);
-    const float scale = inv_sqrt_block<LB>();
+    sign_flip<LB>(v, tab, t, S::lo(0), S::nb(0));
     for (int layer = 0; layer < layers; ++layer) {
       const bool odd = layer & 1;
       layer_fht<LB>(v, lds, t, odd);
       if (odd)
-        sign_scale<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(0), S::nb(0), scale);
+        sign_flip<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(0), S::nb(0));
       else
-        sign_scale<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(S::N - 1), S::nb(S::N - 1), scale);
+        sign_flip<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(S::N - 1), S::nb(S::N - 1));
     }
+    const float scale = transform_scale<LB>(layers);
     // store from the layout the last layer ended in
     const int64_t base = block * Gm::B;
     const int64_t lo = start - base > 0 ? start - base : 0;
@@ -264,12 +272,12 @@ __device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Sto
         // positions outside [lo, hi) dropped by its range check
         const auto out_r = out.range(base + lo - start, hi - lo);
 #pragma unroll
-        for (int r = 0; r < 32; ++r) out(out_r, pb + group_pos<LB, 5>(0, r, glo, gnb) - (int)lo, v[r]);
+        for (int r = 0; r < 32; ++r) out(out_r, pb + group_pos<LB, 5>(0, r, glo, gnb) - (int)lo, v[r] * scale);
       } else {
 #pragma unroll
         for (int r = 0; r < 32; ++r) {
           const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
-          if (p >= lo && p < hi) out.at(base + p - start, v[r]);
+          if (p >= lo && p < hi) out.at(base + p - start, v[r] * scale);
         }
       }
     };
@@ -326,17 +334,17 @@ __device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ pa
       }
     }
     __syncthreads();  // the sign table is complete
-    sign_scale<LB>(v, tab + layers * Gm::TB, t, S::lo(0), S::nb(0), 1.0f);
-    const float scale = inv_sqrt_block<LB>();
+    sign_flip<LB>(v, tab + layers * Gm::TB, t, S::lo(0), S::nb(0));
     for (int i = 0; i < layers; ++i) {
       const bool odd = i & 1;
       layer_fht<LB>(v, lds, t, odd);
       const uint32_t* words = tab + (layers - 1 - i) * Gm::TB;
       if (odd)
-        sign_scale<LB>(v, words, t, S::lo(0), S::nb(0), scale);
+        sign_flip<LB>(v, words, t, S::lo(0), S::nb(0));
       else
-        sign_scale<LB>(v, words, t, S::lo(S::N - 1), S::nb(S::N - 1), scale);
+        sign_flip<LB>(v, words, t, S::lo(S::N - 1), S::nb(S::N - 1));
     }
+    const float scale = transform_scale<LB>(layers);
     auto write = [&](int glo, int gnb) {
       if (!active) return;
       const int pb = group_pos<LB, 5>(t, 0, glo, gnb);
@@ -348,9 +356,9 @@ __device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ pa
         for (int r = 0; r < 32; ++r) {
           const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
           if (direct)
-            buf_store<T>(v[r], d_r, p);
+            buf_store<T>(v[r] * scale, d_r, p);
           else
-            buf_store<float>(v[r], d_r, p);
+            buf_store<float>(v[r] * scale, d_r, p);
         }
       } else {
 #pragma unroll
@@ -358,9 +366,9 @@ __device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ pa
           const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
           if (p < n) {
             if (direct)
-              grad_latent[p] = from_f32<T>(v[r]);
+              grad_latent[p] = from_f32<T>(v[r] * scale);
             else
-              partial[slot * stride + p] = v[r];
+              partial[slot * stride + p] = v[r] * scale;
           }
         }
       }
