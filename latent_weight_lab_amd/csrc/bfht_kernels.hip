@@ -76,71 +76,100 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
 // loads in flight and leaves most of the chip idle for latent lengths of a
 // few 10^4.)
 constexpr int kRedWaves = 8;
-constexpr int kRedCols = 128;
 constexpr int kRedDepth = 16;
 
-// Column pair c0, c0 + 1 of the sum; every thread of the workgroup calls it,
-// and wave 0 returns true with the totals.
-template <bool kPairs>
+template <int kVec>
+struct RedVec;
+template <>
+struct RedVec<1> { typedef float type; };
+template <>
+struct RedVec<2> { typedef float2 type; };
+template <>
+struct RedVec<4> { typedef float4 type; };
+
+// Columns c0 .. c0 + kVec - 1 of the sum (kVec-wide loads when the row stride
+// allows); every thread of the workgroup calls it, and wave 0 returns true with
+// the totals.  Wave w adds rows w, w + 8, w + 16, ... in ascending order with
+// kRedDepth row loads in flight (rows past the end are loaded from row 0 and
+// not added, so the loads need no branch), and wave 0 adds the 8 wave sums in
+// wave order: the result does not depend on kVec or on timing.
+template <int kVec>
 __device__ __forceinline__ bool reduce_columns(const float* __restrict__ part, int64_t nblocks, int64_t stride,
-                                               int n, int c0, float (&sums)[kRedWaves][2][64], float& t0,
-                                               float& t1) {
+                                               int n, int c0, float (&sums)[kRedWaves][kVec][64],
+                                               float (&t)[kVec]) {
+  typedef typename RedVec<kVec>::type V;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool has0 = c0 < n, has1 = c0 + 1 < n;
-  float a0 = 0.0f, a1 = 0.0f;
-  // columns past n read column 0 of the row (always valid) and are zeroed by a
-  // select: no branch around the loads, so kRedDepth of them are in flight
-  const int c0s = has0 ? c0 : 0, c1s = has1 ? c0 + 1 : 0;
-  auto row = [&](int64_t b) -> float2 {
-    const float* r = part + b * stride;
-    if (kPairs && has1) return *reinterpret_cast<const float2*>(r + c0);
-    const float x0 = r[c0s], x1 = r[c1s];
-    return float2{has0 ? x0 : 0.0f, has1 ? x1 : 0.0f};
+  float a[kVec];
+#pragma unroll
+  for (int e = 0; e < kVec; ++e) a[e] = 0.0f;
+  auto lanes = [](const V& v, int e) -> float {
+    if constexpr (kVec == 1) return v;
+    else return reinterpret_cast<const float*>(&v)[e];
   };
-  int64_t b = wave;
-  for (; b + (int64_t)kRedWaves * (kRedDepth - 1) < nblocks; b += (int64_t)kRedWaves * kRedDepth) {
-    float2 v[kRedDepth];
+  if (c0 + kVec <= n) {
+    // every column of the lane is in range: vector loads
+    for (int64_t b0 = wave; b0 < nblocks; b0 += (int64_t)kRedWaves * kRedDepth) {
+      V v[kRedDepth];
 #pragma unroll
-    for (int j = 0; j < kRedDepth; ++j) v[j] = row(b + (int64_t)kRedWaves * j);
+      for (int j = 0; j < kRedDepth; ++j) {
+        const int64_t b = b0 + (int64_t)kRedWaves * j;
+        v[j] = *reinterpret_cast<const V*>(part + (b < nblocks ? b : 0) * stride + c0);
+      }
 #pragma unroll
-    for (int j = 0; j < kRedDepth; ++j) {
-      a0 += v[j].x;
-      a1 += v[j].y;
+      for (int j = 0; j < kRedDepth; ++j) {
+        const bool ok = b0 + (int64_t)kRedWaves * j < nblocks;
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) a[e] = ok ? a[e] + lanes(v[j], e) : a[e];
+      }
+    }
+  } else {
+    // the tail of the row: element loads, columns past n read column 0
+    for (int64_t b0 = wave; b0 < nblocks; b0 += (int64_t)kRedWaves * kRedDepth) {
+      float v[kRedDepth][kVec];
+#pragma unroll
+      for (int j = 0; j < kRedDepth; ++j) {
+        const int64_t b = b0 + (int64_t)kRedWaves * j;
+        const float* r = part + (b < nblocks ? b : 0) * stride;
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) v[j][e] = r[c0 + e < n ? c0 + e : 0];
+      }
+#pragma unroll
+      for (int j = 0; j < kRedDepth; ++j) {
+        const bool ok = b0 + (int64_t)kRedWaves * j < nblocks;
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) a[e] = ok ? a[e] + v[j][e] : a[e];
+      }
     }
   }
-  for (; b < nblocks; b += kRedWaves) {
-    const float2 v = row(b);
-    a0 += v.x;
-    a1 += v.y;
-  }
-  sums[wave][0][lane] = a0;
-  sums[wave][1][lane] = a1;
+#pragma unroll
+  for (int e = 0; e < kVec; ++e) sums[wave][e][lane] = a[e];
   __syncthreads();
   if (wave != 0) return false;
-  t0 = 0.0f;
-  t1 = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kRedWaves; ++w) {
-    t0 += sums[w][0][lane];
-    t1 += sums[w][1][lane];
+  for (int e = 0; e < kVec; ++e) {
+    t[e] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kRedWaves; ++w) t[e] += sums[w][e][lane];
   }
   return true;
 }
 
-template <class T, bool kPairs>
+template <class T, int kVec>
 __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_blocks(const float* __restrict__ part,
                                                                      int64_t nblocks, int64_t stride, int n,
                                                                      T* __restrict__ grad_latent) {
-  __shared__ float sums[kRedWaves][2][64];
-  const int c0 = blockIdx.x * kRedCols + 2 * (threadIdx.x & 63);
-  float t0, t1;
-  if (!reduce_columns<kPairs>(part, nblocks, stride, n, c0, sums, t0, t1)) return;
-  if (c0 < n) grad_latent[c0] = from_f32<T>(t0);
-  if (c0 + 1 < n) grad_latent[c0 + 1] = from_f32<T>(t1);
+  __shared__ float sums[kRedWaves][kVec][64];
+  const int c0 = (blockIdx.x * 64 + (threadIdx.x & 63)) * kVec;
+  float t[kVec];
+  if (!reduce_columns<kVec>(part, nblocks, stride, n, c0, sums, t)) return;
+#pragma unroll
+  for (int e = 0; e < kVec; ++e)
+    if (c0 + e < n) grad_latent[c0 + e] = from_f32<T>(t[e]);
 }
 
 // Grouped block sums with the flush epilogue: r = T(T(sum) * scale), added to
-// the destination in T when the job accumulates.
+// the destination in T when the job accumulates.  Rows are 128-byte aligned
+// (the planner rounds the stride up to 32 floats), so loads are 16 bytes wide.
 template <class T>
 __device__ __forceinline__ void grad_store(T* dst, int i, float sum, float scale, int accumulate) {
   float r = round_to<T>(round_to<T>(sum) * scale);
@@ -150,31 +179,38 @@ __device__ __forceinline__ void grad_store(T* dst, int i, float sum, float scale
 
 template <class T>
 __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_grouped(const GroupTable g) {
-  static_assert(kGroupReduceCols == kRedCols, "grouped prefix counts reduce tiles");
-  __shared__ float sums[kRedWaves][2][64];
+  static_assert(kGroupReduceCols == 64 * 4, "grouped prefix counts reduce tiles of 4 columns per lane");
+  __shared__ float sums[kRedWaves][4][64];
   const int j = group_job(g, (int)blockIdx.x);
   const GroupJob& jb = g.job[j];
   const int n = jb.n;
-  const int c0 = (blockIdx.x - g.prefix[j]) * kRedCols + 2 * (threadIdx.x & 63);
-  float t0, t1;
-  // 8-byte row loads need even row strides (part is 256-byte aligned)
-  const bool done = (jb.stride % 2 == 0) ? reduce_columns<true>(jb.part, jb.nblocks, jb.stride, n, c0, sums, t0, t1)
-                                         : reduce_columns<false>(jb.part, jb.nblocks, jb.stride, n, c0, sums, t0, t1);
-  if (!done) return;
+  const int c0 = ((blockIdx.x - g.prefix[j]) * 64 + (threadIdx.x & 63)) * 4;
+  float t[4];
+  if (!reduce_columns<4>(jb.part, jb.nblocks, jb.stride, n, c0, sums, t)) return;
   T* dst = static_cast<T*>(jb.dst);
-  if (c0 < n) grad_store<T>(dst, c0, t0, jb.scale, jb.accumulate);
-  if (c0 + 1 < n) grad_store<T>(dst, c0 + 1, t1, jb.scale, jb.accumulate);
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (c0 + e < n) grad_store<T>(dst, c0 + e, t[e], jb.scale, jb.accumulate);
+}
+
+template <class T, int kVec>
+static void launch_reduce_vec(const float* part, int64_t nblocks, int64_t stride, int64_t n, T* dst, hipStream_t s) {
+  const dim3 grid((unsigned)((n + 64 * kVec - 1) / (64 * kVec))), block(64 * kRedWaves);
+  hipLaunchKernelGGL((bfht_reduce_blocks<T, kVec>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
 }
 
 template <class T>
 static hipError_t launch_reduce(const float* part, int64_t nblocks, int64_t stride, int64_t n, T* dst,
                                 hipStream_t s) {
-  const dim3 grid((unsigned)((n + kRedCols - 1) / kRedCols)), block(64 * kRedWaves);
-  // 8-byte row loads need even column offsets in every row: part is 256-byte aligned
-  if (stride % 2 == 0)
-    hipLaunchKernelGGL((bfht_reduce_blocks<T, true>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
+  // The widest row loads the stride allows (part is 256-byte aligned) that still
+  // give every CU a workgroup: 64 * kVec columns per workgroup.
+  auto fits = [&](int v) { return stride % v == 0 && (n + 64 * v - 1) / (64 * v) >= 256; };
+  if (fits(4))
+    launch_reduce_vec<T, 4>(part, nblocks, stride, n, dst, s);
+  else if (fits(2))
+    launch_reduce_vec<T, 2>(part, nblocks, stride, n, dst, s);
   else
-    hipLaunchKernelGGL((bfht_reduce_blocks<T, false>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
+    launch_reduce_vec<T, 1>(part, nblocks, stride, n, dst, s);
   return hipGetLastError();
 }
 

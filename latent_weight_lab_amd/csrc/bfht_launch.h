@@ -131,8 +131,8 @@ hipError_t launch_block_grouped(const GroupTable& g, int dtype, int wdtype, int 
                                 bool fwd);
 // bfloat16 jobs of block 2^15 and one layer count on the matrix cores.
 hipError_t launch_mfma15_grouped(const GroupTable& g, int layers, hipStream_t s, bool fwd);
-// Block sums of backward jobs of one latent dtype (prefix in 128-column tiles).
-constexpr int kGroupReduceCols = 128;
+// Block sums of backward jobs of one latent dtype (prefix in 256-column tiles).
+constexpr int kGroupReduceCols = 256;
 hipError_t launch_reduce_grouped(const GroupTable& g, int dtype, hipStream_t s);
 
 // One generator of a grouped call (validated by the C ABI).
