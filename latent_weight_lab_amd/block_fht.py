@@ -91,21 +91,20 @@ def block_fht_grad_latent(latent: torch.Tensor, grad_out: torch.Tensor, size: in
 
 
 def block_fht_linear_forward(input: torch.Tensor, latent: torch.Tensor, out_features: int, layers: int, seed: int,
-                             weight_scale: float = 1.0, fused: bool | None = None) -> torch.Tensor:
+                             weight_scale: float = 1.0, fused: bool = True) -> torch.Tensor:
     """``input @ (weight_scale * W)^T`` with ``W = BlockFHT(latent)[: in*out].view(out, in)``
     (reference ``block_fht.py:251-288``).
 
-    Two routes compute it.  The fused kernel (``fused=True``, bf16 latents of block
-    2^15 with ``in_features % 8 == 0``, 528..5120) generates W on chip for every
-    token range and never stores it.  The default generates W once into a transient
-    buffer (one launch, ``weight_scale`` folded in) and calls ``F.linear`` — the
-    reference's own route at these shapes (its fused gate, ``:263-273``, needs
-    ``B <= 16384`` and ``B % in == 0``).  On MI355X the second is faster at every
-    batch size measured (1 to 8192 tokens, GPT-2 shapes): the fused kernel
-    regenerates each block per token range and streams x once per block, while
-    the transient W costs ~1 µs of HBM traffic and the GEMM runs on hipBLASLt.
-    With autograd recording and a latent that requires grad, W comes from the
-    differentiable ``block_fht_slice``, as in the reference's fallback.
+    With ``fused=True`` (default) shapes the fused kernel takes (bf16 latents of block
+    2^15, ``in_features % 8 == 0``, 528..5120) generate W on chip for every token range
+    and contract it there, so only the latent and the activations live in HBM.  Other
+    shapes, or ``fused=False``, generate W once into a transient buffer (one launch,
+    ``weight_scale`` folded in) and call ``F.linear`` — the reference's fallback
+    (``:282-288``).  On MI355X that second route is the faster one at every batch size
+    measured (it costs the transient W, ~1 µs of HBM traffic per GPT-2 matrix), so callers
+    that can hold W pass ``fused=False``.  With autograd recording and a latent that
+    requires grad, W comes from the differentiable ``block_fht_slice``, as in the
+    reference's fallback.
     """
     return _generated_linear(input, latent, out_features, layers, seed, weight_scale, None, fused)
 
@@ -316,16 +315,17 @@ class BlockFHTLinear(nn.Module):
                                        self.fused_latent_grad)
 
     def forward_fused(self, input: torch.Tensor, weight_scale: float = 1.0) -> torch.Tensor:
-        """Inference forward (reference ``block_fht.py:482-501``): W generated once into a
-        transient buffer, then one GEMM that also adds the bias when no modulation or
-        residual term comes between; otherwise the reference's sequence of terms."""
+        """Inference forward (reference ``block_fht.py:482-501``): the fused kernel where it
+        applies (W never stored), else W generated once and one GEMM that also adds the
+        bias when no modulation or residual term comes between; otherwise the reference's
+        sequence of terms."""
         if self.output_gain is not None or self.input_gain is not None or self.spectral_core is not None:
             return F.linear(input, self.weight.to(dtype=input.dtype), self.bias)
         g = self.generator
         scale = weight_scale * self.weight_scale
         if self.modulation_alpha == 0.0 and self.residual_base_weight is None:
             # the bias rides in the GEMM's epilogue
-            return _generated_linear(input, g.latent, self.out_features, g.layers, g.seed, scale, self.bias, None)
+            return _generated_linear(input, g.latent, self.out_features, g.layers, g.seed, scale, self.bias, True)
         out = block_fht_linear_forward(input, g.latent, self.out_features, g.layers, g.seed, weight_scale=scale)
         if self.modulation_alpha != 0.0:
             modulation = self.modulation_alpha * self._modulation_offset()
