@@ -153,6 +153,8 @@ lwl::LinearArgs plan_linear(int dtype, int64_t tokens, int64_t in_features, int6
   a.seed32 = fold_seed(seed);
   a.layers = (int)layers;
   a.weight_scale = (float)weight_scale;
+  a.blocks_per_wg = 1;
+  a.blocks_per_wg = lwl::linear_blocks_per_wg(a);
   a.token_splits = lwl::linear_token_splits(a);
   return a;
 }

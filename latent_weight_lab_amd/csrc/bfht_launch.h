@@ -53,6 +53,7 @@ struct LinearArgs {
   uint32_t seed32;
   int layers;
   float weight_scale;
+  int blocks_per_wg;   // generated blocks per workgroup (linear_blocks_per_wg)
   int token_splits;
 };
 
@@ -64,7 +65,8 @@ extern const bool kLinearKernelAvailable;
 // in_features % 8 == 0 and 528 <= in_features <= 5120 (at most 64 output rows per
 // generated block, and their k-major table fits in the LDS).
 bool linear_applicable(int dtype, int log_block, int64_t in_features);
-int linear_token_splits(const LinearArgs& a);
+int linear_blocks_per_wg(const LinearArgs& a);  // needs tokens, in/out features, nblocks_w
+int linear_token_splits(const LinearArgs& a);     // needs blocks_per_wg
 // Workspace of one call: float32 partial dot products of the rows that
 // straddle two blocks, then (for large batches) x re-laid out in MFMA order.
 size_t linear_workspace_bytes(const LinearArgs& a);

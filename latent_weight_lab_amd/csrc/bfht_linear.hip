@@ -43,21 +43,46 @@ __device__ __forceinline__ f32x4v mfma16(u32x4 a, u32x4 b, f32x4v c) {
                                                  0, 0, 0);
 }
 
+// A workgroup contracts a tile of KB consecutive generated blocks (KB = 1, or 2
+// for large batches: twice the rows per loaded x element, half the x traffic).
 // Up to kMaxNT tiles of 16 output rows per block (in_features >= 2^15/(16*kMaxNT - 2)), and the
-// k-major table (4*linear_steps(in) chunks x 16*NT rows x 16 bytes) must fit in the
+// k-major table (4*linear_steps(in) chunks x `pitch` rows x 16 bytes) must fit in the
 // workgroup's LDS (all 160 KiB of a gfx950 CU; the generator's exchange uses the first 128).
 // Together: in_features % 8 == 0 and 528 <= in_features <= 5120.
 constexpr int kMaxNT = 4;
+constexpr int kMaxNT2 = 6;  // two blocks per workgroup: 16-row tiles (register budget)
 constexpr int kLinearLdsBytes = 160 * 1024;
 static_assert(kLinearLdsBytes >= kLdsBytes, "the generator chain runs in the same LDS");
 
-__host__ __device__ constexpr int64_t linear_row_tiles(int64_t in_features) {
-  return ((kB + in_features - 1) / in_features + 1 + 15) / 16;  // incl. two partial rows
+// output rows a tile of kb blocks can touch, incl. the two partial ones
+__host__ __device__ constexpr int64_t linear_rows(int64_t in_features, int kb) {
+  return ((int64_t)kb * kB + in_features - 1) / in_features + 1;
+}
+__host__ __device__ constexpr int64_t linear_row_tiles(int64_t in_features, int kb = 1) {
+  return (linear_rows(in_features, kb) + 15) / 16;
 }
 
 // k steps of 32 per row, rounded up to whole prefetch rounds of kDepth steps
 __host__ __device__ constexpr int linear_steps(int64_t in_features) {
   return (int)(((in_features + kKStep - 1) / kKStep + kDepth - 1) / kDepth * kDepth);
+}
+
+constexpr int64_t linear_table_bytes(int64_t in_features, int64_t pitch) {
+  return (int64_t)4 * linear_steps(in_features) * pitch * 16;
+}
+// Table rows: whole 16-row tiles (zero-padded) when they fit in the LDS, else the
+// exact row count (the kernel masks the last tile's extra rows on read; those
+// reads run up to 15 rows past the table, so an exact table leaves that much
+// LDS free).
+constexpr int64_t kExactPitchSlack = 16 * 16;
+int linear_pitch(int64_t in_features, int kb) {
+  const int64_t padded = 16 * linear_row_tiles(in_features, kb);
+  return (int)(linear_table_bytes(in_features, padded) <= kLinearLdsBytes ? padded : linear_rows(in_features, kb));
+}
+bool linear_pitch_fits(int64_t in_features, int kb) {
+  const int pitch = linear_pitch(in_features, kb);
+  const bool exact = pitch < 16 * linear_row_tiles(in_features, kb);
+  return linear_table_bytes(in_features, pitch) + (exact ? kExactPitchSlack : 0) <= kLinearLdsBytes;
 }
 
 // Batches from this many tokens read x from the tiled copy.
@@ -82,38 +107,43 @@ bool linear_tiled(const LinearArgs& a) {
 }
 
 size_t partial_bytes(const LinearArgs& a) {
-  return ((size_t)a.nblocks_w * 2 * (size_t)a.tokens * sizeof(float) + 255) / 256 * 256;
+  const int64_t ntiles = (a.nblocks_w + a.blocks_per_wg - 1) / a.blocks_per_wg;
+  return ((size_t)ntiles * 2 * (size_t)a.tokens * sizeof(float) + 255) / 256 * 256;
 }
 
+// One workgroup per (4 k steps, token tile): wave w writes the 1 KiB chunk
+// group of step 4 * blockIdx.x + w; lane l reads x[16 T + (l & 15)][32 s + 8 (l >> 4) .. +7].
 __global__ __launch_bounds__(256) void bfht_linear_tile_x(const __bf16* __restrict__ x, u32x4* __restrict__ xt,
-                                                          int tokens, int in_f, int steps, int64_t chunks) {
+                                                          int tokens, int in_f, int steps) {
   const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * in_f * 2));
-  for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < chunks; j += (int64_t)gridDim.x * 256) {
-    const int lane = (int)(j & 63);
-    const int64_t r = j >> 6;
-    const int s = (int)(r % steps);
-    const int t = (int)(r / steps) * kTokTile + (lane & 15);
-    const int k = kKStep * s + 8 * (lane >> 4);
-    const bool in_range = t < tokens && k < in_f;
-    xt[j] = __builtin_amdgcn_raw_buffer_load_b128(x_r, in_range ? (t * in_f + k) * 2 : (int)0x80000000, 0, 0);
-  }
+  const int lane = threadIdx.x & 63;
+  const int s = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tt = blockIdx.y;
+  if (s >= steps) return;
+  const int t = tt * kTokTile + (lane & 15);
+  const int k = kKStep * s + 8 * (lane >> 4);
+  const bool in_range = t < tokens && k < in_f;
+  xt[((int64_t)tt * steps + s) * 64 + lane] =
+      __builtin_amdgcn_raw_buffer_load_b128(x_r, in_range ? (t * in_f + k) * 2 : (int)0x80000000, 0, 0);
 }
 
-template <int L, int NT, bool kTiled>
+template <int L, int NT, bool kTiled, int KB>
 __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __restrict__ x,
                                                                const __bf16* __restrict__ latent,
                                                                __bf16* __restrict__ out,
                                                                float* __restrict__ partial, int tokens,
                                                                int in_f, int out_f, int n, uint32_t seed32,
-                                                               float scale, int token_split) {
+                                                               float scale, int token_split, int64_t nblocks,
+                                                               int pitch) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLinearLdsBytes];
-  const int64_t block = blockIdx.x / token_split;
+  const int64_t tile = blockIdx.x / token_split;  // blocks tile*KB .. tile*KB + KB - 1
   const int split = blockIdx.x % token_split;
-  constexpr int kRows = 16 * NT;  // table rows (output rows of the block, zero-padded)
+  // `pitch` table rows (>= the tile's output rows; 16*NT, zero-padded, when that
+  // fits in the LDS, else exact and the last row tile masked on read)
 
   const int64_t size = (int64_t)in_f * out_f;
-  const int64_t g0 = block * kB;                         // first flat position
-  const int64_t g1 = (g0 + kB < size) ? g0 + kB : size;  // one past the last
+  const int64_t g0 = tile * KB * kB;                          // first flat position
+  const int64_t g1 = (g0 + KB * kB < size) ? g0 + KB * kB : size;  // one past the last
   const int o_first = (int)(g0 / in_f);
   const int o_last = (int)((g1 - 1) / in_f);
   const bool first_partial = (g0 % in_f) != 0;
@@ -123,29 +153,41 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   const int nsteps = linear_steps(in_f);
   const int kchunks = 4 * nsteps;  // 8-element k chunks per table row
 
-  // 1. generate the block (signed bf16) and scatter it into LDS as a k-major
-  //    table of 16-byte chunks: table[kc * kRows + (o - o_first)] holds
-  //    W[o][8*kc .. 8*kc+7]; entries outside the block read 0.
+  // 1. generate the tile's blocks (signed bf16; the first kept in registers
+  //    while the next one's chain uses the LDS) and scatter them into LDS as a
+  //    k-major table of 16-byte chunks: table[kc * pitch + (o - o_first)] holds
+  //    W[o][8*kc .. 8*kc+7]; entries outside the tile read 0.
   u32x4* table = reinterpret_cast<u32x4*>(lds);
   {
-    const Ctx c = make_ctx(seed32, block);
-    u32x4 src[kTiles][2];
-    load_latent(c, latent, n, src);
-    f32x16 acc[kTiles];
-    uint32_t nw[4];
-    run_chain<L>(acc, c, lds, src, [](int i) { return i; }, nw);
-    u32x4 v[8];
+    u32x4 v[KB][8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = out_chunk<L>(acc, nw, c, k);
+    for (int kb = 0; kb < KB; ++kb) {
+      const int64_t block = tile * KB + kb;
+      if (kb > 0) __syncthreads();  // every wave has read the previous chain's last exchange
+      if (block < nblocks) {       // uniform across the workgroup
+        const Ctx c = make_ctx(seed32, block);
+        u32x4 src[kTiles][2];
+        load_latent(c, latent, n, src);
+        f32x16 acc[kTiles];
+        uint32_t nw[4];
+        run_chain<L>(acc, c, lds, src, [](int i) { return i; }, nw);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[kb][k] = out_chunk<L>(acc, nw, c, k);
+      }
+    }
     __syncthreads();  // every wave has read its last exchange
-    for (int i = threadIdx.x; i < kchunks * kRows; i += kThreads) table[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = threadIdx.x; i < kchunks * pitch; i += kThreads) table[i] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
+    const Ctx c = make_ctx(seed32, tile * KB);  // chunk positions do not depend on the block
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int64_t gp = g0 + out_chunk_pos<L>(c, k);
-      if (gp < g1) {
-        const uint32_t o = (uint32_t)(gp / in_f), kc = (uint32_t)(gp - (int64_t)o * in_f) >> 3;
-        table[kc * kRows + (o - o_first)] = v[k];
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int64_t gp = g0 + (int64_t)kb * kB + out_chunk_pos<L>(c, k);
+        if (gp < g1) {
+          const uint32_t o = (uint32_t)(gp / in_f), kc = (uint32_t)(gp - (int64_t)o * in_f) >> 3;
+          table[kc * pitch + (o - o_first)] = v[kb][k];
+        }
       }
     }
   }
@@ -163,9 +205,16 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   const int ntiles_all = (tokens + kTokTile - 1) / kTokTile;
   const auto x_r = rsrc(x, kTiled ? (uint32_t)((int64_t)ntiles_all * xsteps * 1024)
                                   : (uint32_t)((int64_t)tokens * in_f * 2));
-  float* part_first = partial + (block * 2 + 0) * (int64_t)tokens;
-  float* part_last = partial + (block * 2 + 1) * (int64_t)tokens;
-  const u32x4* brow = table + kq * kRows + l16;  // + step*4*kRows + 16*nt
+  float* part_first = partial + (tile * 2 + 0) * (int64_t)tokens;
+  float* part_last = partial + (tile * 2 + 1) * (int64_t)tokens;
+  const u32x4* brow = table + kq * pitch + l16;  // + step*4*pitch + 16*nt
+  // rows of the last 16-row tile past `pitch` (exact pitch) read zero
+  const bool last_row_ok = 16 * (NT - 1) + l16 < pitch;
+  auto brd = [&](const u32x4* b, int nt) -> u32x4 {
+    const u32x4 w = b[16 * nt];
+    if (nt == NT - 1) return last_row_ok ? w : u32x4{0u, 0u, 0u, 0u};
+    return w;
+  };
   constexpr uint32_t kOff = 0x80000000u;  // voffset that reads 0
 
   // Each wave takes groups of kGroup token tiles (64 tokens): per k step it
@@ -213,14 +262,14 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
     const u32x4* bs = brow;
     u32x4 bt[NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) bt[nt] = bs[16 * nt];
+    for (int nt = 0; nt < NT; ++nt) bt[nt] = brd(bs, nt);
     for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
 #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
-        const u32x4* bsn = (s0 + d + 1 < nsteps) ? bs + 4 * kRows : bs;
+        const u32x4* bsn = (s0 + d + 1 < nsteps) ? bs + 4 * pitch : bs;
         u32x4 bn[NT];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) bn[nt] = bsn[16 * nt];
+        for (int nt = 0; nt < NT; ++nt) bn[nt] = brd(bsn, nt);
         bs = bsn;
 #pragma unroll
         for (int g = 0; g < kGroup; ++g)
@@ -263,43 +312,56 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   }
 }
 
-// Rows straddling blocks b-1 and b: out[t][o] = scale * (last(b-1)[t] + first(b)[t]).
+// Rows straddling tiles b-1 and b: out[t][o] = scale * (last(b-1)[t] + first(b)[t]).
 __global__ __launch_bounds__(256) void bfht_linear_combine(const float* __restrict__ partial,
                                                            __bf16* __restrict__ out, int tokens, int in_f,
-                                                           int out_f, int64_t nblocks, float scale) {
+                                                           int out_f, int64_t ntiles, int64_t tile_len,
+                                                           float scale) {
   const int t = blockIdx.x * 256 + threadIdx.x;
   const int64_t b = (int64_t)blockIdx.y + 1;
-  if (t >= tokens || b >= nblocks) return;
-  const int64_t g0 = b * mfma15::kB;
+  if (t >= tokens || b >= ntiles) return;
+  const int64_t g0 = b * tile_len;
   if (g0 % in_f == 0) return;
   const int o = (int)(g0 / in_f);
   const float v = partial[((b - 1) * 2 + 1) * (int64_t)tokens + t] + partial[(b * 2) * (int64_t)tokens + t];
   out[(int64_t)t * out_f + o] = (__bf16)(scale * v);
 }
 
-template <int L, bool kTiled>
-hipError_t launch_linear_L(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
-  const int nt = (int)linear_row_tiles(a.in_features);
-  const dim3 grid((unsigned)(a.nblocks_w * a.token_splits)), block(mfma15::kThreads);
+template <int L, bool kTiled, int KB>
+hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
+  const int nt = (int)linear_row_tiles(a.in_features, KB);
+  const int64_t ntiles = (a.nblocks_w + KB - 1) / KB;
+  const int pitch = linear_pitch(a.in_features, KB);
+  const dim3 grid((unsigned)(ntiles * a.token_splits)), block(mfma15::kThreads);
   auto* lat = (const __bf16*)a.latent;
   auto* o = (__bf16*)a.out;
-#define LWL_LIN(NT)                                                                                             \
-  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT, kTiled>), grid, block, 0, s, x, lat, o, partial, (int)a.tokens, \
-                     (int)a.in_features, (int)a.out_features, (int)a.n, a.seed32, a.weight_scale, a.token_splits)
+#define LWL_LIN(NT)                                                                                               \
+  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT, kTiled, KB>), grid, block, 0, s, x, lat, o, partial,              \
+                     (int)a.tokens, (int)a.in_features, (int)a.out_features, (int)a.n, a.seed32, a.weight_scale, \
+                     a.token_splits, a.nblocks_w, pitch)
   switch (nt) {
     case 1: LWL_LIN(1); break;
     case 2: LWL_LIN(2); break;
     case 3: LWL_LIN(3); break;
     case 4: LWL_LIN(4); break;
+    case 5: if constexpr (KB == 2) LWL_LIN(5); else return hipErrorInvalidValue; break;
+    case 6: if constexpr (KB == 2) LWL_LIN(6); else return hipErrorInvalidValue; break;
     default: return hipErrorInvalidValue;
   }
 #undef LWL_LIN
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.nblocks_w < 2) return e;
-  hipLaunchKernelGGL(bfht_linear_combine, dim3((unsigned)((a.tokens + 255) / 256), (unsigned)(a.nblocks_w - 1)),
+  if (e != hipSuccess || ntiles < 2) return e;
+  hipLaunchKernelGGL(bfht_linear_combine, dim3((unsigned)((a.tokens + 255) / 256), (unsigned)(ntiles - 1)),
                      dim3(256), 0, s, (const float*)partial, o, (int)a.tokens, (int)a.in_features,
-                     (int)a.out_features, a.nblocks_w, a.weight_scale);
+                     (int)a.out_features, ntiles, (int64_t)KB * mfma15::kB, a.weight_scale);
   return hipGetLastError();
+}
+
+template <int L, bool kTiled>
+hipError_t launch_linear_L(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
+  if constexpr (kTiled)
+    if (a.blocks_per_wg == 2) return launch_linear_kb<L, true, 2>(a, x, partial, s);
+  return launch_linear_kb<L, kTiled, 1>(a, x, partial, s);
 }
 
 template <int L>
@@ -308,10 +370,8 @@ hipError_t launch_linear_L(const LinearArgs& a, hipStream_t s) {
   if (!linear_tiled(a)) return launch_linear_L<L, false>(a, (const __bf16*)a.x, partial, s);
   const XTiling xt = x_tiling(a);
   auto* tiled = reinterpret_cast<u32x4*>((unsigned char*)a.work + partial_bytes(a));
-  const int64_t chunks = (int64_t)xt.bytes() / 16;
-  const int64_t grid = std::min<int64_t>((chunks + 255) / 256, 4096);
-  hipLaunchKernelGGL(bfht_linear_tile_x, dim3((unsigned)grid), dim3(256), 0, s, (const __bf16*)a.x, tiled,
-                     (int)a.tokens, (int)a.in_features, xt.steps, chunks);
+  hipLaunchKernelGGL(bfht_linear_tile_x, dim3((unsigned)((xt.steps + 3) / 4), (unsigned)xt.tiles), dim3(256), 0, s,
+                     (const __bf16*)a.x, tiled, (int)a.tokens, (int)a.in_features, xt.steps);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_linear_L<L, true>(a, (const __bf16*)tiled, partial, s);
@@ -326,8 +386,18 @@ bool linear_applicable(int dtype, int log_block, int64_t in_features) {
   // at most kMaxNT tiles of 16 rows per block; the k-major table fits in LDS.
   if (dtype != kBF16 || log_block != mfma15::kLog || in_features % 8 != 0 || in_features > mfma15::kB) return false;
   const int64_t nt = linear_row_tiles(in_features);
-  const int64_t table_bytes = (int64_t)4 * linear_steps(in_features) * 16 * nt * 16;
-  return nt <= kMaxNT && table_bytes <= kLinearLdsBytes;
+  return nt <= kMaxNT && linear_table_bytes(in_features, 16 * nt) <= kLinearLdsBytes;
+}
+
+int linear_blocks_per_wg(const LinearArgs& a) {
+  // Two blocks per workgroup for batches read from the tiled x copy when a block
+  // holds few rows (at most 32: the contraction is bound by streaming x, and two
+  // blocks feed each x element twice the rows), their rows fit the register
+  // budget and their table the LDS.  With more rows per block the loop is fed
+  // well enough and a second generator chain per workgroup costs more than it saves.
+  if (!linear_tiled(a) || a.nblocks_w < 2 || linear_rows(a.in_features, 1) > 32) return 1;
+  if (linear_row_tiles(a.in_features, 2) > kMaxNT2) return 1;
+  return linear_pitch_fits(a.in_features, 2) ? 2 : 1;
 }
 
 size_t linear_workspace_bytes(const LinearArgs& a) {
@@ -335,10 +405,11 @@ size_t linear_workspace_bytes(const LinearArgs& a) {
 }
 
 int linear_token_splits(const LinearArgs& a) {
-  // one workgroup per CU: split tokens so that blocks x splits fills 256 CUs,
-  // never below one 16-token tile per split
+  // one workgroup per CU: split tokens so that block tiles x splits fills 256
+  // CUs, never below one 16-token tile per split
   const int64_t tiles = (a.tokens + kTokTile - 1) / kTokTile;
-  int64_t split = a.nblocks_w >= 256 ? 1 : 256 / a.nblocks_w;
+  const int64_t wtiles = (a.nblocks_w + a.blocks_per_wg - 1) / a.blocks_per_wg;
+  int64_t split = wtiles >= 256 ? 1 : 256 / wtiles;
   if (split > tiles) split = tiles;
   return (int)(split < 1 ? 1 : split);
 }

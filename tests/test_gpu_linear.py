@@ -43,6 +43,10 @@ def oracle_linear(x: torch.Tensor, latent: torch.Tensor, out_f: int, layers: int
         (257, 1024, 200, 32768, 2, 21, 1.0),    # just above it: tiled x, last tile holds one token
         (20, 528, 200, 32768, 3, 31, 1.0),      # smallest in_features: 4 row tiles per block
         (40, 5120, 30, 32768, 2, 32, 1.0),      # largest: the k-major table fills all 160 KiB of LDS
+        (333, 2048, 90, 32768, 3, 33, 1.0),     # two blocks per workgroup, exact table pitch (33 rows)
+        (280, 1064, 90, 32768, 2, 36, 1.0),     # 32 rows per block (the two-block limit): 64-row tiles
+        (600, 3072, 100, 32768, 2, 34, 0.5),    # two blocks per workgroup, 23-row pitch, 5 tiles
+        (300, 5120, 41, 32768, 3, 35, 1.0),     # two blocks per workgroup, one row tile, last tile single
     ],
 )
 def test_fused_linear_matches_oracle(tokens, in_f, out_f, n, layers, seed, scale):
