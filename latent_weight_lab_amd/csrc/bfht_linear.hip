@@ -34,9 +34,18 @@ using namespace mfma15;
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kTokTile = 16;  // tokens per MFMA tile
+constexpr int kXcds = 8;      // MI355X: workgroup i is dispatched to XCD i % 8
 constexpr int kKStep = 32;    // k per MFMA
 constexpr int kGroup = 4;     // token tiles per wave pass (each W read feeds kGroup MFMAs)
 constexpr int kDepth = 4;     // x prefetch distance in k steps
+
+// Scattered bf16 store written through the XCD's L2 (sc0 sc1).  The combine
+// kernel's stores touch one 2-byte element per 128-byte line; written back,
+// each such line would be a partial-line write-back at the kernel's end.
+__device__ __forceinline__ void store_bf16_through(__bf16* p, float v) {
+  const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v);
+  asm volatile("global_store_short %0, %1, off sc0 sc1" ::"v"(p), "v"(bits) : "memory");
+}
 
 __device__ __forceinline__ f32x4v mfma16(u32x4 a, u32x4 b, f32x4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
@@ -50,6 +59,7 @@ __device__ __forceinline__ f32x4v mfma16(u32x4 a, u32x4 b, f32x4v c) {
 // workgroup's LDS (all 160 KiB of a gfx950 CU; the generator's exchange uses the first 128).
 // Together: in_features % 8 == 0 and 528 <= in_features <= 5120.
 constexpr int kMaxNT = 4;
+constexpr int kLinearMaxIn = 5120;  // the range the tests cover (the table itself would fit larger rows)
 constexpr int kMaxNT2 = 6;  // two blocks per workgroup: 16-row tiles (register budget)
 constexpr int kLinearLdsBytes = 160 * 1024;
 static_assert(kLinearLdsBytes >= kLdsBytes, "the generator chain runs in the same LDS");
@@ -67,8 +77,19 @@ __host__ __device__ constexpr int linear_steps(int64_t in_features) {
   return (int)(((in_features + kKStep - 1) / kKStep + kDepth - 1) / kDepth * kDepth);
 }
 
+// Table chunk (kc, r) — row r of the tile, k chunk kc — lives at
+// kc * pitch + r + (kc >> 2): every k step's 4 chunks are shifted one slot
+// further than the previous step's.  That makes the scatter of a generated
+// block conflict-free: the 16 lanes of one LDS write phase hold chunks 4 apart
+// in one row (kc, kc + 4, ...), whose slots then differ by 4 * pitch + 1, an odd
+// number, so they fall in 16 distinct 16-byte bank groups for any pitch; the
+// contraction reads one step's chunks at a common shift, so its reads stay
+// contiguous.  The table holds 4 * steps * pitch + steps chunks.
+__device__ __forceinline__ int table_slot(int kc, int r, int pitch) { return kc * pitch + r + (kc >> 2); }
+
 constexpr int64_t linear_table_bytes(int64_t in_features, int64_t pitch) {
-  return (int64_t)4 * linear_steps(in_features) * pitch * 16;
+  const int64_t steps = linear_steps(in_features);
+  return (4 * steps * pitch + steps) * 16;
 }
 // Table rows: whole 16-row tiles (zero-padded) when they fit in the LDS, else the
 // exact row count (the kernel masks the last tile's extra rows on read; those
@@ -111,20 +132,38 @@ size_t partial_bytes(const LinearArgs& a) {
   return ((size_t)ntiles * 2 * (size_t)a.tokens * sizeof(float) + 255) / 256 * 256;
 }
 
-// One workgroup per (4 k steps, token tile): wave w writes the 1 KiB chunk
-// group of step 4 * blockIdx.x + w; lane l reads x[16 T + (l & 15)][32 s + 8 (l >> 4) .. +7].
+// One wave per (token tile T, run of kTileSteps k steps): lane l reads
+// x[16 T + (l & 15)][32 s + 8 (l >> 4) .. +7] for every step s of the run (all
+// loads in flight before the first store; each pair of steps reads 16 whole
+// 128-byte row segments) and writes the 1 KiB chunk group of each step.  The
+// copy is stored write-through: the fused kernel reads it from other XCDs, and
+// streaming it out during the kernel avoids a serial L2 write-back at its end.
+constexpr int kTileSteps = 8;
+
 __global__ __launch_bounds__(256) void bfht_linear_tile_x(const __bf16* __restrict__ x, u32x4* __restrict__ xt,
-                                                          int tokens, int in_f, int steps) {
+                                                          int tokens, int in_f, int steps, int runs, int waves) {
+  const int wv = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar: uniform resources
+  if (wv >= waves) return;
+  const int tt = wv / runs;
+  const int s0 = (wv - tt * runs) * kTileSteps;
   const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * in_f * 2));
+  const auto xt_r = rsrc(xt, (uint32_t)((int64_t)(tt + 1) * steps * 1024));
   const int lane = threadIdx.x & 63;
-  const int s = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int tt = blockIdx.y;
-  if (s >= steps) return;
   const int t = tt * kTokTile + (lane & 15);
-  const int k = kKStep * s + 8 * (lane >> 4);
-  const bool in_range = t < tokens && k < in_f;
-  xt[((int64_t)tt * steps + s) * 64 + lane] =
-      __builtin_amdgcn_raw_buffer_load_b128(x_r, in_range ? (t * in_f + k) * 2 : (int)0x80000000, 0, 0);
+  const int k0 = kKStep * s0 + 8 * (lane >> 4);
+  u32x4 v[kTileSteps];
+#pragma unroll
+  for (int j = 0; j < kTileSteps; ++j) {
+    const int k = k0 + kKStep * j;
+    const bool in_range = t < tokens && k < in_f;  // in_f % 8 == 0: whole chunks
+    v[j] = __builtin_amdgcn_raw_buffer_load_b128(x_r, in_range ? (t * in_f + k) * 2 : (int)0x80000000, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < kTileSteps; ++j) {
+    const int s = s0 + j;  // steps past the row are not stored (the copy holds `steps` steps per tile)
+    const int off = s < steps ? ((tt * steps + s) * 64 + lane) * 16 : (int)0x80000000;
+    __builtin_amdgcn_raw_buffer_store_b128(v[j], xt_r, off, 0, kStreamStore);
+  }
 }
 
 template <int L, int NT, bool kTiled, int KB>
@@ -136,8 +175,16 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
                                                                float scale, int token_split, int64_t nblocks,
                                                                int pitch) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLinearLdsBytes];
-  const int64_t tile = blockIdx.x / token_split;  // blocks tile*KB .. tile*KB + KB - 1
-  const int split = blockIdx.x % token_split;
+  // XCD-aware work order: workgroup i runs on XCD i % 8, and work item
+  // p = split * ntiles + tile (split-major) goes to XCD p / per_xcd, so each
+  // XCD's L2 holds the x rows of one or two token splits instead of all of x.
+  const int64_t ntiles = (nblocks + KB - 1) / KB;
+  const int64_t nwork = ntiles * token_split;
+  const int64_t per_xcd = (nwork + kXcds - 1) / kXcds;
+  const int64_t p = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (p >= nwork) return;  // uniform: the grid is rounded up to whole XCD rows
+  const int split = (int)(p / ntiles);
+  const int64_t tile = p - (int64_t)split * ntiles;  // blocks tile*KB .. tile*KB + KB - 1
   // `pitch` table rows (>= the tile's output rows; 16*NT, zero-padded, when that
   // fits in the LDS, else exact and the last row tile masked on read)
 
@@ -155,10 +202,18 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
 
   // 1. generate the tile's blocks (signed bf16; the first kept in registers
   //    while the next one's chain uses the LDS) and scatter them into LDS as a
-  //    k-major table of 16-byte chunks: table[kc * pitch + (o - o_first)] holds
-  //    W[o][8*kc .. 8*kc+7]; entries outside the tile read 0.
+  //    k-major table of 16-byte chunks: table[table_slot(kc, r, pitch)]
+  //    holds W[o_first + r][8*kc .. 8*kc+7]; entries outside the tile read 0.
   u32x4* table = reinterpret_cast<u32x4*>(lds);
   {
+    const int nrows = o_last - o_first + 1;
+    const int row_chunks = in_f >> 3;                   // chunks holding data in a row
+    const int c_first = (int)(g0 - (int64_t)o_first * in_f) >> 3;  // first chunk of row 0 in the tile
+    const int c_last = (int)(g1 - (int64_t)o_last * in_f) >> 3;    // chunks of the last row in the tile
+    // block position p of block kb -> tile-relative flat offset rel = base_rel + kb * kB + p,
+    // row r = rel / in_f (rel < in_f + KB * kB: float quotient, corrected by one)
+    const int base_rel = c_first << 3;
+    const float inv_in = 1.0f / (float)in_f;
     u32x4 v[KB][8];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
@@ -176,18 +231,49 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
       }
     }
     __syncthreads();  // every wave has read its last exchange
-    for (int i = threadIdx.x; i < kchunks * pitch; i += kThreads) table[i] = u32x4{0u, 0u, 0u, 0u};
-    __syncthreads();
+    // Zero exactly the entries the scatter leaves out (disjoint from it, so no
+    // barrier in between): rows past the tile's last row, chunks before the
+    // tile's start in row 0 and from its end in the last row, and k padding.
+    {
+      const int pad_rows = pitch - nrows;
+      const int n_pad = pad_rows * kchunks;  // (kc, r >= nrows)
+      const int n_edge = 2 * kchunks;        // rows 0 and nrows - 1, every kc
+      for (int i = threadIdx.x; i < n_pad + n_edge; i += kThreads) {
+        int kc, r;
+        bool zero = true;
+        if (i < n_pad) {
+          kc = i / pad_rows;
+          r = nrows + (i - kc * pad_rows);
+        } else {
+          const int j = i - n_pad;
+          const int e = j >= kchunks;
+          kc = j - e * kchunks;
+          r = e ? nrows - 1 : 0;
+          const int lo = r == 0 ? c_first : 0;
+          const int hi = r == nrows - 1 ? c_last : row_chunks;
+          zero = kc < lo || kc >= hi;
+        }
+        if (zero) table[table_slot(kc, r, pitch)] = u32x4{0u, 0u, 0u, 0u};
+      }
+      // k padding of the inner rows (only when the row length is not a whole number of prefetch rounds)
+      const int n_kpad = (kchunks - row_chunks) * (nrows > 2 ? nrows - 2 : 0);
+      for (int i = threadIdx.x; i < n_kpad; i += kThreads) {
+        const int q = kchunks - row_chunks;
+        const int r = 1 + i / q, kc = row_chunks + (i - (i / q) * q);
+        table[table_slot(kc, r, pitch)] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
     const Ctx c = make_ctx(seed32, tile * KB);  // chunk positions do not depend on the block
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const int64_t gp = g0 + (int64_t)kb * kB + out_chunk_pos<L>(c, k);
-        if (gp < g1) {
-          const uint32_t o = (uint32_t)(gp / in_f), kc = (uint32_t)(gp - (int64_t)o * in_f) >> 3;
-          table[kc * pitch + (o - o_first)] = v[kb][k];
-        }
+        const int rel = base_rel + kb * kB + out_chunk_pos<L>(c, k);
+        int r = (int)((float)rel * inv_in);
+        r -= r * in_f > rel;
+        r += (r + 1) * in_f <= rel;
+        const int kc = (rel - r * in_f) >> 3;
+        if (g0 + rel - base_rel < g1) table[table_slot(kc, r, pitch)] = v[kb][k];
       }
     }
   }
@@ -198,7 +284,9 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   const int per_split = (ntiles_tok + token_split - 1) / token_split;
   const int tt0 = split * per_split;
   const int tt1 = (tt0 + per_split < ntiles_tok) ? tt0 + per_split : ntiles_tok;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index as a scalar: the token tiles, and so the buffer resources of
+  // the epilogue's stores, are then known to be uniform across the wave
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, kq = lane >> 4;  // A/B: row/col l16, k = 8*kq + j
   // x: the tiled copy (kTiled) or the row-major input; offsets past the end read 0
   const int xsteps = (in_f + kKStep - 1) / kKStep;
@@ -207,7 +295,7 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
                                   : (uint32_t)((int64_t)tokens * in_f * 2));
   float* part_first = partial + (tile * 2 + 0) * (int64_t)tokens;
   float* part_last = partial + (tile * 2 + 1) * (int64_t)tokens;
-  const u32x4* brow = table + kq * pitch + l16;  // + step*4*pitch + 16*nt
+  const u32x4* brow = table + kq * pitch + l16;  // + step * (4 * pitch + 1) + 16 * nt
   // rows of the last 16-row tile past `pitch` (exact pitch) read zero
   const bool last_row_ok = 16 * (NT - 1) + l16 < pitch;
   auto brd = [&](const u32x4* b, int nt) -> u32x4 {
@@ -266,7 +354,8 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
     for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
 #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
-        const u32x4* bsn = (s0 + d + 1 < nsteps) ? bs + 4 * pitch : bs;
+        const int sn = (s0 + d + 1 < nsteps) ? s0 + d + 1 : s0 + d;
+        const u32x4* bsn = brow + sn * (4 * pitch + 1);
         u32x4 bn[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) bn[nt] = brd(bsn, nt);
@@ -286,26 +375,41 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
         for (int g = 0; g < kGroup; ++g) ring[d][g] = xload(g, s0 + d + kDepth);
       }
     }
-    // D[m = 4*kq + r][n = l16]
+    // D[m = 4*kq + r][n = l16]: token 16 tt + 4 kq + r, row o_first + 16 nt + l16.
+    // Branch-free stores: each token tile gets buffer resources over its own rows
+    // of out and of the partials (tokens past the end fall outside them), and an
+    // element that does not belong in a destination gets the offset that drops it.
 #pragma unroll
     for (int g = 0; g < kGroup; ++g) {
       const int tt = tg + g;
-      if (tt >= tt1) continue;
+      if (tt >= tt1) continue;  // uniform across the wave
+      const int t0 = tt * kTokTile;
+      const int nt_tok = tokens - t0 < kTokTile ? tokens - t0 : kTokTile;
+      const auto o_r = rsrc(out + (int64_t)t0 * out_f, (uint32_t)(nt_tok * out_f * 2));
+      const auto pf_r = rsrc(part_first + t0, (uint32_t)(nt_tok * 4));
+      const auto pl_r = rsrc(part_last + t0, (uint32_t)(nt_tok * 4));
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int o = o_first + 16 * nt + l16;
-        if (o > o_last) continue;
+        const bool is_first = first_partial && o == o_first;
+        const bool is_last = last_partial && o == o_last;
+        const bool is_out = o <= o_last && !is_first && !is_last;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int tr = tt * kTokTile + 4 * kq + r;
-          if (tr >= tokens) continue;
+          const int m = 4 * kq + r;
           const float v = acc[g][nt][r];
-          if (o == o_first && first_partial)
-            part_first[tr] = v;
-          else if (o == o_last && last_partial)
-            part_last[tr] = v;
-          else
-            out[(int64_t)tr * out_f + o] = (__bf16)(scale * v);
+          const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)(scale * v));
+          __builtin_amdgcn_raw_buffer_store_b16(b, o_r, is_out ? (m * out_f + o) * 2 : (int)kOff, 0, 0);
+        }
+        // partial rows: the first row of the tile (nt 0, l16 0) and its last row
+        if (nt == 0 || 16 * (nt + 1) > o_last - o_first) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = 4 * kq + r;
+            const uint32_t bits = __float_as_uint(acc[g][nt][r]);
+            __builtin_amdgcn_raw_buffer_store_b32(bits, pf_r, is_first ? m * 4 : (int)kOff, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(bits, pl_r, is_last ? m * 4 : (int)kOff, 0, 0);
+          }
         }
       }
     }
@@ -324,7 +428,7 @@ __global__ __launch_bounds__(256) void bfht_linear_combine(const float* __restri
   if (g0 % in_f == 0) return;
   const int o = (int)(g0 / in_f);
   const float v = partial[((b - 1) * 2 + 1) * (int64_t)tokens + t] + partial[(b * 2) * (int64_t)tokens + t];
-  out[(int64_t)t * out_f + o] = (__bf16)(scale * v);
+  store_bf16_through(out + (int64_t)t * out_f + o, scale * v);
 }
 
 template <int L, bool kTiled, int KB>
@@ -332,7 +436,8 @@ hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial
   const int nt = (int)linear_row_tiles(a.in_features, KB);
   const int64_t ntiles = (a.nblocks_w + KB - 1) / KB;
   const int pitch = linear_pitch(a.in_features, KB);
-  const dim3 grid((unsigned)(ntiles * a.token_splits)), block(mfma15::kThreads);
+  const int64_t per_xcd = (ntiles * a.token_splits + kXcds - 1) / kXcds;
+  const dim3 grid((unsigned)(per_xcd * kXcds)), block(mfma15::kThreads);
   auto* lat = (const __bf16*)a.latent;
   auto* o = (__bf16*)a.out;
 #define LWL_LIN(NT)                                                                                               \
@@ -370,8 +475,10 @@ hipError_t launch_linear_L(const LinearArgs& a, hipStream_t s) {
   if (!linear_tiled(a)) return launch_linear_L<L, false>(a, (const __bf16*)a.x, partial, s);
   const XTiling xt = x_tiling(a);
   auto* tiled = reinterpret_cast<u32x4*>((unsigned char*)a.work + partial_bytes(a));
-  hipLaunchKernelGGL(bfht_linear_tile_x, dim3((unsigned)((xt.steps + 3) / 4), (unsigned)xt.tiles), dim3(256), 0, s,
-                     (const __bf16*)a.x, tiled, (int)a.tokens, (int)a.in_features, xt.steps);
+  const int runs = (xt.steps + kTileSteps - 1) / kTileSteps;
+  const int waves = (int)xt.tiles * runs;
+  hipLaunchKernelGGL(bfht_linear_tile_x, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, (const __bf16*)a.x,
+                     tiled, (int)a.tokens, (int)a.in_features, xt.steps, runs, waves);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_linear_L<L, true>(a, (const __bf16*)tiled, partial, s);
@@ -385,8 +492,7 @@ bool linear_applicable(int dtype, int log_block, int64_t in_features) {
   // bf16 matrix-core generator (B = 2^15); 16-byte rows of x and W (in % 8 == 0);
   // at most kMaxNT tiles of 16 rows per block; the k-major table fits in LDS.
   if (dtype != kBF16 || log_block != mfma15::kLog || in_features % 8 != 0 || in_features > mfma15::kB) return false;
-  const int64_t nt = linear_row_tiles(in_features);
-  return nt <= kMaxNT && linear_table_bytes(in_features, 16 * nt) <= kLinearLdsBytes;
+  return in_features <= kLinearMaxIn && linear_row_tiles(in_features) <= kMaxNT && linear_pitch_fits(in_features, 1);
 }
 
 int linear_blocks_per_wg(const LinearArgs& a) {
