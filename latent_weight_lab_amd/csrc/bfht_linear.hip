@@ -62,7 +62,7 @@ constexpr int kMaxNT = 4;
 constexpr int kLinearMaxIn = 5120;  // the range the tests cover (the table itself would fit larger rows)
 constexpr int kMaxNT2 = 6;  // two blocks per workgroup: 16-row tiles (register budget)
 constexpr int kLinearLdsBytes = 160 * 1024;
-static_assert(kLinearLdsBytes >= kLdsBytes, "the generator chain runs in the same LDS");
+static_assert(kLinearLdsBytes >= kChainLdsBytes, "the generator chain runs in the same LDS");
 
 // output rows a tile of kb blocks can touch, incl. the two partial ones
 __host__ __device__ constexpr int64_t linear_rows(int64_t in_features, int kb) {

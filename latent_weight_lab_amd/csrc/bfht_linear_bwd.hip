@@ -130,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_bwd_mfma15(const u32x4* 
                                                                    int in_f, int out_f, int n, int steps,
                                                                    int itiles, uint32_t seed32, float scale,
                                                                    int token_split) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kChainLdsBytes];
   const int64_t block = blockIdx.x / token_split;
   const int split = blockIdx.x % token_split;
   const int64_t size = (int64_t)in_f * out_f;

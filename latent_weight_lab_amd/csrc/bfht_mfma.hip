@@ -21,7 +21,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
                                                             __bf16* __restrict__ out, int n,
                                                             int64_t first_block, int64_t start,
                                                             int64_t stop, uint32_t seed32) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kChainLdsBytes];
   const int64_t block = first_block + blockIdx.x;
   const Ctx x = make_ctx(seed32, block);
   u32x4 src[kTiles][2];
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
                                                             float* __restrict__ partial, int n,
                                                             int64_t first_block, int64_t start,
                                                             int64_t stop, uint32_t seed32) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kChainLdsBytes];
   const int64_t slot = blockIdx.x;
   const int64_t block = first_block + slot;
   const Ctx x = make_ctx(seed32, block);
@@ -119,7 +119,7 @@ __device__ __forceinline__ u32x4 scale_chunk(u32x4 v, float scale) {
 // the bf16 output times the job's weight scale.
 template <int L>
 __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd_grouped(const GroupTable g) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kChainLdsBytes];
   const int j = group_job(g, (int)blockIdx.x);
   const GroupJob& jb = g.job[j];
   const int64_t block = (int64_t)blockIdx.x - g.prefix[j];
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd_grouped(const GroupT
 // gradient, as bfht_mfma15_bwd), into the job's partial rows.
 template <int L>
 __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd_grouped(const GroupTable g) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kChainLdsBytes];
   const int j = group_job(g, (int)blockIdx.x);
   const GroupJob& jb = g.job[j];
   const int64_t slot = (int64_t)blockIdx.x - g.prefix[j];

@@ -66,6 +66,13 @@ constexpr int kChunks = kB / 8;  // 16-byte chunks of 8 bf16 in one block
 // costs LDS cycles in proportion); two buffers back to back (128 KiB).
 constexpr int kXBufBytes = kChunks * 16;
 constexpr int kLdsBytes = 2 * kXBufBytes;
+// Sign-word table after the exchange buffers: the words of sign layers 1..L
+// (1024 per layer, 32 positions each), hashed once per block while the
+// block's source loads are in flight.  A chain kernel's LDS is kChainLdsBytes.
+constexpr int kMaxChainLayers = 3;
+constexpr int kWordsPerLayer = kB / 32;
+constexpr int kWordTableBytes = kMaxChainLayers * kWordsPerLayer * 4;
+constexpr int kChainLdsBytes = kLdsBytes + kWordTableBytes;
 constexpr uint32_t kPairSign = 0x80008000u;
 
 __device__ __forceinline__ uint32_t pk(float lo, float hi) {
@@ -258,17 +265,40 @@ __device__ __forceinline__ void exchange_read_stage_c(f32x16 (&acc)[kTiles], con
   }
 }
 
-// Inverted sign words of the layer applied after the chain, in the output
-// layout (S1 when L is odd: 4 words, slot = p13 + 2*p14; S0 when L is even:
-// 2 words, slot = p11), unpermuted.
-template <int L>
-__device__ __forceinline__ void final_words(const Ctx& x, int layer, uint32_t (&nw)[4]) {
-  const uint32_t key = x.bkey ^ layer_key(layer);
-  constexpr bool kOutS1 = (L % 2) == 1;
+// Fills the sign-word table (bytes kLdsBytes.. of the chain's LDS): slot j - 1
+// holds the 1024 inverted words of sign layer sign_layer(j), j = 1..L, two per
+// thread, in the form their reader applies: sign layer j < L is read by kernel
+// layer j, whose stage a runs in S1 (j odd: bit permutation swap_idx34) or S0
+// (j even: swap_idx04); the last one (j = L) is read by the output code, unpermuted.
+template <int L, class SignLayer>
+__device__ __forceinline__ void fill_words(const Ctx& x, uint32_t* wtab, SignLayer sign_layer) {
+  static_assert(L <= kMaxChainLayers, "word table holds kMaxChainLayers layers");
 #pragma unroll
-  for (int s = 0; s < (kOutS1 ? 4 : 2); ++s)
-    nw[s] = ~(kOutS1 ? slot_word(key, x.gw1, s, 8) : slot_word(key, x.gw0, s, 6));
-  if (!kOutS1) nw[2] = nw[3] = 0;
+  for (int j = 1; j <= L; ++j) {
+    const uint32_t key = x.bkey ^ layer_key(sign_layer(j));
+#pragma unroll
+    for (int h = 0; h < kWordsPerLayer / kThreads; ++h) {
+      const uint32_t w = (uint32_t)threadIdx.x + (uint32_t)(h * kThreads);
+      uint32_t v = ~lowbias32(key ^ (0xc2b2ae35u * (w + 1u)));
+      if (j < L) v = (j & 1) ? swap_idx34(v) : swap_idx04(v);
+      wtab[(j - 1) * kWordsPerLayer + (int)w] = v;
+    }
+  }
+}
+
+// This lane's words of table slot `slot` as layer_words<kOdd> returns them
+// (S1: slot = p13 + 2*p14, word index base1 + s*2^8; S0: slot = p11,
+// base0 + s*2^6).  kPermuted: the slot holds the stage-a form (S1 words still
+// take this wave's p4 pre-shift).
+template <bool kOdd, bool kPermuted>
+__device__ __forceinline__ void read_words(const Ctx& x, const uint32_t* wtab, int slot, uint32_t (&nw)[4]) {
+  const uint32_t* t = wtab + slot * kWordsPerLayer;
+#pragma unroll
+  for (int s = 0; s < (kOdd ? 4 : 2); ++s) {
+    const uint32_t v = kOdd ? t[x.base1 + (s << 8)] : t[x.base0 + (s << 6)];
+    nw[s] = (kOdd && kPermuted) ? (v >> (8 * x.p4)) : v;
+  }
+  if (!kOdd) nw[2] = nw[3] = 0;
 }
 
 // Runs the L-layer chain on a block whose unsigned input sits in `src`
@@ -279,15 +309,17 @@ __device__ __forceinline__ void final_words(const Ctx& x, int layer, uint32_t (&
 // in S1 (L odd) or S0 (L even).  Layer i exchanges through buffer i & 1 of
 // `lds`: the previous readers of that buffer (layer i - 2) are past layer
 // i - 1's barrier, and buffer L & 1 needs no barrier before its next writes.
+// `lds` spans kChainLdsBytes; the sign words of layers 1..L are hashed into
+// its table first (their loads' latency covers the hashing) and read after
+// each layer's exchange barrier, which also orders the table's writes.
 template <int L, class SignLayer>
 __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, unsigned char* lds,
                                           const u32x4 (&src)[kTiles][2], SignLayer sign_layer,
                                           uint32_t (&fin)[4]) {
-  // The words of sign layer i + 1 are hashed during layer i, after its stage
-  // a: the VALU work then overlaps stage b's matrix-core work instead of
-  // delaying the first stage.
+  uint32_t* wtab = reinterpret_cast<uint32_t*>(lds + kLdsBytes);
   uint32_t nw[L][4];
   layer_words<false>(x, sign_layer(0), nw[0]);
+  fill_words<L>(x, wtab, sign_layer);
   const int lane = threadIdx.x & 63;
   // Stage a: Q/4 (even layers), S/4 (odd); stage b: Q/8; stage c: S/4 (even),
   // Q/4 (odd); the last stage c carries the residual 2^(-L/2): S/4*2^-0.5
@@ -317,18 +349,18 @@ __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, u
     } else {
       stage_rows<true, false>(acc, hq4, nw[i]);
     }
-    if (i + 1 < L) {
-      if ((i + 1) & 1)
-        layer_words<true>(x, sign_layer(i + 1), nw[i + 1]);
-      else
-        layer_words<false>(x, sign_layer(i + 1), nw[i + 1]);
-    } else {
-      final_words<L>(x, sign_layer(L), fin);
-    }
     stage_rows<false, false>(acc, hq8, nw[i]);
     u32x2* xbuf = reinterpret_cast<u32x2*>(lds + (i & 1) * kXBufBytes);
     exchange_write(acc, xbuf, x);
     __syncthreads();
+    if (i + 1 < L) {
+      if ((i + 1) & 1)
+        read_words<true, true>(x, wtab, i, nw[i + 1]);
+      else
+        read_words<false, true>(x, wtab, i, nw[i + 1]);
+    } else {
+      read_words<(L % 2) == 1, false>(x, wtab, L - 1, fin);
+    }
     exchange_read_stage_c(acc, i == L - 1 ? hlast : (odd ? hq4 : hs4), xbuf, x);
   }
 }
