@@ -91,10 +91,10 @@ constexpr int64_t linear_table_bytes(int64_t in_features, int64_t pitch) {
   const int64_t steps = linear_steps(in_features);
   return (4 * steps * pitch + steps) * 16;
 }
-// Table rows: whole 16-row tiles (zero-padded) when they fit in the LDS, else the
-// exact row count (the kernel masks the last tile's extra rows on read; those
-// reads run up to 15 rows past the table, so an exact table leaves that much
-// LDS free).
+// Table rows: whole 16-row tiles when they fit in the LDS, else the exact row
+// count (the reads of the last row tile then run up to 15 rows past the table,
+// into entries whose output columns are never stored, so an exact table leaves
+// that much LDS free).
 constexpr int64_t kExactPitchSlack = 16 * 16;
 int linear_pitch(int64_t in_features, int kb) {
   const int64_t padded = 16 * linear_row_tiles(in_features, kb);
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   if (p >= nwork) return;  // uniform: the grid is rounded up to whole XCD rows
   const int split = (int)(p / ntiles);
   const int64_t tile = p - (int64_t)split * ntiles;  // blocks tile*KB .. tile*KB + KB - 1
-  // `pitch` table rows (>= the tile's output rows; 16*NT, zero-padded, when that
+  // `pitch` table rows (>= the tile's output rows; 16*NT when that
   // fits in the LDS, else exact and the last row tile masked on read)
 
   const int64_t size = (int64_t)in_f * out_f;
@@ -203,7 +203,8 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   // 1. generate the tile's blocks (signed bf16; the first kept in registers
   //    while the next one's chain uses the LDS) and scatter them into LDS as a
   //    k-major table of 16-byte chunks: table[table_slot(kc, r, pitch)]
-  //    holds W[o_first + r][8*kc .. 8*kc+7]; entries outside the tile read 0.
+  //    holds W[o_first + r][8*kc .. 8*kc+7]; entries of the tile's rows outside
+  //    [g0, g1) read 0.
   u32x4* table = reinterpret_cast<u32x4*>(lds);
   {
     const int nrows = o_last - o_first + 1;
@@ -231,29 +232,19 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
       }
     }
     __syncthreads();  // every wave has read its last exchange
-    // Zero exactly the entries the scatter leaves out (disjoint from it, so no
-    // barrier in between): rows past the tile's last row, chunks before the
-    // tile's start in row 0 and from its end in the last row, and k padding.
+    // Zero exactly the entries of the tile's rows that the scatter leaves out
+    // (disjoint from it, so no barrier in between): chunks before the tile's
+    // start in row 0 and from its end in the last row, and k padding.  Rows
+    // past the last one stay as they are (their output columns are not stored).
     {
-      const int pad_rows = pitch - nrows;
-      const int n_pad = pad_rows * kchunks;  // (kc, r >= nrows)
-      const int n_edge = 2 * kchunks;        // rows 0 and nrows - 1, every kc
-      for (int i = threadIdx.x; i < n_pad + n_edge; i += kThreads) {
-        int kc, r;
-        bool zero = true;
-        if (i < n_pad) {
-          kc = i / pad_rows;
-          r = nrows + (i - kc * pad_rows);
-        } else {
-          const int j = i - n_pad;
-          const int e = j >= kchunks;
-          kc = j - e * kchunks;
-          r = e ? nrows - 1 : 0;
-          const int lo = r == 0 ? c_first : 0;
-          const int hi = r == nrows - 1 ? c_last : row_chunks;
-          zero = kc < lo || kc >= hi;
-        }
-        if (zero) table[table_slot(kc, r, pitch)] = u32x4{0u, 0u, 0u, 0u};
+      const int n_edge = 2 * kchunks;  // rows 0 and nrows - 1, every kc
+      for (int i = threadIdx.x; i < n_edge; i += kThreads) {
+        const int e = i >= kchunks;
+        const int kc = i - e * kchunks;
+        const int r = e ? nrows - 1 : 0;
+        const int lo = r == 0 ? c_first : 0;
+        const int hi = r == nrows - 1 ? c_last : row_chunks;
+        if (kc < lo || kc >= hi) table[table_slot(kc, r, pitch)] = u32x4{0u, 0u, 0u, 0u};
       }
       // k padding of the inner rows (only when the row length is not a whole number of prefetch rounds)
       const int n_kpad = (kchunks - row_chunks) * (nrows > 2 ? nrows - 2 : 0);
@@ -296,13 +287,11 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   float* part_first = partial + (tile * 2 + 0) * (int64_t)tokens;
   float* part_last = partial + (tile * 2 + 1) * (int64_t)tokens;
   const u32x4* brow = table + kq * pitch + l16;  // + step * (4 * pitch + 1) + 16 * nt
-  // rows of the last 16-row tile past `pitch` (exact pitch) read zero
-  const bool last_row_ok = 16 * (NT - 1) + l16 < pitch;
-  auto brd = [&](const u32x4* b, int nt) -> u32x4 {
-    const u32x4 w = b[16 * nt];
-    if (nt == NT - 1) return last_row_ok ? w : u32x4{0u, 0u, 0u, 0u};
-    return w;
-  };
+  // Table rows past the tile's last row (zero padding up to 16 * NT, or with an
+  // exact pitch the next chunk's rows) are read as they are: W row o only
+  // feeds output column o of the MFMA, and the epilogue stores no column past
+  // o_last, so no load waits on a mask before the next step's MFMAs.
+  auto brd = [&](const u32x4* b, int nt) -> u32x4 { return b[16 * nt]; };
   constexpr uint32_t kOff = 0x80000000u;  // voffset that reads 0
 
   // Each wave takes groups of kGroup token tiles (64 tokens): per k step it
