@@ -18,6 +18,8 @@
 // csrc/block_fht_ext_cuda.cu:185-223 and :568-622 (backward).
 #include "bfht_block.h"
 
+#include <algorithm>
+
 namespace lwl {
 
 // Element access of the per-generator launches: the slice in the latent dtype.
@@ -275,8 +277,11 @@ __device__ __forceinline__ void tile_fht_bits(float* lds, int tid) {
 // buffer), transforms its bit group (`pre`), applies the sign layer
 // `sign_layer`, transforms the same bit group again (`post`), scales, and
 // stores it (work buffer, output slice, or partial gradient row).  Each thread
-// hashes one of the tile's 1024 sign words into a shared table.  Grid: one
-// workgroup per (block slot, tile), 2^(LB-15) tiles per block.
+// hashes one of the tile's 1024 sign words into a shared table.  Tiles are
+// numbered slot * 2^(LB-15) + tile (2^(LB-15) tiles per block slot); the grid is
+// persistent (one workgroup per CU walks tiles blockIdx.x, + gridDim.x, ...) and
+// loads the next tile into registers while it transforms the current one, so a
+// CU's loads, transforms and stores overlap.
 //
 // Element r * 1024 + tid of the tile sits at block position pt(tid) + pr(r)
 // (disjoint bit fields), so each thread keeps one 32-bit offset and adds a
@@ -286,7 +291,8 @@ __device__ __forceinline__ void tile_fht_bits(float* lds, int tid) {
 template <class T, int SRC, int DST, int TL>
 __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
     const T* __restrict__ src_io, float* __restrict__ work, T* __restrict__ dst_io, int LB, int pre, int post,
-    int n, int64_t first_block, int64_t start, int64_t stop, uint32_t seed32, int sign_layer, float scale) {
+    int n, int64_t first_block, int64_t ntiles_total, int64_t start, int64_t stop, uint32_t seed32, int sign_layer,
+    float scale) {
   __shared__ float lds[kTilePadded];
   __shared__ uint32_t words[kTileElems / 32];
   static_assert(kTileElems / 32 == kTileThreads, "one sign word per thread");
@@ -294,76 +300,88 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
   constexpr bool high = TL > 0;
   const int tid = threadIdx.x;
   const int tiles_log = LB - kTileLog;  // log2 tiles per block
-  const int64_t slot = (int64_t)blockIdx.x >> tiles_log;
-  const int tile = (int)(blockIdx.x & ((1u << tiles_log) - 1));
-  const int64_t block = first_block + slot;
   const int64_t B = (int64_t)1 << LB;
-  const int64_t base = block * B;  // global coordinate of the block's position 0
   constexpr int col_log = kTileLog - TL;  // high tile: columns per row (>= 7 for LB <= 23)
   constexpr int lo_bit = high ? col_log : 0;  // the tile-index bits the pass transforms
 
   // tile element e -> block position; elements 32q .. 32q+31 are positions
   // pos(32q) .. pos(32q)+31 (columns are at least 32 wide)
-  auto pos = [&](uint32_t e) -> uint32_t {
+  auto pos = [&](uint32_t e, int tile) -> uint32_t {
     if (!high) return ((uint32_t)tile << kTileLog) | e;
     const uint32_t row = e >> col_log, col = e & ((1u << col_log) - 1);
     return (row << kTileLog) | ((uint32_t)tile << col_log) | col;
   };
-  words[tid] = sign_word(block_key(seed32, block), layer_key(sign_layer), pos(32u * tid) >> 5);
-  // pos(r * 1024 + tid) = pos(tid) + (pos(r * 1024) - pos(0)) for the disjoint fields
-  const int pt = (int)pos((uint32_t)tid);
-  const int p0 = (int)pos(0u);
-  auto pr = [&](int r) { return (int)pos((uint32_t)r * kTileThreads) - p0; };
+  // pos(r * 1024 + tid) = pos(tid) + pr(r): the register's field does not depend on the tile
+  auto pr = [&](int r) { return (int)pos((uint32_t)r * kTileThreads, 0); };
+
+  struct Geo {
+    int64_t slot, block, base, lo, hi;  // block-local slice range [lo, hi) (grad / out)
+    int tile, pt;
+  };
+  auto geo = [&](int64_t t) {
+    Geo g;
+    g.slot = t >> tiles_log;
+    g.tile = (int)(t & ((1 << tiles_log) - 1));
+    g.block = first_block + g.slot;
+    g.base = g.block * B;
+    g.lo = start - g.base > 0 ? start - g.base : 0;
+    g.hi = stop - g.base < B ? stop - g.base : B;
+    g.pt = (int)pos((uint32_t)tid, g.tile);
+    return g;
+  };
+  auto load_tile = [&](const Geo& g, float (&x)[32]) {
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      if constexpr (SRC == kSrcLatent) {
+        x[r] = buf_load<T>(tile_rsrc(src_io, (uint64_t)n * sizeof(T)), g.pt + pr(r));
+      } else if constexpr (SRC == kSrcGrad) {
+        // buffer over grad[lo..hi) of this block, indexed by block position - lo
+        const T* g0 = src_io + (g.base + g.lo - start);
+        x[r] = buf_load<T>(tile_rsrc(g0, (uint64_t)(g.hi - g.lo) * sizeof(T)), g.pt + pr(r) - (int)g.lo);
+      } else {
+        x[r] = buf_load<float>(tile_rsrc(work + g.slot * B, (uint64_t)B * 4), g.pt + pr(r));
+      }
+    }
+  };
 
   // padded LDS index of element r * 1024 + tid: lt + r * (1024 + 32)
   const int lt = tid + (tid >> 5);
   constexpr int kRowStride = kTileThreads + kTileThreads / 32;
-  // block-local range [lo, hi) of the slice (grad / out)
-  const int64_t lo = start - base > 0 ? start - base : 0;
-  const int64_t hi = stop - base < B ? stop - base : B;
-  float x[16];
+  float x[32];
+  int64_t t = blockIdx.x;
+  if (t < ntiles_total) load_tile(geo(t), x);
+  for (; t < ntiles_total; t += gridDim.x) {
+    const Geo g = geo(t);
+    __syncthreads();  // the previous tile's LDS reads (sign table, stores) are done
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+    for (int r = 0; r < 32; ++r) lds[lt + r * kRowStride] = x[r];
+    words[tid] = sign_word(block_key(seed32, g.block), layer_key(sign_layer), pos(32u * tid, g.tile) >> 5);
+    if (t + gridDim.x < ntiles_total) load_tile(geo(t + gridDim.x), x);  // in flight during the transforms
+    if (pre)
+      tile_fht_bits<lo_bit>(lds, tid);
+    else
+      __syncthreads();
+    // each thread flips only the elements it stored, after the barrier that
+    // published the sign table
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int r = 16 * half + j;
-      if constexpr (SRC == kSrcLatent) {
-        x[j] = buf_load<T>(tile_rsrc(src_io, (uint64_t)n * sizeof(T)), pt + pr(r));
-      } else if constexpr (SRC == kSrcGrad) {
-        // buffer over grad[lo..hi) of this block, indexed by block position - lo
-        const T* g0 = src_io + (base + lo - start);
-        x[j] = buf_load<T>(tile_rsrc(g0, (uint64_t)(hi - lo) * sizeof(T)), pt + pr(r) - (int)lo);
-      } else {
-        x[j] = buf_load<float>(tile_rsrc(work + slot * B, (uint64_t)B * 4), pt + pr(r));
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) lds[lt + (16 * half + j) * kRowStride] = x[j];
-  }
-  if (pre)
-    tile_fht_bits<lo_bit>(lds, tid);
-  else
-    __syncthreads();
-  // each thread flips only the elements it loaded, after the barrier that
-  // published the sign table
-#pragma unroll
-  for (int r = 0; r < 32; ++r)  // element r * 1024 + tid: word r * 32 + tid / 32, bit tid % 32
-    lds[lt + r * kRowStride] = signed_by(lds[lt + r * kRowStride], words[r * 32 + (tid >> 5)], tid & 31);
-  if (post)
-    tile_fht_bits<lo_bit>(lds, tid);
-  else
-    __syncthreads();
+    for (int r = 0; r < 32; ++r)  // element r * 1024 + tid: word r * 32 + tid / 32, bit tid % 32
+      lds[lt + r * kRowStride] = signed_by(lds[lt + r * kRowStride], words[r * 32 + (tid >> 5)], tid & 31);
+    if (post)
+      tile_fht_bits<lo_bit>(lds, tid);
+    else
+      __syncthreads();
 
 #pragma unroll
-  for (int r = 0; r < 32; ++r) {
-    const float v = lds[lt + r * kRowStride] * scale;
-    if constexpr (DST == kDstWork) {
-      buf_store<float>(v, tile_rsrc(work + slot * B, (uint64_t)B * 4), pt + pr(r));
-    } else if constexpr (DST == kDstOut) {
-      T* o0 = dst_io + (base + lo - start);
-      buf_store<T>(v, tile_rsrc(o0, (uint64_t)(hi - lo) * sizeof(T)), pt + pr(r) - (int)lo);
-    } else {  // kDstPartial: the first n positions, left in the work buffer
-      buf_store<float>(v, tile_rsrc(work + slot * B, (uint64_t)n * 4), pt + pr(r));
+    for (int r = 0; r < 32; ++r) {
+      const float v = lds[lt + r * kRowStride] * scale;
+      if constexpr (DST == kDstWork) {
+        buf_store<float>(v, tile_rsrc(work + g.slot * B, (uint64_t)B * 4), g.pt + pr(r));
+      } else if constexpr (DST == kDstOut) {
+        T* o0 = dst_io + (g.base + g.lo - start);
+        buf_store<T>(v, tile_rsrc(o0, (uint64_t)(g.hi - g.lo) * sizeof(T)), g.pt + pr(r) - (int)g.lo);
+      } else {  // kDstPartial: the first n positions, left in the work buffer
+        buf_store<float>(v, tile_rsrc(work + g.slot * B, (uint64_t)n * 4), g.pt + pr(r));
+      }
     }
   }
 }
@@ -409,12 +427,13 @@ static hipError_t dispatch_block(int LB, bool fwd, const BfhtArgs& a, hipStream_
 template <class T, int SRC, int DST>
 static hipError_t launch_tile_kind(const BfhtArgs& a, hipStream_t s, int tl, int pre, int post, int layer,
                                    float scale, unsigned grid) {
+  const int64_t ntiles = a.nblocks << (a.log_block - kTileLog);
   constexpr bool typed = SRC != kSrcWork || DST == kDstOut;
   using U = std::conditional_t<typed, T, float>;
 #define LWL_TILE(TL)                                                                                      \
   hipLaunchKernelGGL((bfht_tile_pass<U, SRC, DST, TL>), dim3(grid), dim3(kTileThreads), 0, s,            \
                      (const U*)a.src, (float*)a.work, (U*)a.dst, a.log_block, pre, post, (int)a.n,         \
-                     a.first_block, a.start, a.stop, a.seed32, layer, scale)
+                     a.first_block, ntiles, a.start, a.stop, a.seed32, layer, scale)
   switch (tl) {
     case 0: LWL_TILE(0); break;
     case 1: if constexpr (SRC == kSrcWork) LWL_TILE(1); break;
@@ -449,9 +468,23 @@ static hipError_t launch_tile_pass(const BfhtArgs& a, hipStream_t s, int src, in
 // Pass k >= 1 completes layer k - 1 and applies its 2^(-LB/2).  The backward
 // runs the same schedule on grad with the sign layers in reverse (D_L first,
 // D_0 last) and leaves partial rows of n values for the block sum.
+// Workgroups of the persistent tile passes: one per CU (a workgroup takes all
+// of a CU's LDS), never more than the tiles.
+static unsigned tile_grid(int64_t ntiles) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      cus = v;
+    else
+      cus = 256;
+  }
+  return (unsigned)std::min<int64_t>(ntiles, cus);
+}
+
 template <class T>
 static hipError_t run_tiles(const BfhtArgs& a, hipStream_t s, bool fwd) {
-  const unsigned grid = (unsigned)(a.nblocks << (a.log_block - kTileLog));
+  const unsigned grid = tile_grid(a.nblocks << (a.log_block - kTileLog));
   const int L = a.layers;
   const int LB = a.log_block;
   const float norm = (LB & 1) ? 0.70710678118654752440f / (float)(1 << (LB >> 1)) : 1.0f / (float)(1 << (LB >> 1));
