@@ -26,6 +26,8 @@
 // block per 8-token tile and requires block_size % in_features == 0).
 #include "bfht_mfma_chain.h"
 
+#include <type_traits>
+
 namespace lwl {
 namespace {
 
@@ -37,7 +39,7 @@ constexpr int kTokTile = 16;  // tokens per MFMA tile
 constexpr int kXcds = 8;      // MI355X: workgroup i is dispatched to XCD i % 8
 constexpr int kKStep = 32;    // k per MFMA
 constexpr int kGroup = 4;     // token tiles per wave pass (each W read feeds kGroup MFMAs)
-constexpr int kDepth = 4;     // x prefetch distance in k steps
+constexpr int kDepth = 4;     // x prefetch distance in k steps (and nsteps' rounding)
 
 // Scattered bf16 store written through the XCD's L2 (sc0 sc1).  The combine
 // kernel's stores touch one 2-byte element per 128-byte line; written back,
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(256) void bfht_linear_tile_x(const __bf16* __restri
   }
 }
 
-template <int L, int NT, bool kTiled, int KB>
+template <int L, int NT, bool kTiled, int KB, int KG = kGroup, int KD = kDepth>
 __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __restrict__ x,
                                                                const __bf16* __restrict__ latent,
                                                                __bf16* __restrict__ out,
@@ -294,19 +296,21 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   auto brd = [&](const u32x4* b, int nt) -> u32x4 { return b[16 * nt]; };
   constexpr uint32_t kOff = 0x80000000u;  // voffset that reads 0
 
-  // Each wave takes groups of kGroup token tiles (64 tokens): per k step it
-  // reads the NT W tiles once from LDS and issues kGroup * NT MFMAs; x is
-  // prefetched kDepth steps ahead into a register ring.  The loop body has no
-  // branches, so the compiler can count the loads in flight.
-  for (int tg = tt0 + kGroup * wave; tg < tt1; tg += kGroup * kWaves) {
-    uint32_t xo[kGroup];
+  // A pass takes G consecutive token tiles (16 G tokens) of this wave: per k
+  // step it reads the NT W tiles once from LDS and issues G * NT MFMAs; x is
+  // prefetched KD steps ahead into a register ring (KD divides kDepth, the
+  // rounding of nsteps).  The loop body has no branches, so the compiler can
+  // count the loads in flight.  Tiles from `tend` on are masked.
+  auto pass = [&](auto g_const, int tg, int tend) {
+    constexpr int G = decltype(g_const)::value;
+    uint32_t xo[G];
 #pragma unroll
-    for (int g = 0; g < kGroup; ++g) {
+    for (int g = 0; g < G; ++g) {
       const int tt = tg + g, t = tt * kTokTile + l16;
       if constexpr (kTiled)
-        xo[g] = tt < tt1 ? (uint32_t)((tt * xsteps * 64 + lane) * 16) : kOff;
+        xo[g] = tt < tend ? (uint32_t)((tt * xsteps * 64 + lane) * 16) : kOff;
       else
-        xo[g] = (tt < tt1 && t < tokens) ? (uint32_t)((t * in_f + 8 * kq) * 2) : kOff;
+        xo[g] = (tt < tend && t < tokens) ? (uint32_t)((t * in_f + 8 * kq) * 2) : kOff;
     }
     // steps past the row (row-major: the lanes whose 8 k-values lie past it,
     // all or none as in % 8 == 0) read 0
@@ -319,19 +323,19 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
         return __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)off, step * kKStep * 2, 0);
       }
     };
-    f32x4v acc[kGroup][NT];
+    f32x4v acc[G][NT];
 #pragma unroll
-    for (int g = 0; g < kGroup; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) acc[g][nt] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    // Issue the first kDepth steps' loads in slot order, the order the loop
+    // Issue the first KD steps' loads in slot order, the order the loop
     // refills them in: the wait counts the compiler derives at the loop
     // head then let slot d's data arrive behind the later slots' requests.
-    u32x4 ring[kDepth][kGroup];
+    u32x4 ring[KD][G];
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
+    for (int d = 0; d < KD; ++d) {
 #pragma unroll
-      for (int g = 0; g < kGroup; ++g) ring[d][g] = xload(g, d);
+      for (int g = 0; g < G; ++g) ring[d][g] = xload(g, d);
       __builtin_amdgcn_sched_barrier(0);
     }
     // W tiles of step s are read one step ahead (bt holds step s, bn step s + 1),
@@ -340,9 +344,9 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
     u32x4 bt[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) bt[nt] = brd(bs, nt);
-    for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
+    for (int s0 = 0; s0 < nsteps; s0 += KD) {
 #pragma unroll
-      for (int d = 0; d < kDepth; ++d) {
+      for (int d = 0; d < KD; ++d) {
         const int sn = (s0 + d + 1 < nsteps) ? s0 + d + 1 : s0 + d;
         const u32x4* bsn = brow + sn * (4 * pitch + 1);
         u32x4 bn[NT];
@@ -350,7 +354,7 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
         for (int nt = 0; nt < NT; ++nt) bn[nt] = brd(bsn, nt);
         bs = bsn;
 #pragma unroll
-        for (int g = 0; g < kGroup; ++g)
+        for (int g = 0; g < G; ++g)
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) acc[g][nt] = mfma16(ring[d][g], bt[nt], acc[g][nt]);
 #pragma unroll
@@ -361,7 +365,7 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
         // loop back-edge, which serialises the whole prefetch.
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int g = 0; g < kGroup; ++g) ring[d][g] = xload(g, s0 + d + kDepth);
+        for (int g = 0; g < G; ++g) ring[d][g] = xload(g, s0 + d + KD);
       }
     }
     // D[m = 4*kq + r][n = l16]: token 16 tt + 4 kq + r, row o_first + 16 nt + l16.
@@ -369,9 +373,9 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
     // of out and of the partials (tokens past the end fall outside them), and an
     // element that does not belong in a destination gets the offset that drops it.
 #pragma unroll
-    for (int g = 0; g < kGroup; ++g) {
+    for (int g = 0; g < G; ++g) {
       const int tt = tg + g;
-      if (tt >= tt1) continue;  // uniform across the wave
+      if (tt >= tend) continue;  // uniform across the wave
       const int t0 = tt * kTokTile;
       const int nt_tok = tokens - t0 < kTokTile ? tokens - t0 : kTokTile;
       const auto o_r = rsrc(out + (int64_t)t0 * out_f, (uint32_t)(nt_tok * out_f * 2));
@@ -402,9 +406,27 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
         }
       }
     }
+  };
+
+  // Whole rounds in which every wave takes KG tiles, then the remainder.  With
+  // three or more row tiles a single-tile pass still issues 3+ MFMAs per load,
+  // so the remainder is split evenly over the waves in single-tile passes (a
+  // round with only some waves busy would leave the CU's other SIMDs idle for a
+  // whole KG-tile pass); with one or two row tiles a single-tile pass waits on
+  // its loads, and the remainder runs as KG-tile passes.
+  const int full = (tt1 - tt0) / (KG * kWaves);
+  for (int r = 0; r < full; ++r) pass(std::integral_constant<int, KG>{}, tt0 + (r * kWaves + wave) * KG, tt1);
+  const int rest0 = tt0 + full * KG * kWaves;
+  if constexpr (NT >= 3) {
+    const int per = (tt1 - rest0 + kWaves - 1) / kWaves;
+    for (int i = 0; i < per; ++i) {
+      const int tt = rest0 + wave * per + i;
+      if (tt < tt1) pass(std::integral_constant<int, 1>{}, tt, tt1);  // uniform across the wave
+    }
+  } else {
+    for (int tg = rest0 + KG * wave; tg < tt1; tg += KG * kWaves) pass(std::integral_constant<int, KG>{}, tg, tt1);
   }
 }
-
 // Rows straddling tiles b-1 and b: out[t][o] = scale * (last(b-1)[t] + first(b)[t]).
 __global__ __launch_bounds__(256) void bfht_linear_combine(const float* __restrict__ partial,
                                                            __bf16* __restrict__ out, int tokens, int in_f,
@@ -430,7 +452,8 @@ hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial
   auto* lat = (const __bf16*)a.latent;
   auto* o = (__bf16*)a.out;
 #define LWL_LIN(NT)                                                                                               \
-  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT, kTiled, KB>), grid, block, 0, s, x, lat, o, partial,              \
+  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT, kTiled, KB>), \
+                     grid, block, 0, s, x, lat, o, partial,                                                      \
                      (int)a.tokens, (int)a.in_features, (int)a.out_features, (int)a.n, a.seed32, a.weight_scale, \
                      a.token_splits, a.nblocks_w, pitch)
   switch (nt) {
@@ -486,11 +509,11 @@ bool linear_applicable(int dtype, int log_block, int64_t in_features) {
 
 int linear_blocks_per_wg(const LinearArgs& a) {
   // Two blocks per workgroup for batches read from the tiled x copy when a block
-  // holds few rows (at most 32: the contraction is bound by streaming x, and two
-  // blocks feed each x element twice the rows), their rows fit the register
-  // budget and their table the LDS.  With more rows per block the loop is fed
-  // well enough and a second generator chain per workgroup costs more than it saves.
-  if (!linear_tiled(a) || a.nblocks_w < 2 || linear_rows(a.in_features, 1) > 32) return 1;
+  // holds at most 64 rows (the contraction is bound by streaming x, and two
+  // blocks feed each x element twice the rows: at 768 -> 3072 the second chain
+  // costs ~7 us and the contraction saves ~13), their rows fit the register
+  // budget and their table the LDS.
+  if (!linear_tiled(a) || a.nblocks_w < 2 || linear_rows(a.in_features, 1) > 64) return 1;
   if (linear_row_tiles(a.in_features, 2) > kMaxNT2) return 1;
   return linear_pitch_fits(a.in_features, 2) ? 2 : 1;
 }

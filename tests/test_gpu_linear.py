@@ -44,7 +44,9 @@ def oracle_linear(x: torch.Tensor, latent: torch.Tensor, out_f: int, layers: int
         (20, 528, 200, 32768, 3, 31, 1.0),      # smallest in_features: 4 row tiles per block
         (40, 5120, 30, 32768, 2, 32, 1.0),      # largest: the k-major table fills all 160 KiB of LDS
         (333, 2048, 90, 32768, 3, 33, 1.0),     # two blocks per workgroup, exact table pitch (33 rows)
-        (280, 1064, 90, 32768, 2, 36, 1.0),     # 32 rows per block (the two-block limit): 64-row tiles
+        (280, 1064, 90, 32768, 2, 36, 1.0),     # 32 rows per block: two blocks in 64-row tiles
+        (320, 704, 64, 32768, 3, 37, 1.0),      # two blocks of 47 rows (6 row tiles), one token tile per workgroup
+        (6144, 768, 3072, 32768, 3, 38, 1.0),   # two blocks per workgroup, 55 token tiles: one full round + 3 singles
         (600, 3072, 100, 32768, 2, 34, 0.5),    # two blocks per workgroup, 23-row pitch, 5 tiles
         (300, 5120, 41, 32768, 3, 35, 1.0),     # two blocks per workgroup, one row tile, last tile single
     ],
