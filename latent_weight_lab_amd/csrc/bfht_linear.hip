@@ -64,7 +64,8 @@ constexpr int kMaxNT = 4;
 constexpr int kLinearMaxIn = 5120;  // the range the tests cover (the table itself would fit larger rows)
 constexpr int kMaxNT2 = 6;  // two blocks per workgroup: 16-row tiles (register budget)
 constexpr int kLinearLdsBytes = 160 * 1024;
-static_assert(kLinearLdsBytes >= kChainLdsBytes, "the generator chain runs in the same LDS");
+static_assert(kLinearLdsBytes >= kChainLdsBytes && kLinearLdsBytes >= kChain2LdsBytes,
+              "the generator chains run in the same LDS");
 
 // output rows a tile of kb blocks can touch, incl. the two partial ones
 __host__ __device__ constexpr int64_t linear_rows(int64_t in_features, int kb) {
@@ -218,20 +219,26 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
     const int base_rel = c_first << 3;
     const float inv_in = 1.0f / (float)in_f;
     u32x4 v[KB][8];
+    if (KB == 2 && tile * KB + 1 < nblocks) {  // both blocks at once (uniform across the workgroup)
+      const Ctx c[2] = {make_ctx(seed32, tile * KB), make_ctx(seed32, tile * KB + 1)};
+      u32x4 src[kTiles][2];
+      load_latent(c[0], latent, n, src);
+      f32x16 acc[2][kTiles];
+      uint32_t nw[2][4];
+      run_chain2<L>(acc, c, lds, src, [](int i) { return i; }, nw);
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      const int64_t block = tile * KB + kb;
-      if (kb > 0) __syncthreads();  // every wave has read the previous chain's last exchange
-      if (block < nblocks) {       // uniform across the workgroup
-        const Ctx c = make_ctx(seed32, block);
-        u32x4 src[kTiles][2];
-        load_latent(c, latent, n, src);
-        f32x16 acc[kTiles];
-        uint32_t nw[4];
-        run_chain<L>(acc, c, lds, src, [](int i) { return i; }, nw);
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[kb][k] = out_chunk<L>(acc, nw, c, k);
-      }
+        for (int k = 0; k < 8; ++k) v[kb][k] = out_chunk<L>(acc[kb], nw[kb], c[kb], k);
+    } else {  // one block (KB = 1, or the last tile of an odd block count)
+      const Ctx c = make_ctx(seed32, tile * KB);
+      u32x4 src[kTiles][2];
+      load_latent(c, latent, n, src);
+      f32x16 acc[kTiles];
+      uint32_t nw[4];
+      run_chain<L>(acc, c, lds, src, [](int i) { return i; }, nw);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[0][k] = out_chunk<L>(acc, nw, c, k);
     }
     __syncthreads();  // every wave has read its last exchange
     // Zero exactly the entries of the tile's rows that the scatter leaves out

@@ -365,6 +365,80 @@ __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, u
   }
 }
 
+// Two blocks of the same latent through the chain together (the fused linear's
+// two-block workgroups): the stages of both interleave, so one block's MFMAs
+// and VALU work fill the other's dependency waits, and both share each
+// layer's barrier and the source operands (the latent is the same; only the
+// sign words differ).  LDS (kChain2LdsBytes): one exchange buffer per block
+// (64 KiB each) and one sign-word table per block; a buffer is rewritten every
+// layer, so layers after the first wait at a second barrier until every wave
+// has read the previous layer's exchange.  Results as run_chain, per block.
+constexpr int kChain2LdsBytes = 2 * kXBufBytes + 2 * kWordTableBytes;
+
+template <int L, class SignLayer>
+__device__ __forceinline__ void run_chain2(f32x16 (&acc)[2][kTiles], const Ctx (&x)[2], unsigned char* lds,
+                                           const u32x4 (&src)[kTiles][2], SignLayer sign_layer,
+                                           uint32_t (&fin)[2][4]) {
+  uint32_t* wtab[2] = {reinterpret_cast<uint32_t*>(lds + 2 * kXBufBytes),
+                       reinterpret_cast<uint32_t*>(lds + 2 * kXBufBytes + kWordTableBytes)};
+  u32x2* xbuf[2] = {reinterpret_cast<u32x2*>(lds), reinterpret_cast<u32x2*>(lds + kXBufBytes)};
+  uint32_t nw[2][L][4];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    layer_words<false>(x[b], sign_layer(0), nw[b][0]);
+    fill_words<L>(x[b], wtab[b], sign_layer);
+  }
+  const int lane = threadIdx.x & 63;
+  u32x4 hq4[2], hq8[2], hs4[2], hlast[2];
+  walsh_operand(kWalshQ4, lane, hq4);
+  walsh_operand(kWalshQ8, lane, hq8);
+  walsh_operand(kWalshS4, lane, hs4);
+  walsh_operand(L == 1 ? kWalshSL1 : L == 2 ? kWalshQ8 : kWalshSL3, lane, hlast);
+  const f32x16 zero = {};
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    const bool odd = i & 1;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if (i == 0) {
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+          u32x4 a[2] = {src[t][0], src[t][1]};
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<false>(nw[b][0], t, c, v);
+          f32x16 d = mfma(a[0], hq4[0], zero);
+          acc[b][t] = mfma(a[1], hq4[1], d);
+        }
+      } else if (odd) {
+        stage_rows<true, true>(acc[b], hs4, nw[b][i]);
+      } else {
+        stage_rows<true, false>(acc[b], hq4, nw[b][i]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) stage_rows<false, false>(acc[b], hq8, nw[b][i]);
+    if (i > 0) __syncthreads();  // every wave has read layer i - 1's exchange
+#pragma unroll
+    for (int b = 0; b < 2; ++b) exchange_write(acc[b], xbuf[b], x[b]);
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if (i + 1 < L) {
+        if ((i + 1) & 1)
+          read_words<true, true>(x[b], wtab[b], i, nw[b][i + 1]);
+        else
+          read_words<false, true>(x[b], wtab[b], i, nw[b][i + 1]);
+      } else {
+        read_words<(L % 2) == 1, false>(x[b], wtab[b], L - 1, fin[b]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) exchange_read_stage_c(acc[b], i == L - 1 ? hlast : (odd ? hq4 : hs4), xbuf[b], x[b]);
+  }
+}
+
 // Cache policy of the kernels' large output stores: sc0 | sc1 (system scope)
 // writes through the XCD's L2.  The L2s of the XCDs are not coherent with each
 // other, so a kernel's end writes every dirty L2 line back before the next
