@@ -99,8 +99,9 @@ __device__ __forceinline__ uint32_t swap_idx34(uint32_t x) {
 // Walsh operands: for lane l and register pair (c, v), entries k = 16c +
 // 8*(l>>5) + 2v + {0, 1}, o = l & 31, equal scale * (-1)^popcount(remap(k) & o)
 // where remap moves k bit i to bit M[i].  The same registers serve as B operand
-// (o = column) and as A operand (o = row).  Precomputed at compile time as bf16
-// pairs for the five (permutation, scale) combinations the kernels use:
+// (o = column) and as A operand (o = row).  make_walsh_table spells them out as
+// bf16 pairs for the five (permutation, scale) combinations the kernels use
+// (walsh_words below builds the same words in registers, checked at compile time):
 //   Q = (0,1,3,2,4) (k bits 2 and 3 exchanged), S = (1,0,2,3,4) (bits 0 and 1);
 //   bf16 0x3e80 = 1/4, 0x3e00 = 1/8, 0x3e35 = bf16(2^-2.5), 0x3db5 = bf16(2^-3.5).
 enum { kWalshQ4, kWalshQ8, kWalshS4, kWalshSL1, kWalshSL3, kWalshSets };
@@ -131,12 +132,55 @@ constexpr WalshTable make_walsh_table() {
   return tab;
 }
 
-__device__ const WalshTable kWalsh = make_walsh_table();
+
+// The same operands computed from the lane index (the table above is their
+// definition; the chain builds them in registers, which saves every CU a
+// 64 KiB read at the start of each block).  With o' the lane's column bits
+// moved by the set's permutation (o'_i = bit perm[i] of o), entry k has the
+// sign parity(k & o'), and k = 16c + 8h + 2v + s puts s, v0, v1, h, c at
+// bits 0-4: word (c, v) = mag * 0x10001 with the high half's sign s-flipped by
+// o'_0 and both signs flipped by h o'_3 ^ c o'_4 ^ v0 o'_1 ^ v1 o'_2.
+__host__ __device__ constexpr uint32_t walsh_perm_bit(int set, int i) {
+  // Q = (0,1,3,2,4) for the Q sets, S = (1,0,2,3,4) for the S sets
+  return (set == kWalshQ4 || set == kWalshQ8) ? (i == 2 ? 3 : i == 3 ? 2 : i) : (i == 0 ? 1 : i == 1 ? 0 : i);
+}
+__host__ __device__ constexpr uint32_t walsh_mag(int set) {
+  return set == kWalshQ4 ? 0x3e80u : set == kWalshQ8 ? 0x3e00u : set == kWalshS4 ? 0x3e80u
+       : set == kWalshSL1 ? 0x3e35u : 0x3db5u;
+}
+__host__ __device__ constexpr void walsh_words(int set, int lane, uint32_t (&w)[8]) {
+  const uint32_t o = (uint32_t)lane & 31u, h = (uint32_t)lane >> 5;
+  auto ob = [&](int i) { return (o >> walsh_perm_bit(set, i)) & 1u; };
+  const uint32_t both = kPairSign;
+  const uint32_t base = walsh_mag(set) * 0x10001u ^ (ob(0) << 31) ^ ((h & ob(3)) ? both : 0u);
+  const uint32_t m1 = ob(1) ? both : 0u, m2 = ob(2) ? both : 0u, m4 = ob(4) ? both : 0u;
+  w[0] = base;
+  w[1] = base ^ m1;
+  w[2] = base ^ m2;
+  w[3] = w[1] ^ m2;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) w[4 + v] = w[v] ^ m4;
+}
+
+// Compile-time check: the register construction equals the table, entry by entry.
+constexpr bool walsh_words_match_table() {
+  const WalshTable tab = make_walsh_table();
+  for (int set = 0; set < kWalshSets; ++set)
+    for (int lane = 0; lane < 64; ++lane) {
+      uint32_t w[8] = {};
+      walsh_words(set, lane, w);
+      for (int i = 0; i < 8; ++i)
+        if (w[i] != tab.v[set][lane][i]) return false;
+    }
+  return true;
+}
+static_assert(walsh_words_match_table(), "Walsh operands built in registers differ from their definition");
 
 __device__ __forceinline__ void walsh_operand(int set, int lane, u32x4 (&h)[2]) {
-  const u32x4* row = reinterpret_cast<const u32x4*>(kWalsh.v[set][lane]);
-  h[0] = row[0];
-  h[1] = row[1];
+  uint32_t w[8] = {};
+  walsh_words(set, lane, w);
+  h[0] = u32x4{w[0], w[1], w[2], w[3]};
+  h[1] = u32x4{w[4], w[5], w[6], w[7]};
 }
 
 struct Ctx {
