@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -97,10 +98,13 @@ size_t forward_ws(const lwl::BfhtArgs& a) {
 
 size_t backward_ws(const lwl::BfhtArgs& a) {
   if (a.nblocks == 0) return 0;
-  // whole-block kernels: one float32 partial row of n values per block (the
-  // matrix-core kernel writes it even for a single block)
-  if (a.log_block <= lwl::kWholeBlockMaxLog)
-    return align_up((size_t)a.nblocks * (size_t)a.n * sizeof(float));
+  // whole-block kernels: one float32 partial row of n values per block, or
+  // (matrix-core kernel, which writes it even for a single block) one
+  // bfloat16 row padded to 8 values
+  if (a.log_block <= lwl::kWholeBlockMaxLog) {
+    const size_t row = std::max((size_t)a.n * sizeof(float), (size_t)lwl::mfma15_part_stride(a.n) * 2);
+    return align_up((size_t)a.nblocks * row);
+  }
   return align_up((size_t)a.nblocks * ((size_t)1 << a.log_block) * sizeof(float));
 }
 

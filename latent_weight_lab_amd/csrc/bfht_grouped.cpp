@@ -51,8 +51,12 @@ ClassKey class_of(const WeightJob& j, bool fwd) {
   return ClassKey{mfma, j.ldtype, mfma ? kBF16 : j.wdtype, lb, mfma ? j.layers : 0};
 }
 
-// Partial rows of the backward are 128-byte aligned: n rounded up to 32 floats.
-int64_t row_stride(const WeightJob& j) { return (j.n + 31) / 32 * 32; }
+// Partial rows of the backward: bfloat16 for the matrix-core chain (as in its
+// per-module launch), float32 otherwise; 128-byte aligned, so n is rounded up
+// to 64 bfloat16 or 32 float32 values.
+bool part_bf16(const WeightJob& j) { return class_of(j, false).mfma; }
+int64_t row_stride(const WeightJob& j) { return part_bf16(j) ? (j.n + 63) / 64 * 64 : (j.n + 31) / 32 * 32; }
+size_t row_bytes(const WeightJob& j) { return (size_t)row_stride(j) * (part_bf16(j) ? 2 : 4); }
 
 size_t partial_bytes(const WeightJob& j);
 
@@ -68,9 +72,9 @@ int64_t workgroups_of(const ClassKey& k, const WeightJob& j) {
   return (blocks_of(j) + g - 1) / g;
 }
 
-size_t partial_bytes(const WeightJob& j) { return align_up((size_t)blocks_of(j) * (size_t)row_stride(j) * 4); }
+size_t partial_bytes(const WeightJob& j) { return align_up((size_t)blocks_of(j) * row_bytes(j)); }
 
-GroupJob device_job(const WeightJob& j, bool fwd, float* part) {
+GroupJob device_job(const WeightJob& j, bool fwd, void* part) {
   GroupJob d{};
   d.src = fwd ? j.latent : j.grad_weight;
   d.dst = fwd ? j.weight : j.grad_latent;
@@ -78,6 +82,7 @@ GroupJob device_job(const WeightJob& j, bool fwd, float* part) {
   d.size = j.size;
   d.n = (int32_t)j.n;
   d.stride = (int32_t)row_stride(j);
+  d.part_bf16 = !fwd && part_bf16(j);
   d.nblocks = (int32_t)blocks_of(j);
   d.seed32 = j.seed32;
   d.layers = j.layers;
@@ -141,9 +146,9 @@ hipError_t launch_grouped(const WeightJob* jobs, int64_t count, void* work, hipS
   std::vector<ClassKey> keys((size_t)count);
   size_t off = 0;
   for (int64_t i = 0; i < count; ++i) {
-    float* part = nullptr;
+    void* part = nullptr;
     if (!fwd) {
-      part = reinterpret_cast<float*>(static_cast<char*>(work) + off);
+      part = static_cast<char*>(work) + off;
       off += partial_bytes(jobs[i]);
     }
     djobs[i] = device_job(jobs[i], fwd, part);
@@ -169,16 +174,18 @@ hipError_t launch_grouped(const WeightJob* jobs, int64_t count, void* work, hipS
     if (e != hipSuccess) return e;
   }
   if (fwd) return hipSuccess;
-  // fixed-order block sums with the scale / accumulate epilogue, per latent dtype
-  for (int dtype : {kF32, kF16, kBF16}) {
-    std::vector<int> idx;
-    for (int64_t m = 0; m < count; ++m)
-      if (jobs[m].ldtype == dtype) idx.push_back((int)m);
-    const hipError_t e = run_tables(
-        idx, djobs, [&](int m) { return (jobs[m].n + kGroupReduceCols - 1) / kGroupReduceCols; },
-        [&](const GroupTable& t) { return launch_reduce_grouped(t, dtype, s); });
-    if (e != hipSuccess) return e;
-  }
+  // fixed-order block sums with the scale / accumulate epilogue, per latent
+  // dtype and partial-row type
+  for (int dtype : {kF32, kF16, kBF16})
+    for (bool bf16_rows : {false, true}) {
+      std::vector<int> idx;
+      for (int64_t m = 0; m < count; ++m)
+        if (jobs[m].ldtype == dtype && part_bf16(jobs[m]) == bf16_rows) idx.push_back((int)m);
+      const hipError_t e = run_tables(
+          idx, djobs, [&](int m) { return (jobs[m].n + kGroupReduceCols - 1) / kGroupReduceCols; },
+          [&](const GroupTable& t) { return launch_reduce_grouped(t, dtype, bf16_rows, s); });
+      if (e != hipSuccess) return e;
+    }
   return hipSuccess;
 }
 

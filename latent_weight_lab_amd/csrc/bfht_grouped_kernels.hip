@@ -54,7 +54,7 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd_grouped(const Grou
   const int j = group_job(g, (int)blockIdx.x);
   const GroupJob& jb = g.job[j];
   const int64_t slot = (int64_t)(blockIdx.x - g.prefix[j]) * Geo<LB>::G + (threadIdx.x >> Geo<LB>::LT);
-  block_bwd_slot<LB, T>(WeightGradLoad<T, W>{static_cast<const W*>(jb.src)}, jb.part, jb.stride,
+  block_bwd_slot<LB, T>(WeightGradLoad<T, W>{static_cast<const W*>(jb.src)}, static_cast<float*>(jb.part), jb.stride,
                         static_cast<T*>(nullptr), jb.n, 0, slot, jb.nblocks, 0, jb.size, jb.seed32, jb.layers, 0,
                         smem);
 }

@@ -19,6 +19,7 @@
 #include "bfht_block.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace lwl {
 
@@ -95,19 +96,36 @@ struct RedVec<4> { typedef float4 type; };
 // kRedDepth row loads in flight (rows past the end are loaded from row 0 and
 // not added, so the loads need no branch), and wave 0 adds the 8 wave sums in
 // wave order: the result does not depend on kVec or on timing.
+// kVec partial-row elements of type P, loaded together and widened to float
+template <class P, int kVec>
+struct PartVec;
 template <int kVec>
-__device__ __forceinline__ bool reduce_columns(const float* __restrict__ part, int64_t nblocks, int64_t stride,
+struct PartVec<float, kVec> {
+  typedef typename RedVec<kVec>::type type;
+  static __device__ float at(const type& v, int e) {
+    if constexpr (kVec == 1) return v;
+    else return reinterpret_cast<const float*>(&v)[e];
+  }
+};
+template <int kVec>
+struct PartVec<bf16, kVec> {  // kVec bf16 = 2, 4 or 8 bytes
+  typedef typename std::conditional<kVec == 1, uint16_t,
+                                    typename std::conditional<kVec == 2, uint32_t, uint2>::type>::type type;
+  static __device__ float at(const type& v, int e) {
+    return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(&v)[e] << 16);
+  }
+};
+
+template <int kVec, class P = float>
+__device__ __forceinline__ bool reduce_columns(const P* __restrict__ part, int64_t nblocks, int64_t stride,
                                                int n, int c0, float (&sums)[kRedWaves][kVec][64],
                                                float (&t)[kVec]) {
-  typedef typename RedVec<kVec>::type V;
+  typedef typename PartVec<P, kVec>::type V;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float a[kVec];
 #pragma unroll
   for (int e = 0; e < kVec; ++e) a[e] = 0.0f;
-  auto lanes = [](const V& v, int e) -> float {
-    if constexpr (kVec == 1) return v;
-    else return reinterpret_cast<const float*>(&v)[e];
-  };
+  auto lanes = [](const V& v, int e) -> float { return PartVec<P, kVec>::at(v, e); };
   if (c0 + kVec <= n) {
     // every column of the lane is in range: vector loads
     for (int64_t b0 = wave; b0 < nblocks; b0 += (int64_t)kRedWaves * kRedDepth) {
@@ -131,9 +149,9 @@ __device__ __forceinline__ bool reduce_columns(const float* __restrict__ part, i
 #pragma unroll
       for (int j = 0; j < kRedDepth; ++j) {
         const int64_t b = b0 + (int64_t)kRedWaves * j;
-        const float* r = part + (b < nblocks ? b : 0) * stride;
+        const P* r = part + (b < nblocks ? b : 0) * stride;
 #pragma unroll
-        for (int e = 0; e < kVec; ++e) v[j][e] = r[c0 + e < n ? c0 + e : 0];
+        for (int e = 0; e < kVec; ++e) v[j][e] = to_f32(r[c0 + e < n ? c0 + e : 0]);
       }
 #pragma unroll
       for (int j = 0; j < kRedDepth; ++j) {
@@ -156,14 +174,14 @@ __device__ __forceinline__ bool reduce_columns(const float* __restrict__ part, i
   return true;
 }
 
-template <class T, int kVec>
-__global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_blocks(const float* __restrict__ part,
+template <class T, int kVec, class P = float>
+__global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_blocks(const P* __restrict__ part,
                                                                      int64_t nblocks, int64_t stride, int n,
                                                                      T* __restrict__ grad_latent) {
   __shared__ float sums[kRedWaves][kVec][64];
   const int c0 = (blockIdx.x * 64 + (threadIdx.x & 63)) * kVec;
   float t[kVec];
-  if (!reduce_columns<kVec>(part, nblocks, stride, n, c0, sums, t)) return;
+  if (!reduce_columns<kVec, P>(part, nblocks, stride, n, c0, sums, t)) return;
 #pragma unroll
   for (int e = 0; e < kVec; ++e)
     if (c0 + e < n) grad_latent[c0 + e] = from_f32<T>(t[e]);
@@ -179,7 +197,7 @@ __device__ __forceinline__ void grad_store(T* dst, int i, float sum, float scale
   dst[i] = from_f32<T>(r);
 }
 
-template <class T>
+template <class T, class P>
 __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_grouped(const GroupTable g) {
   static_assert(kGroupReduceCols == 64 * 4, "grouped prefix counts reduce tiles of 4 columns per lane");
   __shared__ float sums[kRedWaves][4][64];
@@ -188,21 +206,21 @@ __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_grouped(const Grou
   const int n = jb.n;
   const int c0 = ((blockIdx.x - g.prefix[j]) * 64 + (threadIdx.x & 63)) * 4;
   float t[4];
-  if (!reduce_columns<4>(jb.part, jb.nblocks, jb.stride, n, c0, sums, t)) return;
+  if (!reduce_columns<4, P>(static_cast<const P*>(jb.part), jb.nblocks, jb.stride, n, c0, sums, t)) return;
   T* dst = static_cast<T*>(jb.dst);
 #pragma unroll
   for (int e = 0; e < 4; ++e)
     if (c0 + e < n) grad_store<T>(dst, c0 + e, t[e], jb.scale, jb.accumulate);
 }
 
-template <class T, int kVec>
-static void launch_reduce_vec(const float* part, int64_t nblocks, int64_t stride, int64_t n, T* dst, hipStream_t s) {
+template <class T, int kVec, class P>
+static void launch_reduce_vec(const P* part, int64_t nblocks, int64_t stride, int64_t n, T* dst, hipStream_t s) {
   const dim3 grid((unsigned)((n + 64 * kVec - 1) / (64 * kVec))), block(64 * kRedWaves);
-  hipLaunchKernelGGL((bfht_reduce_blocks<T, kVec>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
+  hipLaunchKernelGGL((bfht_reduce_blocks<T, kVec, P>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
 }
 
-template <class T>
-static hipError_t launch_reduce(const float* part, int64_t nblocks, int64_t stride, int64_t n, T* dst,
+template <class T, class P = float>
+static hipError_t launch_reduce(const P* part, int64_t nblocks, int64_t stride, int64_t n, T* dst,
                                 hipStream_t s) {
   // The widest row loads the stride allows (part is 256-byte aligned) that still
   // give every CU a workgroup: 64 * kVec columns per workgroup.
@@ -511,20 +529,24 @@ static hipError_t run_typed(const BfhtArgs& a, hipStream_t s, bool fwd) {
   if (mfma15_applicable(a)) {
     hipError_t e = launch_mfma15(a, s, fwd);
     if (e != hipSuccess || fwd) return e;
-    return launch_reduce<T>((const float*)a.work, a.nblocks, a.n, a.n, (T*)a.dst, s);
+    return launch_reduce<T, bf16>((const bf16*)a.work, a.nblocks, mfma15_part_stride(a.n), a.n, (T*)a.dst, s);
   }
   if (a.log_block <= kTileLog)
     return dispatch_block<T>(a.log_block, fwd, a, s, std::make_integer_sequence<int, kTileLog + 1>{});
   return run_tiles<T>(a, s, fwd);
 }
 
-hipError_t launch_reduce_grouped(const GroupTable& g, int dtype, hipStream_t s) {
+hipError_t launch_reduce_grouped(const GroupTable& g, int dtype, bool part_bf16, hipStream_t s) {
   if (g.count <= 0 || g.prefix[g.count] == 0) return hipSuccess;
   const dim3 grid((unsigned)g.prefix[g.count]), block(64 * kRedWaves);
+  if (part_bf16 && dtype != kBF16) return hipErrorInvalidValue;  // only the bf16 matrix-core chain writes them
   switch (dtype) {
-    case kF32: hipLaunchKernelGGL((bfht_reduce_grouped<float>), grid, block, 0, s, g); break;
-    case kF16: hipLaunchKernelGGL((bfht_reduce_grouped<f16>), grid, block, 0, s, g); break;
-    case kBF16: hipLaunchKernelGGL((bfht_reduce_grouped<bf16>), grid, block, 0, s, g); break;
+    case kF32: hipLaunchKernelGGL((bfht_reduce_grouped<float, float>), grid, block, 0, s, g); break;
+    case kF16: hipLaunchKernelGGL((bfht_reduce_grouped<f16, float>), grid, block, 0, s, g); break;
+    case kBF16:
+      if (part_bf16) hipLaunchKernelGGL((bfht_reduce_grouped<bf16, bf16>), grid, block, 0, s, g);
+      else hipLaunchKernelGGL((bfht_reduce_grouped<bf16, float>), grid, block, 0, s, g);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

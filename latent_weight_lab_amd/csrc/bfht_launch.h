@@ -37,6 +37,9 @@ hipError_t launch_bfht(const BfhtArgs& a, hipStream_t s, bool forward);
 // Matrix-core path for bfloat16 blocks of exactly 2^15 (bfht_mfma.hip).  The
 // backward writes one float32 partial row of n values per block into `work`.
 bool mfma15_applicable(const BfhtArgs& a);
+// The matrix-core backward's partial rows: bfloat16, rows of n padded to 8
+// elements (16-byte aligned), inside the float32-row workspace.
+__host__ __device__ inline int64_t mfma15_part_stride(int64_t n) { return (n + 7) / 8 * 8; }
 hipError_t launch_mfma15(const BfhtArgs& a, hipStream_t s, bool forward);
 hipError_t launch_sign_words(uint32_t seed32, int64_t block, int layer, int64_t first_word,
                              int64_t nwords, uint32_t* out, hipStream_t s);
@@ -109,10 +112,11 @@ constexpr int kGroupMaxJobs = 32;
 struct GroupJob {
   const void* src;   // forward: latent [n]; backward: grad of the weight [size] (weight dtype)
   void* dst;         // forward: weight [size] (weight dtype); backward: grad_latent [n]
-  float* part;       // backward: nblocks partial rows of n floats, `stride` floats apart
+  void* part;        // backward: nblocks partial rows of n values, `stride` values apart
   int64_t size;
   int32_t n;
-  int32_t stride;    // n rounded up to 32 (128-byte aligned rows)
+  int32_t stride;    // 128-byte aligned rows: n rounded up to 32 floats or 64 bfloat16
+  int32_t part_bf16; // rows are bfloat16 (the matrix-core chain's backward), else float32
   int32_t nblocks;   // ceil(size / B)
   uint32_t seed32;
   int32_t layers;
@@ -133,9 +137,10 @@ hipError_t launch_block_grouped(const GroupTable& g, int dtype, int wdtype, int 
                                 bool fwd);
 // bfloat16 jobs of block 2^15 and one layer count on the matrix cores.
 hipError_t launch_mfma15_grouped(const GroupTable& g, int layers, hipStream_t s, bool fwd);
-// Block sums of backward jobs of one latent dtype (prefix in 256-column tiles).
+// Block sums of backward jobs of one latent dtype and one partial-row type
+// (prefix in 256-column tiles).
 constexpr int kGroupReduceCols = 256;
-hipError_t launch_reduce_grouped(const GroupTable& g, int dtype, hipStream_t s);
+hipError_t launch_reduce_grouped(const GroupTable& g, int dtype, bool part_bf16, hipStream_t s);
 
 // One generator of a grouped call (validated by the C ABI).
 struct WeightJob {

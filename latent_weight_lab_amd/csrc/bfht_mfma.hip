@@ -64,13 +64,16 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
 
 // ---------------------------------------------------------------- backward
 
-// Per-block partial latent gradient (float32, first n positions) of the
+// Per-block partial latent gradient (first n positions) of the
 // adjoint chain D_0 H D_1 ... H D_L applied to grad scattered into the block.
+// The rows are bfloat16 (the gradient's own type; each of the ~2^8 terms of a
+// position's sum carries one bf16 rounding, ~2^-9 relative, and the sum is
+// formed in float32), half the traffic of float32 rows in both kernels.
 // kWhole: every block's gradient is read whole from a 16-byte aligned place
-// and n % 4 == 0 (the launcher checks), so no partial-chunk paths are needed.
+// and n % 8 == 0 (the launcher checks), so no partial-chunk paths are needed.
 template <int L, bool kWhole>
 __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __restrict__ grad,
-                                                            float* __restrict__ partial, int n,
+                                                            __bf16* __restrict__ partial, int n,
                                                             int64_t first_block, int64_t start,
                                                             int64_t stop, uint32_t seed32) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kChainLdsBytes];
@@ -102,7 +105,7 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
   uint32_t nw[4];
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
 
-  write_partial_row<L, kWhole>(acc, nw, x, lds, partial + slot * (int64_t)n, n, 1.0f);
+  write_partial_row<L, kWhole, __bf16>(acc, nw, x, lds, partial + slot * mfma15_part_stride(n), n, 1.0f);
 }
 
 // ---------------------------------------------------------------- grouped
@@ -192,7 +195,8 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd_grouped(const GroupT
   f32x16 acc[kTiles];
   uint32_t nw[4];
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
-  write_partial_row<L, false>(acc, nw, x, lds, jb.part + slot * (int64_t)jb.stride, jb.n, 1.0f);
+  write_partial_row<L, false, __bf16>(acc, nw, x, lds, static_cast<__bf16*>(jb.part) + slot * (int64_t)jb.stride,
+                                      jb.n, 1.0f);
 }
 
 }  // namespace
@@ -223,7 +227,7 @@ hipError_t launch_mfma15_shape(const BfhtArgs& a, hipStream_t s, bool fwd) {
     }
     return hipGetLastError();
   }
-  auto* part = (float*)a.work;
+  auto* part = (__bf16*)a.work;  // bf16 partial rows (summed in float32, bfht_reduce_blocks)
   switch (a.layers) {
     case 1: hipLaunchKernelGGL((bfht_mfma15_bwd<1, kWhole>), grid, block, 0, s, src, part, n, a.first_block, a.start, a.stop, a.seed32); break;
     case 2: hipLaunchKernelGGL((bfht_mfma15_bwd<2, kWhole>), grid, block, 0, s, src, part, n, a.first_block, a.start, a.stop, a.seed32); break;

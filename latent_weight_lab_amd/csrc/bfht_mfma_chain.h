@@ -583,9 +583,9 @@ __device__ __forceinline__ void stage_output(const f32x16 (&acc)[kTiles], const 
 // spreads 8 of them over the 8 16-byte bank groups of a 128-byte row, while
 // every aligned group of 8 chunks stays in place for the consecutive reads).
 // kExact: n % 4 == 0 (whole 16-byte stores; stores past n are dropped).
-template <int L, bool kExact>
+template <int L, bool kExact, class P = float>
 __device__ __forceinline__ void write_partial_row(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4],
-                                                  const Ctx& x, unsigned char* lds, float* prow, int n,
+                                                  const Ctx& x, unsigned char* lds, P* prow, int n,
                                                   float scale) {
   auto flip = [](float v, uint32_t w, int b) {
     return __uint_as_float(__float_as_uint(v) ^ ((w << (31 - b)) & 0x80000000u));
@@ -616,18 +616,37 @@ __device__ __forceinline__ void write_partial_row(const f32x16 (&acc)[kTiles], c
     stage[c ^ ((c >> 3) & 7)] = v;
   }
   __syncthreads();
-  const auto p_r = rsrc(prow, (uint32_t)n * 4u);
+  const auto p_r = rsrc(prow, (uint32_t)n * (uint32_t)sizeof(P));
+  if constexpr (sizeof(P) == 4) {
 #pragma unroll
-  for (int i = 0; i < (kB / 4) / kThreads; ++i) {
-    const int c = i * kThreads + (int)threadIdx.x;
-    const f32x4 v = stage[c ^ ((c >> 3) & 7)];
-    const int p = c * 4;
-    if (kExact || p + 4 <= n) {
-      __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, kStreamStore);  // dropped past n
-    } else if (p < n) {
+    for (int i = 0; i < (kB / 4) / kThreads; ++i) {
+      const int c = i * kThreads + (int)threadIdx.x;
+      const f32x4 v = stage[c ^ ((c >> 3) & 7)];
+      const int p = c * 4;
+      if (kExact || p + 4 <= n) {
+        __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, kStreamStore);  // dropped past n
+      } else if (p < n) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (p + e < n) prow[p + e] = v[e];
+        for (int e = 0; e < 4; ++e)
+          if (p + e < n) prow[p + e] = v[e];
+      }
+    }
+  } else {  // bf16 row: two staged chunks (8 positions) per 16-byte store
+#pragma unroll
+    for (int i = 0; i < (kB / 8) / kThreads; ++i) {
+      const int c2 = i * kThreads + (int)threadIdx.x;
+      const f32x4 a = stage[(2 * c2) ^ (((2 * c2) >> 3) & 7)];
+      const f32x4 b = stage[(2 * c2 + 1) ^ (((2 * c2 + 1) >> 3) & 7)];
+      const u32x4 v = {pk(a[0], a[1]), pk(a[2], a[3]), pk(b[0], b[1]), pk(b[2], b[3])};
+      const int p = c2 * 8;
+      if (kExact || p + 8 <= n) {
+        __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 2, 0, kStreamStore);  // dropped past n
+      } else if (p < n) {
+        uint16_t* row16 = reinterpret_cast<uint16_t*>(prow);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (p + e < n) row16[p + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+      }
     }
   }
 }

@@ -87,8 +87,11 @@ def test_workspace_sizes():
     assert lib.lwl_bfht_forward_workspace_size(1 << 20, 1 << 26, 0, 1 << 26) == 64 * (1 << 20) * 4
     # slice [12345, 1012345) of B=2^20 touches blocks 0..0
     assert lib.lwl_bfht_forward_workspace_size(1 << 20, 1 << 26, 12345, 1_012_345) == (1 << 20) * 4
-    # backward whole-block sizes: one float32 partial row of latent_size per overlapped block
+    # backward whole-block sizes: one float32 partial row of latent_size per overlapped block,
+    # at least one 8-value bfloat16 row (16 bytes) for the matrix-core chain's padded rows
     assert lib.lwl_bfht_backward_workspace_size(1024, 108_618, 1000, 2000) == 2 * 1024 * 4
+    assert lib.lwl_bfht_backward_workspace_size(3, 4096, 0, 4096) == 1024 * 16
+    assert lib.lwl_bfht_backward_workspace_size(5, 4096, 0, 4096) == 512 * 20
     assert lib.lwl_bfht_backward_workspace_size(1024, 108_618, 0, 1024) == 1024 * 4
     assert lib.lwl_bfht_backward_workspace_size(32768, 8 << 20, 0, 8 << 20) == 256 * 32768 * 4
     assert lib.lwl_bfht_backward_workspace_size(16, 40, 3, 3) == 0
