@@ -187,6 +187,47 @@ __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_blocks(const P* __
     if (c0 + e < n) grad_latent[c0 + e] = from_f32<T>(t[e]);
 }
 
+// Few rows (nblocks <= kRedWaves): one thread per kVec columns adds the rows
+// in ascending order with all of its loads in flight.  That is the wave-split
+// kernel's sum exactly (there wave w holds row w alone, and the wave sums are
+// added in wave order onto 0), without its one load in flight per lane.
+// Rows past nblocks are loaded from row 0 and not added; with no rows at all
+// (part may then be null) nothing is loaded and the sum is 0.
+template <class T, int kVec, class P>
+__global__ __launch_bounds__(256) void bfht_reduce_few(const P* __restrict__ part, int nblocks, int64_t stride,
+                                                       int n, T* __restrict__ grad_latent) {
+  typedef typename PartVec<P, kVec>::type V;
+  const int c0 = (blockIdx.x * 256 + (int)threadIdx.x) * kVec;
+  if (c0 >= n) return;
+  float a[kVec];
+#pragma unroll
+  for (int e = 0; e < kVec; ++e) a[e] = 0.0f;
+  if (nblocks <= 0) {
+    // no partial rows: a zero gradient
+  } else if (c0 + kVec <= n) {
+    V v[kRedWaves];
+#pragma unroll
+    for (int b = 0; b < kRedWaves; ++b) v[b] = *reinterpret_cast<const V*>(part + (b < nblocks ? b : 0) * stride + c0);
+#pragma unroll
+    for (int b = 0; b < kRedWaves; ++b)
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) a[e] = b < nblocks ? a[e] + PartVec<P, kVec>::at(v[b], e) : a[e];
+  } else {
+#pragma unroll
+    for (int b = 0; b < kRedWaves; ++b) {
+      const P* r = part + (b < nblocks ? b : 0) * stride;
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        const float v = to_f32(r[c0 + e < n ? c0 + e : 0]);
+        a[e] = b < nblocks ? a[e] + v : a[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < kVec; ++e)
+    if (c0 + e < n) grad_latent[c0 + e] = from_f32<T>(a[e]);
+}
+
 // Grouped block sums with the flush epilogue: r = T(T(sum) * scale), added to
 // the destination in T when the job accumulates.  Rows are 128-byte aligned
 // (the planner rounds the stride up to 32 floats), so loads are 16 bytes wide.
@@ -215,6 +256,11 @@ __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_grouped(const Grou
 
 template <class T, int kVec, class P>
 static void launch_reduce_vec(const P* part, int64_t nblocks, int64_t stride, int64_t n, T* dst, hipStream_t s) {
+  if (nblocks <= kRedWaves) {
+    const dim3 grid((unsigned)((n + 256 * kVec - 1) / (256 * kVec))), block(256);
+    hipLaunchKernelGGL((bfht_reduce_few<T, kVec, P>), grid, block, 0, s, part, (int)nblocks, stride, (int)n, dst);
+    return;
+  }
   const dim3 grid((unsigned)((n + 64 * kVec - 1) / (64 * kVec))), block(64 * kRedWaves);
   hipLaunchKernelGGL((bfht_reduce_blocks<T, kVec, P>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
 }
@@ -223,8 +269,10 @@ template <class T, class P = float>
 static hipError_t launch_reduce(const P* part, int64_t nblocks, int64_t stride, int64_t n, T* dst,
                                 hipStream_t s) {
   // The widest row loads the stride allows (part is 256-byte aligned) that still
-  // give every CU a workgroup: 64 * kVec columns per workgroup.
-  auto fits = [&](int v) { return stride % v == 0 && (n + 64 * v - 1) / (64 * v) >= 256; };
+  // give every CU a workgroup: 64 * kVec columns per workgroup (256 * kVec with
+  // few rows, where a thread takes every row of its columns).
+  const int64_t per = nblocks <= kRedWaves ? 256 : 64;
+  auto fits = [&](int v) { return stride % v == 0 && (n + per * v - 1) / (per * v) >= 256; };
   if (fits(4))
     launch_reduce_vec<T, 4>(part, nblocks, stride, n, dst, s);
   else if (fits(2))
