@@ -14,8 +14,55 @@ namespace {
 
 // ---------------------------------------------------------------- forward
 
-// kWhole: every block is written whole to a 16-byte aligned place and n % 8
-// == 0 (the launcher checks), so no partial-chunk paths are needed.
+// The 16 bytes that start M bf16 elements before chunk b: the last M elements
+// of chunk a followed by the first 8 - M of b (bytes 16 - 2M .. 31 - 2M of a:b).
+template <int M>
+__device__ __forceinline__ u32x4 chunk_shifted(const u32x4& a, const u32x4& b) {
+  const uint32_t w[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  constexpr int o = 16 - 2 * M, q = o >> 2, r = o & 3;
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (r == 0) v[i] = w[q + i];
+    else v[i] = __builtin_amdgcn_alignbyte(w[q + i + 1], w[q + i], r);
+  }
+  return v;
+}
+
+// Stores block positions [lo, hi) of a staged block to oblk (2-byte aligned,
+// M = its element offset from a 16-byte boundary): slot j of the aligned grid
+// holds positions 8j - M .. 8j - M + 7, built from staged chunks j - 1 and j.
+// Slots inside [lo, hi) take one 16-byte store; the slots at the range's ends,
+// shared with other blocks' outputs, get element stores of their positions in
+// the range.  Slots j = 0 .. kChunks (the last one only exists for M > 0).
+template <int M>
+__device__ __forceinline__ void store_range_shifted(const u32x4* stage, __bf16* oblk, int lo, int hi) {
+  const auto a_r = rsrc(oblk - M, (uint32_t)((kChunks + 1) * 16));
+  uint16_t* o16 = reinterpret_cast<uint16_t*>(oblk);
+  constexpr int kPer = kChunks / kThreads;
+#pragma unroll
+  for (int i = 0; i <= kPer; ++i) {
+    const int j = i * kThreads + (int)threadIdx.x;
+    const int p0 = 8 * j - M;
+    if (j > kChunks || p0 + 8 <= lo || p0 >= hi) continue;
+    const u32x4 a = stage[stage_slot(j > 0 ? j - 1 : 0)];
+    const u32x4 b = stage[stage_slot(j < kChunks ? j : kChunks - 1)];
+    if (p0 >= lo && p0 + 8 <= hi) {
+      __builtin_amdgcn_raw_buffer_store_b128(chunk_shifted<M>(a, b), a_r, j * 16, 0, kStreamStore);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int p = p0 + e;  // chunk j - 1 for e < M, chunk j from e = M
+        if (p >= lo && p < hi) {
+          const u32x4& c = e < M ? a : b;
+          const int q = (e - M) & 7;
+          o16[p] = (uint16_t)(c[q >> 1] >> (16 * (q & 1)));
+        }
+      }
+    }
+  }
+}
+
 template <int L, bool kWhole>
 __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __restrict__ latent,
                                                             __bf16* __restrict__ out, int n,
@@ -40,6 +87,21 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
   const int hi = kWhole ? kB : (int)(stop - base < kB ? stop - base : kB);
   __bf16* oblk = out + (base - start);
   const bool full = kWhole || (lo == 0 && hi == kB && (((uintptr_t)oblk & 15) == 0));
+  if (!kWhole && !full && (((uintptr_t)oblk & 1) == 0)) {
+    // part of a block, or an output off the 16-byte grid: 16-byte stores on the
+    // grid, element stores at the range's ends (uniform branch)
+    switch (((uintptr_t)oblk >> 1) & 7) {
+      case 0: store_range_shifted<0>(stage, oblk, lo, hi); break;
+      case 1: store_range_shifted<1>(stage, oblk, lo, hi); break;
+      case 2: store_range_shifted<2>(stage, oblk, lo, hi); break;
+      case 3: store_range_shifted<3>(stage, oblk, lo, hi); break;
+      case 4: store_range_shifted<4>(stage, oblk, lo, hi); break;
+      case 5: store_range_shifted<5>(stage, oblk, lo, hi); break;
+      case 6: store_range_shifted<6>(stage, oblk, lo, hi); break;
+      default: store_range_shifted<7>(stage, oblk, lo, hi); break;
+    }
+    return;
+  }
   const auto out_r = rsrc(full ? (const void*)oblk : (const void*)out, full ? (uint32_t)(kB * 2) : 0u);
   uint16_t* oblk16 = reinterpret_cast<uint16_t*>(oblk);
   constexpr int kPer = kChunks / kThreads;
