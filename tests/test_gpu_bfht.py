@@ -150,6 +150,24 @@ def test_config2_full_parity(dtype):
     assert rel_l2(to_np(latent.grad), gwant) < TOL[dtype]
 
 
+def test_bf16_slices_equal_full_output_bitwise():
+    """A slice of the matrix-core forward is the same range of the full output, bit for
+    bit, whatever its offset from the 16-byte grid (start mod 8: the slice's blocks are
+    stored through shifted 16-byte slots) and wherever it starts or ends inside a block."""
+    B = 32768
+    size = 6 * B + 1000  # ragged last block
+    lat = latent_for(B, 21, torch.bfloat16).cuda()
+    full = ops.forward(lat, size, 3, 5, 0, size)
+    want = c_oracle.forward(lat.double().cpu().numpy(), size, 3, 5, 0, size)
+    assert rel_l2(to_np(full), want) < TOL[torch.bfloat16]
+    cases = [(8 * 1000 + m, 5 * B + 77 + m) for m in range(8)]  # every grid offset, interior blocks
+    cases += [(2 * B + 5, 2 * B + 100), (B - 3, B + 11), (3 * B, 4 * B), (B + 1, size), (7, 13),
+              (size - 9, size)]
+    for start, stop in cases:
+        y = ops.forward(lat, size, 3, 5, start, stop)
+        assert torch.equal(y, full[start:stop]), (start, stop)
+
+
 def test_config2_slice_and_determinism():
     torch.manual_seed(1)
     lat = torch.randn(32768, dtype=torch.float32)
