@@ -268,7 +268,11 @@ def extra_configs(abi, steps, warmup, only):
         sl = torch.empty(s1 - s0, dtype=dt, device="cuda")
         run(f"c2_slice_{tag}", lambda: abi.forward(latent, sl, C2_SIZE, 3, 7, s0, s1),
             (s1 - s0) * es + C2_N * es, s1 - s0)
-        del latent, out, grad, gl, bws, sl
+        gs = grad[s0:s1]  # the slice's gradient where it lies in the full one (2-byte offset)
+        sws = abi.bwd_ws(C2_N, C2_SIZE, s0, s1, "cuda")
+        run(f"c2_slice_bwd_{tag}", lambda: abi.backward(gs, gl, C2_SIZE, 3, 7, s0, s1, sws),
+            (s1 - s0) * es + C2_N * es, s1 - s0)
+        del latent, out, grad, gl, bws, sl, gs, sws
 
     # config 3: multi-pass blocks 2^20 and 2^23, size 2^26, fp32, layers 3, seed 99
     size = 1 << 26

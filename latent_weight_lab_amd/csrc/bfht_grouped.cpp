@@ -45,9 +45,12 @@ struct ClassKey {
 ClassKey class_of(const WeightJob& j, bool fwd) {
   const int lb = log2_ceil(j.n);
   // the per-module matrix-core predicate (mfma15_applicable): bf16, block 2^15,
-  // 16-byte aligned source (latent, or the weight gradient in the backward)
+  // a 16-byte aligned source (latent, or the weight gradient in the backward);
+  // a bf16 weight gradient at any 2-byte offset too (the kernel reads aligned
+  // 16-byte slots), as in the per-module backward
   const void* src = fwd ? j.latent : j.grad_weight;
-  const bool mfma = j.ldtype == kBF16 && lb == 15 && (uintptr_t)src % 16 == 0;
+  const bool aligned = (uintptr_t)src % 16 == 0 || (!fwd && j.wdtype == kBF16 && (uintptr_t)src % 2 == 0);
+  const bool mfma = j.ldtype == kBF16 && lb == 15 && aligned;
   return ClassKey{mfma, j.ldtype, mfma ? kBF16 : j.wdtype, lb, mfma ? j.layers : 0};
 }
 

@@ -574,7 +574,7 @@ static hipError_t run_typed(const BfhtArgs& a, hipStream_t s, bool fwd) {
                        (T*)a.dst, a.n);
     return hipGetLastError();
   }
-  if (mfma15_applicable(a)) {
+  if (mfma15_applicable(a, fwd)) {
     hipError_t e = launch_mfma15(a, s, fwd);
     if (e != hipSuccess || fwd) return e;
     return launch_reduce<T, bf16>((const bf16*)a.work, a.nblocks, mfma15_part_stride(a.n), a.n, (T*)a.dst, s);

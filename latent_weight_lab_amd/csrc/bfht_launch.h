@@ -36,7 +36,7 @@ hipError_t launch_bfht(const BfhtArgs& a, hipStream_t s, bool forward);
 
 // Matrix-core path for bfloat16 blocks of exactly 2^15 (bfht_mfma.hip).  The
 // backward writes one float32 partial row of n values per block into `work`.
-bool mfma15_applicable(const BfhtArgs& a);
+bool mfma15_applicable(const BfhtArgs& a, bool fwd);
 // The matrix-core backward's partial rows: bfloat16, rows of n padded to 8
 // elements (16-byte aligned), inside the float32-row workspace.
 __host__ __device__ inline int64_t mfma15_part_stride(int64_t n) { return (n + 7) / 8 * 8; }

@@ -126,6 +126,41 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
 
 // ---------------------------------------------------------------- backward
 
+// Loads block positions [lo, hi) of a block's gradient that starts M elements
+// past a 16-byte boundary (gblk, 2-byte aligned), zero elsewhere: the chunk at
+// positions p .. p + 7 is elements M .. 7 of aligned slot p / 8 followed by
+// elements 0 .. M - 1 of the next slot.  A slot is read only when it holds
+// positions of the range; the buffer spans the gradient's 16-byte granules
+// (from the one holding its first element to the one holding its last, gend
+// is one past it; at most the block's kChunks + 1 slots), so no read leaves
+// them, and positions outside the range read from those granules are zeroed.
+template <int M>
+__device__ __forceinline__ void load_grad_shifted(const Ctx& x, const __bf16* gblk, const __bf16* gend, int lo,
+                                                  int hi, u32x4 (&src)[kTiles][2]) {
+  const uintptr_t a0 = (uintptr_t)gblk - 2 * M;
+  const uintptr_t a1 = ((uintptr_t)gend + 15) & ~(uintptr_t)15;
+  // every slot of the block lies in the first kChunks + 1 slots from a0
+  const uintptr_t span = a1 - a0 < (uintptr_t)(kChunks + 1) * 16 ? a1 - a0 : (uintptr_t)(kChunks + 1) * 16;
+  const auto g_r = rsrc((const void*)a0, (uint32_t)span);
+  constexpr uint32_t kOff = 0x80000000u;
+  load_source(
+      x,
+      [&](int p) -> u32x4 {
+        const bool use_a = p + 7 - M >= lo && p < hi;            // slot p/8: positions p .. p + 7 - M
+        const bool use_b = M > 0 && p + 7 >= lo && p + 8 - M < hi;  // next slot: p + 8 - M .. p + 7
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(g_r, (int)(use_a ? (uint32_t)(2 * p) : kOff), 0, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(g_r, (int)(use_b ? (uint32_t)(2 * p + 16) : kOff), 0, 0);
+        u32x4 v = chunk_shifted<8 - M>(a, b);
+        if (p < lo || p + 8 > hi) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (p + e < lo || p + e >= hi) v[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+        }
+        return v;
+      },
+      src);
+}
+
 // Per-block partial latent gradient (first n positions) of the
 // adjoint chain D_0 H D_1 ... H D_L applied to grad scattered into the block.
 // The rows are bfloat16 (the gradient's own type; each of the ~2^8 terms of a
@@ -150,6 +185,20 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
   const auto g_r = rsrc(full ? (const void*)gblk : (const void*)grad, full ? (uint32_t)(kB * 2) : 0u);
   const uint16_t* gblk16 = reinterpret_cast<const uint16_t*>(gblk);
   u32x4 src[kTiles][2];
+  if (!full && (((uintptr_t)gblk & 1) == 0)) {
+    // part of a block, or a gradient off the 16-byte grid: aligned 16-byte slot loads (uniform branch)
+    const __bf16* gend = grad + (stop - start);
+    switch (((uintptr_t)gblk >> 1) & 7) {
+      case 0: load_grad_shifted<0>(x, gblk, gend, lo, hi, src); break;
+      case 1: load_grad_shifted<1>(x, gblk, gend, lo, hi, src); break;
+      case 2: load_grad_shifted<2>(x, gblk, gend, lo, hi, src); break;
+      case 3: load_grad_shifted<3>(x, gblk, gend, lo, hi, src); break;
+      case 4: load_grad_shifted<4>(x, gblk, gend, lo, hi, src); break;
+      case 5: load_grad_shifted<5>(x, gblk, gend, lo, hi, src); break;
+      case 6: load_grad_shifted<6>(x, gblk, gend, lo, hi, src); break;
+      default: load_grad_shifted<7>(x, gblk, gend, lo, hi, src); break;
+    }
+  } else
   load_source(
       x,
       [&](int p) -> u32x4 {
@@ -241,6 +290,20 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd_grouped(const GroupT
   const auto g_r = rsrc(full ? (const void*)gblk : jb.src, full ? (uint32_t)(kB * 2) : 0u);
   const uint16_t* gblk16 = reinterpret_cast<const uint16_t*>(gblk);
   u32x4 src[kTiles][2];
+  if (!full && (((uintptr_t)gblk & 1) == 0)) {
+    // the last, partial block, or a weight gradient off the 16-byte grid (uniform branch)
+    const __bf16* gend = static_cast<const __bf16*>(jb.src) + jb.size;
+    switch (((uintptr_t)gblk >> 1) & 7) {
+      case 0: load_grad_shifted<0>(x, gblk, gend, 0, hi, src); break;
+      case 1: load_grad_shifted<1>(x, gblk, gend, 0, hi, src); break;
+      case 2: load_grad_shifted<2>(x, gblk, gend, 0, hi, src); break;
+      case 3: load_grad_shifted<3>(x, gblk, gend, 0, hi, src); break;
+      case 4: load_grad_shifted<4>(x, gblk, gend, 0, hi, src); break;
+      case 5: load_grad_shifted<5>(x, gblk, gend, 0, hi, src); break;
+      case 6: load_grad_shifted<6>(x, gblk, gend, 0, hi, src); break;
+      default: load_grad_shifted<7>(x, gblk, gend, 0, hi, src); break;
+    }
+  } else
   load_source(
       x,
       [&](int p) -> u32x4 {
@@ -264,10 +327,12 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd_grouped(const GroupT
 }  // namespace
 }  // namespace mfma15
 
-bool mfma15_applicable(const BfhtArgs& a) {
+bool mfma15_applicable(const BfhtArgs& a, bool fwd) {
   // 16-byte vector loads of the latent and stores of the partial rows need
-  // aligned bases; output and grad alignment is checked per block in the kernels.
-  const bool aligned = ((uintptr_t)a.src % 16 == 0) && (a.work == nullptr || (uintptr_t)a.work % 16 == 0);
+  // aligned bases; the backward reads the gradient in aligned 16-byte slots
+  // whatever its offset, and output alignment is handled per block.
+  const bool aligned = ((uintptr_t)a.src % (fwd ? 16 : 2) == 0) &&
+                       (a.work == nullptr || (uintptr_t)a.work % 16 == 0);
   return a.dtype == kBF16 && a.log_block == mfma15::kLog && a.nblocks > 0 && a.n <= mfma15::kB && aligned;
 }
 

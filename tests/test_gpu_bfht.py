@@ -168,6 +168,29 @@ def test_bf16_slices_equal_full_output_bitwise():
         assert torch.equal(y, full[start:stop]), (start, stop)
 
 
+def test_bf16_slice_backward_equals_masked_full_backward_bitwise():
+    """The backward of a slice equals, bit for bit, the full backward of a gradient that is
+    zero outside the slice (the same chain inputs; blocks outside add zero rows), at every
+    offset of the slice's gradient from the 16-byte grid, for a fresh gradient tensor and for
+    a view into a larger one."""
+    B = 32768
+    size = 6 * B + 1000
+    n = B
+    gfull = torch.randn(size, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).cuda()
+    cases = [(8 * 1000 + m, 5 * B + 77 + m) for m in range(8)]
+    cases += [(2 * B + 5, 2 * B + 100), (B - 3, B + 11), (B + 1, size), (size - 9, size)]
+    for start, stop in cases:
+        masked = torch.zeros_like(gfull)
+        masked[start:stop] = gfull[start:stop]
+        want = ops.backward(masked, n, torch.bfloat16, size, 3, 5, 0, size)
+        for g in (gfull[start:stop].clone(), gfull[start:stop]):
+            got = ops.backward(g, n, torch.bfloat16, size, 3, 5, start, stop)
+            assert torch.equal(got, want), (start, stop, g.data_ptr() % 16)
+    gwant = c_oracle.backward(to_np(gfull[8000:5 * B + 77]), n, size, 3, 5, 8000, 5 * B + 77)
+    got = ops.backward(gfull[8000:5 * B + 77], n, torch.bfloat16, size, 3, 5, 8000, 5 * B + 77)
+    assert rel_l2(to_np(got), gwant) < TOL[torch.bfloat16]
+
+
 def test_config2_slice_and_determinism():
     torch.manual_seed(1)
     lat = torch.randn(32768, dtype=torch.float32)
