@@ -313,31 +313,64 @@ constexpr int kTileThreads = 1024;
 constexpr int kTileElems = 1 << kTileLog;
 constexpr int kTilePadded = kTileElems + (kTileElems >> 5);
 
-// In-place unnormalized butterflies over tile-index bits [LO_BIT, 15) of an
-// LDS-resident 2^15 tile, in groups of up to 5 bits.  The element thread t
-// holds in register r of a group is a bit field of t OR-ed with a bit field of
-// r; their low 5 bits never overlap, so its padded LDS index is
-// lds_index(field of t) + lds_index(field of r): a per-thread base plus a
-// compile-time offset per register.
+// Bit groups of a tile pass that transforms tile-index bits [LO_BIT, 15): the
+// register bits of the load layout (element r * 1024 + tid holds bits 10-14
+// in r; those at or above LO_BIT, from register bit kRegLo), then [LO_BIT, 10)
+// in at most two groups of up to 5 bits from the top.
 template <int LO_BIT>
-__device__ __forceinline__ void tile_fht_bits(float* lds, int tid) {
+struct TileGroups {
+  static constexpr int kRegLo = LO_BIT > 10 ? LO_BIT - 10 : 0;
+  static constexpr int kExtra = LO_BIT >= 10 ? 0 : (10 - LO_BIT + 4) / 5;
+  static constexpr int lo(int k) { return 10 - 5 * k - 5 > LO_BIT ? 10 - 5 * k - 5 : LO_BIT; }
+  static constexpr int nb(int k) { return 10 - 5 * k - lo(k); }
+  // the layout after the groups: the last extra group, or the load layout (10, 5)
+  static constexpr int kLastLo = kExtra == 0 ? 10 : lo(kExtra - 1);
+  static constexpr int kLastNb = kExtra == 0 ? 5 : nb(kExtra - 1);
+};
+static_assert(TileGroups<0>::kExtra == 2 && TileGroups<0>::lo(0) == 5 && TileGroups<0>::lo(1) == 0 &&
+                  TileGroups<0>::nb(1) == 5,
+              "low tile: bits 10-14 in registers, then 5-9 and 0-4");
+static_assert(TileGroups<7>::kExtra == 1 && TileGroups<7>::lo(0) == 7 && TileGroups<7>::nb(0) == 3,
+              "2^23 high tile: bits 10-14 in registers, then 7-9");
+static_assert(TileGroups<10>::kExtra == 0 && TileGroups<12>::kRegLo == 2, "small high tiles stay in registers");
+
+
+// Sign layer in bit-group layout (L, NB): element e = group_pos(tid, r, L, NB)
+// takes bit e & 31 of table word e >> 5.
+// In chunks of 8 registers, each chunk's table reads kept behind the previous
+// chunk's flips (at most 8 words in registers beside the tile and the loads
+// in flight for the next one).
+template <int L, int NB>
+__device__ __forceinline__ void tile_signs(const uint32_t* words, float (&v)[32], int tid) {
 #pragma unroll
-  for (int lo = LO_BIT; lo < kTileLog; lo += 5) {
-    const int nb = kTileLog - lo < 5 ? kTileLog - lo : 5;
-    const int base = lds_index(group_pos<kTileLog, 5>(tid, 0, lo, nb));
-    float v[32];
-    __syncthreads();
+  for (int r0 = 0; r0 < 32; r0 += 8) {
 #pragma unroll
-    for (int r = 0; r < 32; ++r) v[r] = lds[base + lds_index(group_pos<kTileLog, 5>(0, r, lo, nb))];
-    butterflies<32>(v, nb);
-#pragma unroll
-    for (int r = 0; r < 32; ++r) lds[base + lds_index(group_pos<kTileLog, 5>(0, r, lo, nb))] = v[r];
+    for (int r = r0; r < r0 + 8; ++r) {
+      const int e = group_pos<kTileLog, 5>(tid, r, L, NB);
+      v[r] = signed_by(v[r], words[e >> 5], e & 31);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __syncthreads();
 }
 
+// Butterflies over register bits [LO, 5).
+template <int LO>
+__device__ __forceinline__ void reg_butterflies(float (&v)[32]) {
+#pragma unroll
+  for (int j = LO; j < 5; ++j)
+#pragma unroll
+    for (int r = 0; r < 32; ++r)
+      if (!(r & (1 << j))) {
+        const float a = v[r], b = v[r | (1 << j)];
+        v[r] = a + b;
+        v[r | (1 << j)] = a - b;
+      }
+}
+
+
 // One pass of the tiled schedule (run_tiles).  A tile is 2^15 positions of one
-// block held in LDS: a low tile is contiguous (block bits 0-14 vary), a high
+// block (in registers, through LDS between bit groups): a low tile is
+// contiguous (block bits 0-14 vary), a high
 // tile is 2^(LB-15) rows of 2^(30-LB) contiguous columns, the rows walking
 // block bits 15..LB-1.  The pass loads the tile (latent, grad or the work
 // buffer), transforms its bit group (`pre`), applies the sign layer
@@ -410,43 +443,96 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
     }
   };
 
-  // padded LDS index of element r * 1024 + tid: lt + r * (1024 + 32)
-  const int lt = tid + (tid >> 5);
-  constexpr int kRowStride = kTileThreads + kTileThreads / 32;
+  // Bit groups (TileGroups): the load layout's register bits (element
+  // r * 1024 + tid), then the groups below bit 10 through LDS.  A tile with no
+  // group below bit 10 stays in registers from load to store.  Otherwise the
+  // first transform starts on the loaded registers, the tile goes to LDS once
+  // (freeing the registers for the next tile's loads) and visits the groups
+  // downwards; the sign layer is applied in the last group's layout — for a low
+  // tile 32 consecutive positions, one sign word, the thread's own — and the
+  // second transform visits the groups upwards and ends in the load layout,
+  // stored from registers.  Per group: a barrier, a read, the butterflies, a
+  // write back of the same elements.
+  using G = TileGroups<lo_bit>;
+  constexpr bool kOwnWord = G::kLastLo == 0 && G::kLastNb == 5;  // 32 consecutive positions per thread
+  auto group_rw = [&](float (&v)[32], int lo, int nb, bool rd) {
+    const int b = group_base<kTileLog, 5>(tid, lo, nb);
+    if (rd) {
+#pragma unroll
+      for (int r = 0; r < 32; ++r) v[r] = lds[group_lds<kTileLog, 5>(b, r, lo, nb)];
+    } else {
+#pragma unroll
+      for (int r = 0; r < 32; ++r) lds[group_lds<kTileLog, 5>(b, r, lo, nb)] = v[r];
+    }
+  };
   float x[32];
   int64_t t = blockIdx.x;
   if (t < ntiles_total) load_tile(geo(t), x);
   for (; t < ntiles_total; t += gridDim.x) {
     const Geo g = geo(t);
-    __syncthreads();  // the previous tile's LDS reads (sign table, stores) are done
+    float v[32];
+    __syncthreads();  // the previous tile's reads of lds and of the sign table are done
+    const uint32_t my_word = sign_word(block_key(seed32, g.block), layer_key(sign_layer), pos(32u * tid, g.tile) >> 5);
+    words[tid] = my_word;
+    if constexpr (G::kExtra == 0) {
 #pragma unroll
-    for (int r = 0; r < 32; ++r) lds[lt + r * kRowStride] = x[r];
-    words[tid] = sign_word(block_key(seed32, g.block), layer_key(sign_layer), pos(32u * tid, g.tile) >> 5);
-    if (t + gridDim.x < ntiles_total) load_tile(geo(t + gridDim.x), x);  // in flight during the transforms
-    if (pre)
-      tile_fht_bits<lo_bit>(lds, tid);
-    else
-      __syncthreads();
-    // each thread flips only the elements it stored, after the barrier that
-    // published the sign table
+      for (int r = 0; r < 32; ++r) v[r] = x[r];
+      if (t + gridDim.x < ntiles_total) load_tile(geo(t + gridDim.x), x);  // in flight during the transforms
+      if (pre) reg_butterflies<G::kRegLo>(v);
+      __syncthreads();  // the sign table is complete
+      tile_signs<10, 5>(words, v, tid);
+      if (post) reg_butterflies<G::kRegLo>(v);
+    } else {
+      if (pre) reg_butterflies<G::kRegLo>(x);
+      group_rw(x, 10, 5, false);
+      if (t + gridDim.x < ntiles_total) load_tile(geo(t + gridDim.x), x);  // in flight during the transforms
+      // downwards: the groups of the first transform, then the sign layer
 #pragma unroll
-    for (int r = 0; r < 32; ++r)  // element r * 1024 + tid: word r * 32 + tid / 32, bit tid % 32
-      lds[lt + r * kRowStride] = signed_by(lds[lt + r * kRowStride], words[r * 32 + (tid >> 5)], tid & 31);
-    if (post)
-      tile_fht_bits<lo_bit>(lds, tid);
-    else
+      for (int k = 0; k < G::kExtra; ++k) {
+        __syncthreads();
+        group_rw(v, G::lo(k), G::nb(k), true);
+        if (pre) butterflies<32>(v, G::nb(k));
+        if (k + 1 < G::kExtra) group_rw(v, G::lo(k), G::nb(k), false);
+      }
+      if constexpr (kOwnWord) {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) v[r] = signed_by(v[r], my_word, r);
+      } else {
+        // a high tile's small group below bit 10: the signs go on in the load
+        // layout (as in a register-only tile), then back to the group
+        group_rw(v, G::kLastLo, G::kLastNb, false);
+        __syncthreads();
+        group_rw(v, 10, 5, true);
+        tile_signs<10, 5>(words, v, tid);  // the table is complete: barriers since its writes
+        group_rw(v, 10, 5, false);
+        __syncthreads();
+        group_rw(v, G::kLastLo, G::kLastNb, true);
+      }
+      // upwards: the groups of the second transform (or only the way back)
+#pragma unroll
+      for (int k = G::kExtra - 1; k >= 0; --k) {
+        if (k + 1 < G::kExtra) {
+          __syncthreads();
+          group_rw(v, G::lo(k), G::nb(k), true);
+        }
+        if (post) butterflies<32>(v, G::nb(k));
+        group_rw(v, G::lo(k), G::nb(k), false);
+      }
       __syncthreads();
+      group_rw(v, 10, 5, true);
+      if (post) reg_butterflies<G::kRegLo>(v);
+    }
 
 #pragma unroll
     for (int r = 0; r < 32; ++r) {
-      const float v = lds[lt + r * kRowStride] * scale;
+      const float vs = v[r] * scale;
       if constexpr (DST == kDstWork) {
-        buf_store<float>(v, tile_rsrc(work + g.slot * B, (uint64_t)B * 4), g.pt + pr(r));
+        buf_store<float>(vs, tile_rsrc(work + g.slot * B, (uint64_t)B * 4), g.pt + pr(r));
       } else if constexpr (DST == kDstOut) {
         T* o0 = dst_io + (g.base + g.lo - start);
-        buf_store<T>(v, tile_rsrc(o0, (uint64_t)(g.hi - g.lo) * sizeof(T)), g.pt + pr(r) - (int)g.lo);
+        buf_store<T>(vs, tile_rsrc(o0, (uint64_t)(g.hi - g.lo) * sizeof(T)), g.pt + pr(r) - (int)g.lo);
       } else {  // kDstPartial: the first n positions, left in the work buffer
-        buf_store<float>(v, tile_rsrc(work + g.slot * B, (uint64_t)n * 4), g.pt + pr(r));
+        buf_store<float>(vs, tile_rsrc(work + g.slot * B, (uint64_t)n * 4), g.pt + pr(r));
       }
     }
   }
