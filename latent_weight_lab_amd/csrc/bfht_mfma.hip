@@ -198,20 +198,21 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
       case 6: load_grad_shifted<6>(x, gblk, gend, lo, hi, src); break;
       default: load_grad_shifted<7>(x, gblk, gend, lo, hi, src); break;
     }
-  } else
-  load_source(
-      x,
-      [&](int p) -> u32x4 {
-        if (full) return __builtin_amdgcn_raw_buffer_load_b128(g_r, p * 2, 0, 0);
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (p + 8 > lo && p < hi) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (p + e >= lo && p + e < hi) v[e >> 1] |= (uint32_t)gblk16[p + e] << (16 * (e & 1));
-        }
-        return v;
-      },
-      src);
+  } else {
+    load_source(
+        x,
+        [&](int p) -> u32x4 {
+          if (full) return __builtin_amdgcn_raw_buffer_load_b128(g_r, p * 2, 0, 0);
+          u32x4 v = {0u, 0u, 0u, 0u};
+          if (p + 8 > lo && p < hi) {
+  #pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (p + e >= lo && p + e < hi) v[e >> 1] |= (uint32_t)gblk16[p + e] << (16 * (e & 1));
+          }
+          return v;
+        },
+        src);
+  }
   f32x16 acc[kTiles];
   uint32_t nw[4];
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
@@ -303,20 +304,21 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd_grouped(const GroupT
       case 6: load_grad_shifted<6>(x, gblk, gend, 0, hi, src); break;
       default: load_grad_shifted<7>(x, gblk, gend, 0, hi, src); break;
     }
-  } else
-  load_source(
-      x,
-      [&](int p) -> u32x4 {
-        if (full) return __builtin_amdgcn_raw_buffer_load_b128(g_r, p * 2, 0, 0);
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (p < hi) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (p + e < hi) v[e >> 1] |= (uint32_t)gblk16[p + e] << (16 * (e & 1));
-        }
-        return v;
-      },
-      src);
+  } else {
+    load_source(
+        x,
+        [&](int p) -> u32x4 {
+          if (full) return __builtin_amdgcn_raw_buffer_load_b128(g_r, p * 2, 0, 0);
+          u32x4 v = {0u, 0u, 0u, 0u};
+          if (p < hi) {
+  #pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (p + e < hi) v[e >> 1] |= (uint32_t)gblk16[p + e] << (16 * (e & 1));
+          }
+          return v;
+        },
+        src);
+  }
   f32x16 acc[kTiles];
   uint32_t nw[4];
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
