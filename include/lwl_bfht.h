@@ -171,7 +171,8 @@ int lwl_bfht_check_linear_backward_latent(int dtype, int64_t tokens, int64_t in_
  * bit-identical to it.  Jobs take latents of length <= 32768 (blocks up to
  * 2^15); bfloat16 latents of block 2^15 need W = bfloat16.  Destinations must
  * not overlap.  Gains, modulation and residual weights stay with the caller.
- * The flush workspace holds every job's per-block float32 partial rows.
+ * The flush workspace holds every job's per-block partial rows (float32, or
+ * bfloat16 for bfloat16 latents of block 2^15, as in the per-module call).
  */
 typedef struct lwl_bfht_weight_job {
   const void* latent;      /* [latent_size], latent_dtype (materialize) */
