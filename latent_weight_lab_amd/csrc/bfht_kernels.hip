@@ -504,23 +504,28 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
         __syncthreads();
         group_rw(v, 10, 5, true);
         tile_signs<10, 5>(words, v, tid);  // the table is complete: barriers since its writes
-        group_rw(v, 10, 5, false);
-        __syncthreads();
-        group_rw(v, G::kLastLo, G::kLastNb, true);
-      }
-      // upwards: the groups of the second transform (or only the way back)
-#pragma unroll
-      for (int k = G::kExtra - 1; k >= 0; --k) {
-        if (k + 1 < G::kExtra) {
+        if (post) {
+          group_rw(v, 10, 5, false);
           __syncthreads();
-          group_rw(v, G::lo(k), G::nb(k), true);
+          group_rw(v, G::kLastLo, G::kLastNb, true);
         }
-        if (post) butterflies<32>(v, G::nb(k));
-        group_rw(v, G::lo(k), G::nb(k), false);
       }
-      __syncthreads();
-      group_rw(v, 10, 5, true);
-      if (post) reg_butterflies<G::kRegLo>(v);
+      // upwards: the groups of the second transform (or only the way back); a
+      // small high group without a second transform is in the load layout already
+      if (kOwnWord || post) {
+#pragma unroll
+        for (int k = G::kExtra - 1; k >= 0; --k) {
+          if (k + 1 < G::kExtra) {
+            __syncthreads();
+            group_rw(v, G::lo(k), G::nb(k), true);
+          }
+          if (post) butterflies<32>(v, G::nb(k));
+          group_rw(v, G::lo(k), G::nb(k), false);
+        }
+        __syncthreads();
+        group_rw(v, 10, 5, true);
+        if (post) reg_butterflies<G::kRegLo>(v);
+      }
     }
 
 #pragma unroll
