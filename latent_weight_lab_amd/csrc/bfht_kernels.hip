@@ -486,13 +486,19 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
       if (pre) reg_butterflies<G::kRegLo>(x);
       group_rw(x, 10, 5, false);
       if (t + gridDim.x < ntiles_total) load_tile(geo(t + gridDim.x), x);  // in flight during the transforms
-      // downwards: the groups of the first transform, then the sign layer
+      // downwards: the groups of the first transform (without one, straight to
+      // the last group's layout), then the sign layer
+      if (pre) {
 #pragma unroll
-      for (int k = 0; k < G::kExtra; ++k) {
+        for (int k = 0; k < G::kExtra; ++k) {
+          __syncthreads();
+          group_rw(v, G::lo(k), G::nb(k), true);
+          butterflies<32>(v, G::nb(k));
+          if (k + 1 < G::kExtra) group_rw(v, G::lo(k), G::nb(k), false);
+        }
+      } else {
         __syncthreads();
-        group_rw(v, G::lo(k), G::nb(k), true);
-        if (pre) butterflies<32>(v, G::nb(k));
-        if (k + 1 < G::kExtra) group_rw(v, G::lo(k), G::nb(k), false);
+        group_rw(v, G::kLastLo, G::kLastNb, true);
       }
       if constexpr (kOwnWord) {
 #pragma unroll
