@@ -239,6 +239,28 @@ def test_config3_multipass(log_block):
     assert rel_l2(to_np(gb), gwant) < 1e-5
 
 
+@pytest.mark.parametrize("layers", [1, 2, 3])
+@pytest.mark.parametrize("log_block", [16, 17, 18, 19, 20, 21, 22, 23])
+def test_tile_pass_block_sizes(log_block, layers):
+    """Every multi-pass block size: the tile passes' bit groups depend on it (tiles of up
+    to 2^20 blocks stay in registers, larger ones send a 1-3 bit group through LDS), and
+    the layer count decides which passes transform before or after their sign layer.
+    Forward and backward on a ragged size and a slice across two block boundaries."""
+    B = 1 << log_block
+    n = B - 3
+    size = 2 * B + B // 2 + 7
+    lat = latent_for(n, log_block + layers, torch.float32)
+    latent = lat.cuda()
+    s0, s1 = B - 1000, 2 * B + 1234
+    y = ops.forward(latent, size, layers, 17, s0, s1)
+    want = c_oracle.forward(lat.double().numpy(), size, layers, 17, s0, s1)
+    assert rel_l2(to_np(y), want) < 1e-5
+    g = torch.randn(s1 - s0, generator=torch.Generator().manual_seed(log_block)).cuda()
+    gl = ops.backward(g, n, torch.float32, size, layers, 17, s0, s1)
+    gwant = c_oracle.backward(g.double().cpu().numpy(), n, size, layers, 17, s0, s1)
+    assert rel_l2(to_np(gl), gwant) < 1e-5
+
+
 def test_reference_2_23_smoke():
     # reference tests/test_block_fht_cuda.py:34-40
     bfht = BlockFHT((1 << 23) - 17, size=1 << 23, layers=1, seed=9).cuda()
