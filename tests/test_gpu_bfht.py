@@ -239,9 +239,10 @@ def test_config3_multipass(log_block):
     assert rel_l2(to_np(gb), gwant) < 1e-5
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("layers", [1, 2, 3])
 @pytest.mark.parametrize("log_block", [16, 17, 18, 19, 20, 21, 22, 23])
-def test_tile_pass_block_sizes(log_block, layers):
+def test_tile_pass_block_sizes(log_block, layers, dtype):
     """Every multi-pass block size: the tile passes' bit groups depend on it (tiles of up
     to 2^20 blocks stay in registers, larger ones send a 1-3 bit group through LDS), and
     the layer count decides which passes transform before or after their sign layer.
@@ -249,16 +250,17 @@ def test_tile_pass_block_sizes(log_block, layers):
     B = 1 << log_block
     n = B - 3
     size = 2 * B + B // 2 + 7
-    lat = latent_for(n, log_block + layers, torch.float32)
+    lat = latent_for(n, log_block + layers, dtype)
     latent = lat.cuda()
     s0, s1 = B - 1000, 2 * B + 1234
     y = ops.forward(latent, size, layers, 17, s0, s1)
+    assert y.dtype == dtype
     want = c_oracle.forward(lat.double().numpy(), size, layers, 17, s0, s1)
-    assert rel_l2(to_np(y), want) < 1e-5
-    g = torch.randn(s1 - s0, generator=torch.Generator().manual_seed(log_block)).cuda()
-    gl = ops.backward(g, n, torch.float32, size, layers, 17, s0, s1)
+    assert rel_l2(to_np(y), want) < TOL[dtype]
+    g = torch.randn(s1 - s0, generator=torch.Generator().manual_seed(log_block)).to(dtype).cuda()
+    gl = ops.backward(g, n, dtype, size, layers, 17, s0, s1)
     gwant = c_oracle.backward(g.double().cpu().numpy(), n, size, layers, 17, s0, s1)
-    assert rel_l2(to_np(gl), gwant) < 1e-5
+    assert rel_l2(to_np(gl), gwant) < TOL[dtype]
 
 
 def test_reference_2_23_smoke():
