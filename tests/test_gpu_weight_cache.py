@@ -190,3 +190,24 @@ def test_model_prepare_flush_matches_per_module(cache_dtype):
     for m in a.modules():
         if isinstance(m, BlockFHTLinear):
             assert m._cached_weight is None
+
+
+def test_flush_weight_gradients_off_the_16_byte_grid_bitwise():
+    """bf16 weight gradients of block-2^15 jobs that are views at 2- and 6-byte offsets
+    (and one aligned) run on the matrix cores in both paths, which read them as aligned
+    16-byte slots: the grouped flush stays bit-identical to the per-module backward."""
+    sizes = [1024 * 1024, 300 * 1000 + 13, 768 * 3072]
+    offsets = [1, 3, 0]
+    base = torch.randn(sum(sizes) + 256, generator=torch.Generator().manual_seed(41)).to(BF16).cuda()
+    specs, at = [], 0  # `at` stays a multiple of 8 elements (16 bytes) from the 256-byte aligned base
+    for i, (size, off) in enumerate(zip(sizes, offsets)):
+        gw = base[at + off: at + off + size]
+        assert gw.data_ptr() % 16 == 2 * off
+        at = (at + off + size + 15) // 8 * 8
+        lat = make_latent(32768 if i != 1 else 20000, BF16, 60 + i)
+        specs.append((lat, gw, size, 3, 70 + i, 0.5 if i else 1.0, None))
+    got = ops.flush_weight_grads(specs)
+    torch.cuda.synchronize()
+    for (lat, gw, size, layers, seed, ws, _), r in zip(specs, got):
+        want = ws * block_fht_grad_latent(lat, gw, size, layers, seed)
+        assert torch.equal(r, want), (size, gw.data_ptr() % 16)
