@@ -21,8 +21,12 @@
  * returns the message of the calling thread's last failure.
  *
  * Element types: the latent, the generated output and their gradients share
- * one dtype (LWL_DTYPE_*).  All arithmetic is float32 except in the explicitly
- * fast-math paths documented per entry point.
+ * one dtype (LWL_DTYPE_*).  Arithmetic is float32 (loads and stores in the I/O
+ * dtype), with one exception: bfloat16 latents whose block is exactly 2^15 run
+ * on the matrix cores, with bfloat16 operands at every radix-32 Walsh stage
+ * (three stages per layer, so 9 roundings at 3 layers, ~5e-3 relative L2
+ * against a float64 chain) and float32 accumulation.  Each entry point names
+ * which of the two it uses.
  */
 #ifndef LWL_BFHT_H
 #define LWL_BFHT_H
@@ -65,8 +69,10 @@ int lwl_abi_version(void);
  * output_size ("invalid slice", .cu:524), layers in {1,2,3} (.cu:525),
  * 1 <= latent_size and B <= 2^23 (.cu:528).
  *
- * dtype F32: float32 arithmetic.  dtype BF16/F16: loads/stores in the 16-bit
- * type, float32 arithmetic.
+ * dtype F32 and F16, and BF16 at blocks other than 2^15: float32 arithmetic,
+ * loads/stores in the I/O type.  dtype BF16 at block 2^15 (16385 <= latent_size
+ * <= 32768) with a 16-byte aligned latent: matrix cores, bfloat16 operands at
+ * each radix-32 stage, float32 accumulation.
  */
 size_t lwl_bfht_forward_workspace_size(int64_t latent_size, int64_t output_size, int64_t start,
                                        int64_t stop);
@@ -87,6 +93,9 @@ int lwl_bfht_check_forward(int dtype, int64_t latent_size, int64_t output_size, 
  *     grad_latent[p] = sum_b [D_{b,0} H D_{b,1} ... H D_{b,L} scatter_b(grad_out)][p].
  * The sum over blocks runs in a fixed order (deterministic, unlike the
  * reference's atomicAdd at .cu:221,493).  grad_out and grad_latent have `dtype`.
+ * Arithmetic as lwl_bfht_forward (BF16 at block 2^15: matrix cores, bfloat16
+ * operands, float32 accumulation, bfloat16 per-block partial rows summed in
+ * float32).
  */
 size_t lwl_bfht_backward_workspace_size(int64_t latent_size, int64_t output_size, int64_t start,
                                         int64_t stop);

@@ -6,7 +6,9 @@ gradient comes from the HIP library (``ops``).  Differences from the
 reference, all widenings:
 
 * float16 and bfloat16 latents run on the GPU (reference: float32 only,
-  ``block_fht.py:161``); arithmetic is float32 inside the kernels;
+  ``block_fht.py:161``).  Arithmetic is float32, except for bfloat16 latents of
+  block 2^15, which run on the matrix cores: bf16 operands at every radix-32
+  stage (9 roundings at 3 layers), float32 accumulation;
 * blocks of any size 2^0 .. 2^23 (reference CUDA: 2^5 .. 2^23);
 * the fused linear accepts any ``in_features <= block_size``
   (reference: ``block_size % in_features == 0`` and block_size <= 2^14,
@@ -102,9 +104,9 @@ def block_fht_linear_forward(input: torch.Tensor, latent: torch.Tensor, out_feat
     ``weight_scale`` folded in) and call ``F.linear`` — the reference's fallback
     (``:282-288``).  On MI355X that second route is the faster one at every batch size
     measured (it costs the transient W, ~1 µs of HBM traffic per GPT-2 matrix), so callers
-    that can hold W pass ``fused=False``.  With autograd recording and a latent that
-    requires grad, W comes from the differentiable ``block_fht_slice``, as in the
-    reference's fallback.
+    that can hold W pass ``fused=False``.  Both routes are differentiable in the input and
+    the latent, as the reference's fallback is: the fused one through ``_FusedLinearFn``
+    (W regenerated in the backward), the other through ``block_fht_slice``.
     """
     return _generated_linear(input, latent, out_features, layers, seed, weight_scale, None, fused)
 
@@ -119,7 +121,10 @@ def _generated_linear(input, latent, out_features, layers, seed, weight_scale, b
     _native.require_cuda(flat, latent)
     size = in_features * out_features
     if fused and ops.linear_supported(in_features, out_features, latent, flat):
-        out = ops.linear_forward(flat, latent, out_features, int(layers), int(seed), float(weight_scale))
+        if torch.is_grad_enabled() and (latent.requires_grad or flat.requires_grad):
+            out = _FusedLinearFn.apply(flat, latent, out_features, int(layers), int(seed), float(weight_scale))
+        else:
+            out = ops.linear_forward(flat, latent, out_features, int(layers), int(seed), float(weight_scale))
         if bias is not None:
             out = out + bias
     elif torch.is_grad_enabled() and latent.requires_grad:
@@ -134,6 +139,43 @@ def _generated_linear(input, latent, out_features, layers, seed, weight_scale, b
                 weight = block_fht_slice(latent, size, int(layers), int(seed), 0, size) * float(weight_scale)
         out = F.linear(flat.contiguous(), weight.view(out_features, in_features), bias)
     return out.reshape(*input.shape[:-1], out_features)
+
+
+class _FusedLinearFn(torch.autograd.Function):
+    """The fused route of ``block_fht_linear_forward`` with the gradients of the
+    reference's differentiable fallback (``block_fht.py:282-288``: W from
+    ``block_fht_slice``, ``* weight_scale``, ``F.linear``).  The forward keeps W on
+    chip; the backward regenerates ``weight_scale * W`` once (one grouped launch)
+    for ``grad_input = g W`` and projects ``grad_weight = g^T x`` onto the latent
+    through the generator's backward, as ``_BlockFHTLinearFn.backward`` does
+    (reference ``:330-350``)."""
+
+    @staticmethod
+    def forward(ctx, x2d, latent, out_features, layers, seed, weight_scale):
+        ctx.save_for_backward(x2d, latent)
+        ctx.meta = (int(out_features), int(layers), int(seed), float(weight_scale))
+        return ops.linear_forward(x2d, latent, out_features, layers, seed, weight_scale)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x2d, latent = ctx.saved_tensors
+        out_f, layers, seed, scale = ctx.meta
+        in_f = int(x2d.shape[1])
+        size = in_f * out_f
+        g = grad_out.reshape(-1, out_f)
+        grad_x = grad_latent = None
+        if ctx.needs_input_grad[0]:
+            with torch.no_grad():
+                lat = latent.detach()
+                if ops.weight_job_supported(lat, size, layers, lat.dtype):
+                    (w,) = ops.materialize_weights([(lat, size, layers, seed, scale, lat.dtype)])
+                else:
+                    w = block_fht_slice(lat, size, layers, seed, 0, size) * scale
+            grad_x = g.to(dtype=w.dtype).matmul(w.view(out_f, in_f)).to(dtype=x2d.dtype)
+        if ctx.needs_input_grad[1]:
+            grad_weight = g.t().to(dtype=latent.dtype).matmul(x2d.to(dtype=latent.dtype))
+            grad_latent = scale * block_fht_grad_latent(latent.detach(), grad_weight.reshape(-1), size, layers, seed)
+        return grad_x, grad_latent, None, None, None, None
 
 
 class _BlockFHTLinearFn(torch.autograd.Function):

@@ -109,7 +109,12 @@ size_t backward_ws(const lwl::BfhtArgs& a) {
 }
 
 // Fused linear checks; messages follow block_fht_ext_cuda.cu:631-644 and
-// block_fht.py:259-260.
+// block_fht.py:259-260.  Two kernels share the entry point: the matrix-core one
+// (bf16, block 2^15; any in_features in its range, rows may straddle blocks)
+// and the reference extension's own domain (float32 / float16 / bfloat16,
+// block <= 2^14, block % in_features == 0).  Sizes that would overflow their
+// 32-bit buffer offsets or grid dimensions are rejected as unsupported (the
+// caller then generates W and calls a GEMM).
 int check_linear(int dtype, int64_t tokens, int64_t in_features, int64_t latent_size,
                  int64_t out_features, int64_t layers) {
   if (!valid_dtype(dtype))
@@ -127,19 +132,36 @@ int check_linear(int dtype, int64_t tokens, int64_t in_features, int64_t latent_
                 (long long)latent_size);
   if (in_features > ((int64_t)1 << lb))
     return fail(LWL_ERR_UNSUPPORTED, "fused linear forward requires in_features <= block_size");
-  if (in_features > lwl::kLinearMaxInFeatures)
-    return fail(LWL_ERR_UNSUPPORTED, "fused linear forward supports in_features up to %d",
-                lwl::kLinearMaxInFeatures);
-  if (!lwl::kLinearKernelAvailable)
-    return fail(LWL_ERR_UNSUPPORTED, "fused linear kernel not available in this build");
-  if (!lwl::linear_applicable(dtype, lb, in_features))
-    return fail(LWL_ERR_UNSUPPORTED,
-                "fused linear forward takes bfloat16 latents of length 16385..32768 (block 2^15) with "
-                "in_features %% 8 == 0 and 528 <= in_features <= 5120 (dtype code %d, latent size %lld, in_features %lld)",
-                dtype, (long long)latent_size, (long long)in_features);
-  if (tokens * in_features * 2 >= ((int64_t)1 << 31))
-    return fail(LWL_ERR_UNSUPPORTED, "fused linear forward: tokens * in_features must stay below 2^30");
-  return LWL_OK;
+  const int64_t esize = dtype == LWL_DTYPE_F32 ? 4 : 2;
+  const int64_t kOffsetLimit = (int64_t)1 << 31;
+  if (lwl::kLinearKernelAvailable && lwl::linear_applicable(dtype, lb, in_features)) {
+    if (tokens * in_features * 2 >= kOffsetLimit)
+      return fail(LWL_ERR_UNSUPPORTED, "fused linear forward: tokens * in_features must stay below 2^30");
+    // the epilogue addresses 16 tokens' rows of out from one buffer resource
+    if (out_features * 16 * 2 >= kOffsetLimit)
+      return fail(LWL_ERR_UNSUPPORTED, "fused linear forward: out_features must stay below 2^26");
+    // the straddling-row combine runs one grid row per tile boundary
+    const int64_t nblocks = (in_features * out_features + ((int64_t)1 << lb) - 1) >> lb;
+    if (nblocks > 65536)
+      return fail(LWL_ERR_UNSUPPORTED, "fused linear forward: in_features * out_features must stay below 2^31");
+    return LWL_OK;
+  }
+  if (lwl::linear_small_applicable(dtype, lb, in_features)) {
+    if (tokens * in_features * esize >= kOffsetLimit || tokens * out_features * esize >= kOffsetLimit)
+      return fail(LWL_ERR_UNSUPPORTED,
+                  "fused linear forward: tokens * in_features and tokens * out_features must stay below 2 GiB");
+    return LWL_OK;
+  }
+  return fail(LWL_ERR_UNSUPPORTED,
+              "fused linear forward takes (a) bfloat16 latents of length 16385..32768 (block 2^15) with "
+              "in_features %% 8 == 0 and 528 <= in_features <= 5120, or (b) float32, float16 or bfloat16 "
+              "latents of block <= 2^14 with block_size %% in_features == 0 (dtype code %d, latent size %lld, "
+              "in_features %lld)",
+              dtype, (long long)latent_size, (long long)in_features);
+}
+
+bool linear_uses_mfma(const lwl::LinearArgs& a) {
+  return lwl::linear_applicable(a.dtype, a.log_block, a.in_features);
 }
 
 lwl::LinearArgs plan_linear(int dtype, int64_t tokens, int64_t in_features, int64_t latent_size,
@@ -158,12 +180,20 @@ lwl::LinearArgs plan_linear(int dtype, int64_t tokens, int64_t in_features, int6
   a.layers = (int)layers;
   a.weight_scale = (float)weight_scale;
   a.blocks_per_wg = 1;
-  a.blocks_per_wg = lwl::linear_blocks_per_wg(a);
-  a.token_splits = lwl::linear_token_splits(a);
+  if (linear_uses_mfma(a)) {
+    a.blocks_per_wg = lwl::linear_blocks_per_wg(a);
+    a.token_splits = lwl::linear_token_splits(a);
+  } else {
+    a.token_splits = lwl::linear_small_token_splits(a);
+  }
   return a;
 }
 
-size_t linear_ws(const lwl::LinearArgs& a) { return align_up(lwl::linear_workspace_bytes(a)); }
+// Workspace: the matrix-core kernel's partial rows and tiled x; the small-block
+// kernel needs none.
+size_t linear_ws(const lwl::LinearArgs& a) {
+  return linear_uses_mfma(a) ? align_up(lwl::linear_workspace_bytes(a)) : 0;
+}
 
 // Fused latent-gradient checks (no reference counterpart: the reference forms
 // grad_weight in HBM, block_fht.py:339-352).
@@ -187,6 +217,9 @@ int check_linear_bwd(int dtype, int64_t tokens, int64_t in_features, int64_t lat
   if (tpad * in_features * 2 >= ((int64_t)1 << 31) || tpad * out_features * 2 >= ((int64_t)1 << 31))
     return fail(LWL_ERR_UNSUPPORTED,
                 "fused linear latent gradient: tokens * in_features and tokens * out_features must stay below 2^30");
+  // the x / g re-layout kernels run one grid row per 128 features
+  if ((in_features + 127) / 128 > 65535 || (out_features + 127) / 128 > 65535)
+    return fail(LWL_ERR_UNSUPPORTED, "fused linear latent gradient: in_features and out_features must stay below 2^23");
   return LWL_OK;
 }
 
@@ -332,7 +365,9 @@ int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features
 
 size_t lwl_bfht_linear_forward_workspace_size(int64_t tokens, int64_t in_features,
                                               int64_t out_features, int64_t latent_size) {
-  // the workspace does not depend on the element type; bf16 is the type the kernel takes
+  // The query has no dtype: it returns what the bfloat16 matrix-core kernel
+  // needs when it takes the shape (other dtypes then run the small-block kernel,
+  // which needs none), else 0.
   if (check_linear(LWL_DTYPE_BF16, tokens, in_features, latent_size, out_features, 1)) return 0;
   return linear_ws(plan_linear(LWL_DTYPE_BF16, tokens, in_features, latent_size, out_features, 1, 0,
                                1.0));
@@ -355,7 +390,9 @@ int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, in
   a.latent = latent;
   a.out = out;
   a.work = workspace;
-  return hip_status(lwl::launch_linear(a, (hipStream_t)stream), "lwl_bfht_linear_forward");
+  const hipError_t e = linear_uses_mfma(a) ? lwl::launch_linear(a, (hipStream_t)stream)
+                                           : lwl::launch_linear_small(a, (hipStream_t)stream);
+  return hip_status(e, "lwl_bfht_linear_forward");
 }
 
 int lwl_bfht_check_linear_backward_latent(int dtype, int64_t tokens, int64_t in_features,

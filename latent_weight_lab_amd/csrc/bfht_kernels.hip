@@ -19,6 +19,7 @@
 #include "bfht_block.h"
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 namespace lwl {
@@ -633,14 +634,22 @@ static hipError_t launch_tile_pass(const BfhtArgs& a, hipStream_t s, int src, in
 // D_0 last) and leaves partial rows of n values for the block sum.
 // Workgroups of the persistent tile passes: one per CU (a workgroup takes all
 // of a CU's LDS), never more than the tiles.
+// The CU count of the current device, cached per device: each slot is written
+// with the same value by whichever thread gets there first (relaxed atomics,
+// so concurrent callers need no lock).
+constexpr int kMaxDevices = 64;
+static std::atomic<int> g_cu_count[kMaxDevices];
+
 static unsigned tile_grid(int64_t ntiles) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-    else
-      cus = 256;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  if (dev >= 0 && dev < kMaxDevices) cus = g_cu_count[dev].load(std::memory_order_relaxed);
+  if (cus <= 0) {
+    int v = 0;
+    cus = (dev >= 0 && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+              ? v
+              : 256;
+    if (dev >= 0 && dev < kMaxDevices) g_cu_count[dev].store(cus, std::memory_order_relaxed);
   }
   return (unsigned)std::min<int64_t>(ntiles, cus);
 }

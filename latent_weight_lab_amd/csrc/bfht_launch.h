@@ -75,6 +75,15 @@ int linear_token_splits(const LinearArgs& a);     // needs blocks_per_wg
 size_t linear_workspace_bytes(const LinearArgs& a);
 hipError_t launch_linear(const LinearArgs& a, hipStream_t s);
 
+// The reference extension's own fused-linear domain (bfht_linear_small.hip):
+// float32 / float16 / bfloat16 latents, B <= 2^14, B % in_features == 0, so no
+// row straddles two blocks.  Blocks generated in float32 into LDS and
+// contracted there in float32; no workspace.
+constexpr int kLinearSmallMaxLog = 14;
+bool linear_small_applicable(int dtype, int log_block, int64_t in_features);
+int linear_small_token_splits(const LinearArgs& a);  // needs tokens, log_block, nblocks_w
+hipError_t launch_linear_small(const LinearArgs& a, hipStream_t s);
+
 // Fused latent gradient of BlockFHTLinear (bfht_linear_bwd.hip):
 // grad_latent = weight_scale * T^T(grad^T x) with grad^T x formed per block on
 // chip.  bf16, B = 2^15, in_features % 16 == 0, at most 4 row tiles per block.

@@ -1,0 +1,172 @@
+// Fused BlockFHTLinear forward for the reference extension's own domain:
+// float32 / float16 / bfloat16, block B <= 2^14 and B % in_features == 0
+// (reference gate latent_weight_lab/block_fht.py:263-273, kernel
+// csrc/block_fht_ext_cuda.cu:225-329, launcher :624-681).
+//
+// out[t, o] = sum_i x[t, i] * (weight_scale * W[o, i]),  W[o, i] = y[o * in + i]
+//
+// in_features divides B, so every output row lies inside one generated block
+// and no row straddles two.  A workgroup owns G consecutive blocks (the slots of
+// the whole-block VALU generator: one block of 2^14 per 512-thread workgroup,
+// or 256 / (B/32) smaller blocks per 256-thread workgroup) and a range of
+// tokens.  It generates its blocks in float32 straight into an LDS weight tile
+// (the generator's final stores land in LDS instead of memory, already scaled
+// by weight_scale, as the reference scales its shared-memory values), then
+// contracts the tile with its tokens: a team of min(in, 64) lanes computes four
+// tokens of one output row, lanes striding over k, and sums its lanes with
+// butterfly shuffles.  All arithmetic is float32; x and out keep the I/O type.
+// The weight never touches memory.
+#include "bfht_block.h"
+
+namespace lwl {
+namespace {
+
+// LDS window of the generator's stores: global position g of the workgroup's
+// tile lands at w[g - base], multiplied by weight_scale.  `range` / call take
+// the role of the buffer-resource form of the per-block store (indices outside
+// [0, count) are dropped), `at` the element form.
+struct LdsRange {
+  int first;
+  int count;
+};
+struct LdsWeightStore {
+  float* w;
+  int64_t base;
+  float scale;
+  __device__ LdsRange range(int64_t first, int64_t count) const {
+    return LdsRange{(int)(first - base), (int)count};
+  }
+  __device__ void operator()(LdsRange r, int i, float v) const {
+    if ((unsigned)i < (unsigned)r.count) w[r.first + i] = v * scale;
+  }
+  __device__ void at(int64_t i, float v) const { w[i - base] = v * scale; }
+};
+
+constexpr int kQuad = 4;  // tokens per team pass
+
+template <int LB>
+struct SmallLinearGeo {
+  using Gm = Geo<LB>;
+  static constexpr int kTileElems = Gm::G * Gm::B;  // weights generated per workgroup
+  static constexpr int kLdsFloats = BlockLds<LB>::FLOATS + kTileElems;
+};
+
+template <int LB, class T>
+__global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small(const T* __restrict__ x,
+                                                                 const T* __restrict__ latent, T* __restrict__ out,
+                                                                 int tokens, int in_f, int log_in, int out_f, int n,
+                                                                 int64_t nblocks, uint32_t seed32, int layers,
+                                                                 float scale, int token_split) {
+  using Gm = Geo<LB>;
+  using SG = SmallLinearGeo<LB>;
+  __shared__ float smem[SG::kLdsFloats];
+  float* wt = smem + BlockLds<LB>::FLOATS;  // the weight tile, row-major [rows][in]
+  const int64_t tile = blockIdx.x;
+  const int split = blockIdx.y;
+  const int64_t size = (int64_t)in_f * out_f;
+  const int64_t base = tile * SG::kTileElems;
+
+  // 1. the tile's G blocks (inactive slots past the last block store nothing;
+  //    their rows lie past out_features and are never read)
+  const int64_t slot = tile * Gm::G + (threadIdx.x >> Gm::LT);
+  block_fwd_slot<LB, T>(latent, LdsWeightStore{wt, base, scale}, n, 0, slot, nblocks, 0, size, seed32, layers,
+                        smem);
+  __syncthreads();
+
+  // 2. rows row0 .. row0 + rows - 1 against this split's token quads
+  const int row0 = (int)(base >> log_in);
+  const int tile_rows = SG::kTileElems >> log_in;
+  const int rows = out_f - row0 < tile_rows ? out_f - row0 : tile_rows;
+  const int quads = (tokens + kQuad - 1) / kQuad;
+  const int per_split = (quads + token_split - 1) / token_split;
+  const int q0 = split * per_split;
+  const int q1 = q0 + per_split < quads ? q0 + per_split : quads;
+  if (rows <= 0 || q0 >= q1) return;  // uniform across the workgroup
+  const int log_ks = log_in < 6 ? log_in : 6;  // lanes per team: min(in, 64)
+  const int ks = 1 << log_ks;
+  const int lane = threadIdx.x & 63;
+  const int j = lane & (ks - 1);
+  const int team = (int)(threadIdx.x >> log_ks);
+  const int nteams = Gm::WG >> log_ks;
+  const int npairs = (q1 - q0) * rows;
+  const auto x_r = tile_rsrc(x, (uint64_t)tokens * in_f * sizeof(T));
+  const auto o_r = tile_rsrc(out, (uint64_t)tokens * out_f * sizeof(T));
+  // A team's lanes share `pr`, so the shuffles below only read lanes that run
+  // the same iteration.
+  for (int pr = team; pr < npairs; pr += nteams) {
+    const int q = q0 + pr / rows;
+    const int r = pr - (pr / rows) * rows;
+    const int t0 = q * kQuad;
+    const float* wrow = wt + (r << log_in);
+    int xi[kQuad];
+#pragma unroll
+    for (int u = 0; u < kQuad; ++u) xi[u] = t0 + u < tokens ? (t0 + u) * in_f : -1;  // -1: reads 0
+    float acc[kQuad] = {0.f, 0.f, 0.f, 0.f};
+    for (int k = j; k < in_f; k += ks) {
+      const float w = wrow[k];
+#pragma unroll
+      for (int u = 0; u < kQuad; ++u) acc[u] += buf_load<T>(x_r, xi[u] < 0 ? -1 : xi[u] + k) * w;
+    }
+#pragma unroll
+    for (int u = 0; u < kQuad; ++u)
+      for (int s = ks >> 1; s >= 1; s >>= 1) acc[u] += __shfl_xor(acc[u], s, 64);
+    if (j == 0) {
+#pragma unroll
+      for (int u = 0; u < kQuad; ++u)
+        buf_store<T>(acc[u], o_r, t0 + u < tokens ? (t0 + u) * out_f + row0 + r : -1);
+    }
+  }
+}
+
+template <int LB, class T>
+hipError_t launch_small_lb(const LinearArgs& a, hipStream_t s) {
+  using Gm = Geo<LB>;
+  const int64_t wtiles = (a.nblocks_w + Gm::G - 1) / Gm::G;
+  int log_in = 0;
+  while (((int64_t)1 << log_in) < a.in_features) ++log_in;
+  hipLaunchKernelGGL((bfht_linear_small<LB, T>), dim3((unsigned)wtiles, (unsigned)a.token_splits), dim3(Gm::WG), 0,
+                     s, (const T*)a.x, (const T*)a.latent, (T*)a.out, (int)a.tokens, (int)a.in_features, log_in,
+                     (int)a.out_features, (int)a.n, a.nblocks_w, a.seed32, a.layers, a.weight_scale,
+                     a.token_splits);
+  return hipGetLastError();
+}
+
+template <class T, int... LBs>
+hipError_t dispatch_small(const LinearArgs& a, hipStream_t s, std::integer_sequence<int, LBs...>) {
+  using Fn = hipError_t (*)(const LinearArgs&, hipStream_t);
+  static const Fn table[] = {&launch_small_lb<LBs, T>...};
+  return table[a.log_block](a, s);
+}
+
+}  // namespace
+
+bool linear_small_applicable(int dtype, int log_block, int64_t in_features) {
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return false;
+  if (log_block < 0 || log_block > kLinearSmallMaxLog || in_features <= 0) return false;
+  return (((int64_t)1 << log_block) % in_features) == 0;
+}
+
+int linear_small_token_splits(const LinearArgs& a) {
+  // Each split regenerates the workgroup's blocks: at least 32 token quads
+  // (128 tokens) per split, and no more workgroups than about four per CU.
+  const int g = a.log_block >= 5 ? (a.log_block >= 13 ? 1 : 256 >> (a.log_block - 5)) : 256;
+  const int64_t wtiles = (a.nblocks_w + g - 1) / g;
+  const int64_t quads = (a.tokens + kQuad - 1) / kQuad;
+  int64_t split = (quads + 31) / 32;
+  const int64_t cap = wtiles >= 1024 ? 1 : (1024 + wtiles - 1) / wtiles;
+  if (split > cap) split = cap;
+  if (split > 65535) split = 65535;
+  return (int)(split < 1 ? 1 : split);
+}
+
+hipError_t launch_linear_small(const LinearArgs& a, hipStream_t s) {
+  using Seq = std::make_integer_sequence<int, kLinearSmallMaxLog + 1>;
+  switch (a.dtype) {
+    case kF32: return dispatch_small<float>(a, s, Seq{});
+    case kF16: return dispatch_small<f16>(a, s, Seq{});
+    case kBF16: return dispatch_small<bf16>(a, s, Seq{});
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace lwl

@@ -156,6 +156,15 @@ def test_next_power_of_two():
         ((2, 16, 768, 32768, 3072, 4), N.LWL_ERR_INVALID, "layers must be 1, 2, or 3"),
         ((2, 16, 0, 32768, 3072, 3), N.LWL_ERR_INVALID, "in_features must be positive"),
         ((2, 1 << 20, 1024, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "2^30"),
+        ((2, 16, 768, 32768, 1 << 26, 3), N.LWL_ERR_UNSUPPORTED, "2^26"),       # 16 tokens' rows of out > 2 GiB
+        ((2, 16, 5120, 32768, 1 << 20, 3), N.LWL_ERR_UNSUPPORTED, "2^31"),      # > 65536 tile boundaries
+        # the reference extension's own domain (block <= 2^14, block % in == 0), every dtype
+        ((0, 5, 8, 32, 6, 2), N.LWL_OK, ""),                                   # reference test shape
+        ((1, 1, 1024, 16384, 4096, 2), N.LWL_OK, ""),                          # reference profiling case
+        ((2, 300, 1024, 16384, 4096, 3), N.LWL_OK, ""),
+        ((0, 9, 1, 1, 7, 3), N.LWL_OK, ""),                                    # block 2^0
+        ((0, 16, 768, 16384, 3072, 3), N.LWL_ERR_UNSUPPORTED, "block_size % in_features == 0"),
+        ((0, 1 << 20, 1024, 16384, 4096, 2), N.LWL_ERR_UNSUPPORTED, "2 GiB"),   # tokens * out * 4 >= 2^31
     ],
 )
 def test_linear_validation(args, code, msg):
@@ -181,6 +190,9 @@ def test_linear_workspace_size():
     # 528 in_features: 125 rows per two blocks exceed the register budget: one block per tile
     partial = (ceil_div(528 * 100, 32768) * 2 * 300 * 4 + 255) // 256 * 256
     assert lib.lwl_bfht_linear_forward_workspace_size(300, 528, 100, 32768) == partial + 19 * 17 * 1024
+    # the reference-domain kernel (block <= 2^14) keeps everything in LDS: no workspace
+    assert lib.lwl_bfht_linear_forward_workspace_size(5, 8, 6, 32) == 0
+    assert lib.lwl_bfht_linear_forward_workspace_size(300, 1024, 4096, 16384) == 0
 
 
 def ceil_div(a, b):
@@ -199,6 +211,7 @@ def ceil_div(a, b):
         ((2, 16, 768, 8192, 64, 3), N.LWL_ERR_UNSUPPORTED, "block 2^15"),      # block 2^13
         ((2, 16, 768, 32768, 64, 0), N.LWL_ERR_INVALID, "layers must be 1, 2, or 3"),
         ((2, 1 << 20, 1024, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "2^30"),
+        ((2, 16, 768, 32768, 1 << 24, 3), N.LWL_ERR_UNSUPPORTED, "2^23"),   # > 65535 re-layout grid rows
     ],
 )
 def test_linear_backward_latent_validation(args, code, msg):

@@ -54,6 +54,26 @@ def test_sign_words_match_golden(golden):
         assert int(got[0]) == value
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_public_signs_for(golden, dtype):
+    """The public ``signs_for`` (reference block_fht.py:55-81) against the reference-written golden
+    sign vectors, in the reference tensor's dtype and device, plus the reference self-test
+    tests/test_block_fht.py:25-31 (signs_for == the bits of sign_word_for, position by position)."""
+    from latent_weight_lab_amd import sign_word_for, signs_for
+
+    ref = torch.empty(1, dtype=dtype, device="cuda")
+    for case in golden["signs"]:
+        got = signs_for(ref, case["block"], case["layer"], case["seed"], case["block_size"])
+        assert got.dtype == dtype and got.device == ref.device and got.shape == (case["block_size"],)
+        assert np.array_equal(to_np(got), decode_array(case["signs"])), case["seed"]
+    got = signs_for(ref, block=3, layer=2, seed=999, block_size=65)
+    want = [1.0 if (sign_word_for(999, 3, 2, p >> 5) >> (p & 31)) & 1 else -1.0 for p in range(65)]
+    assert to_np(got).tolist() == want
+    # a whole 2^15 block against the oracle's sign vector
+    got = signs_for(ref, block=255, layer=3, seed=7, block_size=32768)
+    assert np.array_equal(to_np(got), O.sign_vector(7, 255, 3, 32768))
+
+
 # ---------------------------------------------------------------- golden fixtures
 
 def test_golden_slices_fp32(golden):
@@ -191,20 +211,26 @@ def test_bf16_slice_backward_equals_masked_full_backward_bitwise():
     assert rel_l2(to_np(got), gwant) < TOL[torch.bfloat16]
 
 
-def test_config2_slice_and_determinism():
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_config2_slice_and_determinism(dtype):
+    """Config 2's slice [12,345, 1,012,345) (31 blocks, both ends inside a block) at config 2's
+    own latent (seed 1) and hash seed 7: forward and backward against the C oracle, and
+    run-to-run bit equality of both (the block sum runs in a fixed order)."""
     torch.manual_seed(1)
-    lat = torch.randn(32768, dtype=torch.float32)
+    lat = torch.randn(32768, dtype=torch.float32).to(dtype)
     start, stop = 12_345, 1_012_345
     latent = lat.cuda()
     y1 = ops.forward(latent, 8_388_608, 3, 7, start, stop)
     y2 = ops.forward(latent, 8_388_608, 3, 7, start, stop)
     assert torch.equal(y1, y2)
     want = c_oracle.forward(lat.double().numpy(), 8_388_608, 3, 7, start, stop)
-    assert rel_l2(to_np(y1), want) < 1e-5
-    g = torch.randn(stop - start, generator=torch.Generator().manual_seed(2)).cuda()
-    b1 = ops.backward(g, 32768, torch.float32, 8_388_608, 3, 7, start, stop)
-    b2 = ops.backward(g, 32768, torch.float32, 8_388_608, 3, 7, start, stop)
+    assert rel_l2(to_np(y1), want) < TOL[dtype]
+    g = torch.randn(stop - start, generator=torch.Generator().manual_seed(2)).to(dtype)
+    b1 = ops.backward(g.cuda(), 32768, dtype, 8_388_608, 3, 7, start, stop)
+    b2 = ops.backward(g.cuda(), 32768, dtype, 8_388_608, 3, 7, start, stop)
     assert torch.equal(b1, b2)  # fixed-order reduction
+    gwant = c_oracle.backward(g.double().numpy(), 32768, 8_388_608, 3, 7, start, stop)
+    assert rel_l2(to_np(b1), gwant) < TOL[dtype]
 
 
 # ---------------------------------------------------------------- BASELINE config 3 (multi-pass)

@@ -108,13 +108,14 @@ def test_generate_route_is_differentiable_in_the_latent():
 
 
 def test_unsupported_shapes_fall_back_to_generated_weight():
-    # fp32 latents and blocks other than 2^15 use generate + F.linear (reference gate block_fht.py:263-273)
+    # outside both fused kernels (here fp32, block 2^12, 4096 % 48 != 0) W is generated and
+    # F.linear runs, as the reference's fallback (gate block_fht.py:263-273)
     g = torch.Generator().manual_seed(4)
     latent = torch.randn(4096, generator=g).cuda()
-    x = torch.randn(9, 64, generator=g).cuda()
-    assert not ops.linear_supported(64, 48, latent, x)
-    got = block_fht_linear_forward(x, latent, 48, 2, 13, weight_scale=0.5)
-    want = oracle_linear(x.cpu(), latent.cpu(), 48, 2, 13, 0.5)
+    x = torch.randn(9, 48, generator=g).cuda()
+    assert not ops.linear_supported(48, 64, latent, x)
+    got = block_fht_linear_forward(x, latent, 64, 2, 13, weight_scale=0.5)
+    want = oracle_linear(x.cpu(), latent.cpu(), 64, 2, 13, 0.5)
     assert O.rel_l2(got.double().cpu().numpy(), want) < 1e-5
 
 

@@ -211,3 +211,133 @@ def test_flush_weight_gradients_off_the_16_byte_grid_bitwise():
     for (lat, gw, size, layers, seed, ws, _), r in zip(specs, got):
         want = ws * block_fht_grad_latent(lat, gw, size, layers, seed)
         assert torch.equal(r, want), (size, gw.data_ptr() % 16)
+
+
+# ---------------------------------------------------------------- reference module tests, on the GPU
+
+def _rel(a, b):
+    return O.rel_l2(a.detach().double().cpu().numpy(), b.detach().double().cpu().numpy())
+
+
+def _check_close(got, want, dtype):
+    # reference bar: allclose(atol=1e-6) on float32 CPU tensors; bf16 runs at the 1e-2 rel-L2 bar
+    if dtype == F32:
+        assert torch.allclose(got, want, atol=1e-6, rtol=1e-5), _rel(got, want)
+    else:
+        assert _rel(got, want) < 1e-2
+
+
+def _gain_pair(dtype, shape_kw):
+    kw = dict(bias=True, layers=2, seed=13, output_gain=True, input_gain=True, modulation_alpha=1e-3,
+              modulation_centered=True, **shape_kw)
+    dynamic = BlockFHTLinear(**kw).cuda()
+    with torch.no_grad():
+        dynamic.output_gain.copy_(torch.linspace(0.7, 1.3, dynamic.out_features))
+        dynamic.input_gain.copy_(torch.linspace(0.6, 1.4, dynamic.in_features))
+    dynamic = dynamic.to(dtype)
+    cached = BlockFHTLinear(**kw).cuda().to(dtype)
+    cached.load_state_dict(dynamic.state_dict())
+    return dynamic, cached
+
+
+@pytest.mark.parametrize("dtype,shape_kw", [
+    (F32, dict(in_features=5, out_features=3, latent_dim=8)),           # the reference's shape
+    (F32, dict(in_features=768, out_features=768, latent_dim=5898)),    # GPT-2 proj at latent ratio 0.01
+    (BF16, dict(in_features=768, out_features=3072, latent_dim=32768)),  # matrix-core generator
+])
+def test_cached_grad_matches_dynamic_with_channel_gains(dtype, shape_kw):
+    """Reference tests/test_block_fht.py:100-143 (and :78-97 without gains): the prepare ->
+    forward/backward -> flush path gives the latent, bias and both gains the gradients of the
+    dynamic (uncached) module."""
+    torch.manual_seed(321)
+    dynamic, cached = _gain_pair(dtype, shape_kw)
+    x = torch.randn(4, dynamic.in_features, device="cuda").to(dtype)
+
+    dynamic_loss = dynamic(x).float().square().mean()
+    dynamic_loss.backward()
+
+    prepare_block_fht_weight_cache(cached)
+    assert cached._cached_weight is not None
+    cached_loss = cached(x).float().square().mean()
+    cached_loss.backward()
+    flush_block_fht_weight_cache(cached)
+    assert cached._cached_weight is None
+
+    _check_close(cached_loss, dynamic_loss, dtype)
+    for name in ("generator.latent", "bias", "output_gain", "input_gain"):
+        got = cached.get_parameter(name).grad
+        want = dynamic.get_parameter(name).grad
+        assert got is not None and want is not None, name
+        _check_close(got, want, dtype)
+
+
+@pytest.mark.parametrize("dtype,shape_kw", [
+    (F32, dict(in_features=5, out_features=3, latent_dim=8)),
+    (BF16, dict(in_features=768, out_features=3072, latent_dim=32768)),
+])
+def test_cached_grad_matches_dynamic(dtype, shape_kw):
+    """Reference tests/test_block_fht.py:78-97: no gains, bias only."""
+    torch.manual_seed(123)
+    dynamic = BlockFHTLinear(bias=True, layers=2, seed=11, **shape_kw).cuda().to(dtype)
+    cached = BlockFHTLinear(bias=True, layers=2, seed=11, **shape_kw).cuda().to(dtype)
+    cached.load_state_dict(dynamic.state_dict())
+    x = torch.randn(4, dynamic.in_features, device="cuda").to(dtype)
+    dynamic_loss = dynamic(x).float().square().mean()
+    dynamic_loss.backward()
+    prepare_block_fht_weight_cache(cached)
+    cached_loss = cached(x).float().square().mean()
+    cached_loss.backward()
+    flush_block_fht_weight_cache(cached)
+    _check_close(cached_loss, dynamic_loss, dtype)
+    _check_close(cached.generator.latent.grad, dynamic.generator.latent.grad, dtype)
+    _check_close(cached.bias.grad, dynamic.bias.grad, dtype)
+
+
+@pytest.mark.parametrize("dtype,shape_kw", [
+    (F32, dict(in_features=5, out_features=3, latent_dim=8)),
+    (F32, dict(in_features=768, out_features=2304, latent_dim=17694)),
+    (BF16, dict(in_features=768, out_features=3072, latent_dim=32768)),
+])
+def test_suspended_cache_keeps_ce_grad_and_live_perturbation_grad(dtype, shape_kw):
+    """Reference tests/test_block_fht.py:146-180: a forward with a perturbed live latent runs
+    between prepare and flush with the cache suspended; the flush then adds the cached (CE)
+    gradient to the live perturbation gradient, as the dynamic module accumulates both."""
+    from latent_weight_lab_amd import restore_block_fht_weight_cache, suspend_block_fht_weight_cache
+
+    torch.manual_seed(456)
+    dynamic = BlockFHTLinear(bias=True, layers=2, seed=17, **shape_kw).cuda().to(dtype)
+    hybrid = BlockFHTLinear(bias=True, layers=2, seed=17, **shape_kw).cuda().to(dtype)
+    hybrid.load_state_dict(dynamic.state_dict())
+    x = torch.randn(4, dynamic.in_features, device="cuda").to(dtype)
+    perturbation = torch.randn_like(dynamic.generator.latent) * 1e-3
+
+    dynamic_base = dynamic(x).float().square().mean()
+    dynamic_base.backward()
+    with torch.no_grad():
+        dynamic.generator.latent.add_(perturbation)
+    dynamic_perturbed = dynamic(x).float().square().mean()
+    dynamic_perturbed.backward()
+    with torch.no_grad():
+        dynamic.generator.latent.sub_(perturbation)
+
+    prepare_block_fht_weight_cache(hybrid)
+    hybrid_base = hybrid(x).float().square().mean()
+    hybrid_base.backward()
+    suspended = suspend_block_fht_weight_cache(hybrid)
+    assert len(suspended) == 1 and hybrid._cached_weight is None
+    with torch.no_grad():
+        hybrid.generator.latent.add_(perturbation)
+    hybrid_perturbed = hybrid(x).float().square().mean()
+    hybrid_perturbed.backward()
+    with torch.no_grad():
+        hybrid.generator.latent.sub_(perturbation)
+    restore_block_fht_weight_cache(suspended)
+    assert hybrid._cached_weight is not None
+    with pytest.raises(RuntimeError, match="live cached weight"):
+        restore_block_fht_weight_cache(suspended)
+    flush_block_fht_weight_cache(hybrid)
+
+    _check_close(hybrid_base, dynamic_base, dtype)
+    _check_close(hybrid_perturbed, dynamic_perturbed, dtype)
+    _check_close(hybrid.generator.latent.grad, dynamic.generator.latent.grad, dtype)
+    _check_close(hybrid.bias.grad, dynamic.bias.grad, dtype)
