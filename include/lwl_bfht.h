@@ -103,6 +103,24 @@ int lwl_bfht_backward(const void* grad_out, int dtype, int64_t latent_size, int6
                       int64_t layers, int64_t seed, int64_t start, int64_t stop, void* grad_latent,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------- backward, no allocation
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory or pass a workspace (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): lwl_bfht_backward with the same
+ * arguments but no workspace.  Its scratch is a file-scope device array of
+ * LWL_BFHT_NOALLOC_SCRATCH_BYTES per GPU (held from first use to process
+ * exit); a call whose scratch (lwl_bfht_backward_workspace_size) exceeds it
+ * returns LWL_ERR_UNSUPPORTED.  That covers every whole-block backward (B <=
+ * 2^15) of up to 256 blocks of 2^15 (config 2 in float32), not the multi-pass
+ * blocks' work buffer beyond 32 MiB.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race.
+ * Allocates nothing; results are bit-identical to lwl_bfht_backward.
+ */
+#define LWL_BFHT_NOALLOC_SCRATCH_BYTES (32 << 20)
+int lwl_bfht_backward_noalloc(const void* grad_out, int dtype, int64_t latent_size, int64_t output_size,
+                              int64_t layers, int64_t seed, int64_t start, int64_t stop, void* grad_latent,
+                              void* stream);
+
 /* ---------------------------------------------------------------- fused linear
  * Replaces ext.linear_forward (reference csrc/block_fht_ext.cpp:53-67 ->
  * csrc/block_fht_ext_cuda.cu:624-681), called from block_fht.py:274.

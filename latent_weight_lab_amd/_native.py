@@ -77,6 +77,7 @@ def _bind(lib) -> None:
         "lwl_bfht_check_forward": (i32, [i32, i64, i64, i64, i64, i64]),
         "lwl_bfht_backward_workspace_size": (sz, [i64, i64, i64, i64]),
         "lwl_bfht_backward": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, vp, vp, sz, vp]),
+        "lwl_bfht_backward_noalloc": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, vp, vp]),
         "lwl_bfht_linear_forward_workspace_size": (sz, [i64, i64, i64, i64]),
         "lwl_bfht_linear_forward": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, dbl, vp, vp, sz, vp]),
         "lwl_bfht_check_linear_forward": (i32, [i32, i64, i64, i64, i64, i64]),

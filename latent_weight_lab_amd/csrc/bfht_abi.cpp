@@ -357,6 +357,32 @@ int lwl_bfht_backward(const void* grad_out, int dtype, int64_t latent_size, int6
   return hip_status(lwl::launch_bfht(a, (hipStream_t)stream, false), "lwl_bfht_backward");
 }
 
+int lwl_bfht_backward_noalloc(const void* grad_out, int dtype, int64_t latent_size, int64_t output_size,
+                              int64_t layers, int64_t seed, int64_t start, int64_t stop, void* grad_latent,
+                              void* stream) {
+  int rc = check_common(dtype, latent_size, output_size, layers, start, stop);
+  if (rc) return rc;
+  lwl::BfhtArgs a = plan(dtype, latent_size, layers, seed, start, stop);
+  if (!grad_latent || (a.nblocks > 0 && !grad_out))
+    return fail(LWL_ERR_INVALID, "grad_out and grad_latent must be non-null");
+  const size_t need = backward_ws(a);
+  if (need > (size_t)LWL_BFHT_NOALLOC_SCRATCH_BYTES)
+    return fail(LWL_ERR_UNSUPPORTED,
+                "lwl_bfht_backward_noalloc: this call needs %zu bytes of scratch, more than the %zu of its "
+                "device array; call lwl_bfht_backward with a workspace",
+                need, (size_t)LWL_BFHT_NOALLOC_SCRATCH_BYTES);
+  void* work = nullptr;
+  if (need > 0) {
+    hipError_t e = hipSuccess;
+    work = lwl::noalloc_scratch((hipStream_t)stream, &e);
+    if (!work) return hip_status(e, "lwl_bfht_backward_noalloc: scratch address");
+  }
+  a.src = grad_out;
+  a.dst = grad_latent;
+  a.work = work;
+  return hip_status(lwl::launch_bfht(a, (hipStream_t)stream, false), "lwl_bfht_backward_noalloc");
+}
+
 int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features,
                                   int64_t latent_size, int64_t out_features, int64_t layers) {
   const int rc = check_linear(dtype, tokens, in_features, latent_size, out_features, layers);

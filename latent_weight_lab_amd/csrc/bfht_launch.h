@@ -34,6 +34,10 @@ struct BfhtArgs {
 
 hipError_t launch_bfht(const BfhtArgs& a, hipStream_t s, bool forward);
 
+// Device address of the no-allocation entry's scratch array on the device of
+// stream s (bfht_noalloc.hip), or nullptr with the HIP error in *err.
+void* noalloc_scratch(hipStream_t s, hipError_t* err);
+
 // Matrix-core path for bfloat16 blocks of exactly 2^15 (bfht_mfma.hip).  The
 // backward writes one float32 partial row of n values per block into `work`.
 bool mfma15_applicable(const BfhtArgs& a, bool fwd);
