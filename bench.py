@@ -420,15 +420,28 @@ def stack_bench(abi, torch):
             # one pass of the stack that keeps every output, each call allocating its own output and
             # scratch; latents and inputs resident.  Measured before any buffer of the timed runs
             # below exists.
+            # Reported as the route's own footprint: its resident tensors (latents; x) plus what the
+            # pass allocates at peak over them (outputs, scratch), so allocations elsewhere in this
+            # process do not count.
+            lat_mib = sum(lat.numel() * 2 for _, _, lat, _ in mats) / 2**20
+            x_mib = sum(x.numel() * 2 for x in xs.values()) / 2**20
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
             torch.cuda.reset_peak_memory_stats()
             before = torch.cuda.memory_allocated()
             kept = [lwl_ops.linear_forward(xs[inf], lat, outf, 3, seed, 1.0) for inf, outf, lat, seed in mats]
             torch.cuda.synchronize()
-            row["fused_peak_MiB"] = torch.cuda.max_memory_allocated() / 2**20
-            row["fused_peak_over_resident_MiB"] = (torch.cuda.max_memory_allocated() - before) / 2**20
+            transient = (torch.cuda.max_memory_allocated() - before) / 2**20
+            row["fused_peak_MiB"] = lat_mib + x_mib + transient
+            row["fused_transient_MiB"] = transient
             row["outputs_MiB"] = sum(o.numel() * 2 for o in kept) / 2**20
+            del kept
+            torch.cuda.synchronize()
+            torch.cuda.reset_peak_memory_stats()
+            before = torch.cuda.memory_allocated()
+            kept = lwl_ops.linear_forward_grouped([(xs[inf], lat, outf, 3, seed, 1.0) for inf, outf, lat, seed in mats])
+            torch.cuda.synchronize()
+            row["fused_grouped_peak_MiB"] = lat_mib + x_mib + (torch.cuda.max_memory_allocated() - before) / 2**20
             del kept
             # the same for the dense route: resident materialized weights, one F.linear each
             with torch.no_grad():
@@ -437,9 +450,11 @@ def stack_bench(abi, torch):
             torch.cuda.synchronize()
             row["dense_weights_MiB"] = sum(w.numel() * 2 for w in ws_dense) / 2**20
             torch.cuda.reset_peak_memory_stats()
+            before = torch.cuda.memory_allocated()
             kept = [torch.nn.functional.linear(xs[inf], w) for (inf, _, _, _), w in zip(mats, ws_dense)]
             torch.cuda.synchronize()
-            row["dense_peak_MiB"] = torch.cuda.max_memory_allocated() / 2**20
+            row["dense_peak_MiB"] = (x_mib + row["dense_weights_MiB"]
+                                     + (torch.cuda.max_memory_allocated() - before) / 2**20)
             del kept
             outs = [torch.empty(tokens, outf, dtype=torch.bfloat16, device="cuda") for _, outf, _, _ in mats]
             wss = [abi.linear_ws(tokens, inf, outf, 32768, "cuda") for inf, outf, _, _ in mats]
@@ -467,6 +482,26 @@ def stack_bench(abi, torch):
             sec = time_graph(torch, fused_stack, 5, 2)
             row["fused_ms"] = sec * 1e3
             row["fused_tokens_per_s"] = tokens / sec
+            # all 48 matrices in one grouped call (lwl_bfht_linear_forward_grouped): the jobs that
+            # the matrix-core kernel takes below its tiled batch size share few launches; at 8192
+            # tokens each job runs as its single call
+            N = abi.N
+            jobs = (N.LinearJob * len(mats))()
+            for j, (inf, outf, lat, seed), o in zip(jobs, mats, outs):
+                j.input, j.latent, j.out = xs[inf].data_ptr(), lat.data_ptr(), o.data_ptr()
+                j.tokens, j.in_features, j.latent_size, j.out_features = tokens, inf, lat.numel(), outf
+                j.layers, j.seed, j.weight_scale = 3, seed, 1.0
+            gbytes = abi.lib.lwl_bfht_linear_forward_grouped_workspace_size(2, jobs, len(mats))
+            gws = torch.empty(max(1, gbytes), dtype=torch.uint8, device="cuda")
+            row["fused_grouped_workspace_MiB"] = gbytes / 2**20
+
+            def grouped_stack():
+                N.check(abi.lib.lwl_bfht_linear_forward_grouped(2, jobs, len(mats), gws.data_ptr(), gbytes,
+                                                                abi.stream()))
+
+            sec = time_graph(torch, grouped_stack, 5, 2)
+            row["fused_grouped_ms"] = sec * 1e3
+            row["fused_grouped_tokens_per_s"] = tokens / sec
 
             def dense_stack():
                 for (inf, outf, _, _), o, w in zip(mats, outs, ws_dense):
@@ -476,7 +511,8 @@ def stack_bench(abi, torch):
             row["dense_ms"] = sec * 1e3
             row["dense_tokens_per_s"] = tokens / sec
             row["fused_over_dense"] = row["fused_ms"] / row["dense_ms"]
-            del ws_dense, xs, outs, wss
+            row["fused_grouped_over_dense"] = row["fused_grouped_ms"] / row["dense_ms"]
+            del ws_dense, xs, outs, wss, gws
             torch.cuda.empty_cache()
         except Exception as exc:  # noqa: BLE001
             row["error"] = f"{type(exc).__name__}: {exc}"

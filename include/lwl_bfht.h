@@ -150,6 +150,40 @@ int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, in
 int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features,
                                   int64_t latent_size, int64_t out_features, int64_t layers);
 
+/* ---------------------------------------------------------------- fused linear, grouped
+ * Several lwl_bfht_linear_forward calls in few launches (no reference
+ * counterpart: the reference calls ext.linear_forward once per matrix,
+ * block_fht.py:274, e.g. once per layer of a network in
+ * benchmarks/bench_fused_linear_stack.py:31-36).  Each job's output equals
+ * its own lwl_bfht_linear_forward call bit for bit.  At decode batch sizes a
+ * GPT-2 matrix has 18..72 generated blocks, so one matrix per launch leaves
+ * most of the chip idle; jobs the bf16 matrix-core kernel takes with fewer
+ * than 256 tokens run together, one launch per (layers, row tiles per block)
+ * class of up to 32 jobs; other jobs run as their single calls.  All jobs
+ * share `dtype`; outputs must not overlap; inputs and latents may be shared.
+ * Workspace (query with the same jobs): the grouped jobs' own workspaces side
+ * by side, plus the largest workspace of the jobs that run as single calls
+ * (those run one after another on the stream and share it).
+ */
+typedef struct lwl_bfht_linear_job {
+  const void* input;  /* [tokens, in_features] */
+  const void* latent; /* [latent_size] */
+  void* out;          /* [tokens, out_features] */
+  int64_t tokens;
+  int64_t in_features;
+  int64_t latent_size;
+  int64_t out_features;
+  int64_t layers;
+  int64_t seed;
+  double weight_scale;
+} lwl_bfht_linear_job;
+
+/* Host-only check of `count` jobs (each as lwl_bfht_check_linear_forward, plus disjoint outputs). */
+int lwl_bfht_check_linear_jobs(int dtype, const lwl_bfht_linear_job* jobs, int64_t count);
+size_t lwl_bfht_linear_forward_grouped_workspace_size(int dtype, const lwl_bfht_linear_job* jobs, int64_t count);
+int lwl_bfht_linear_forward_grouped(int dtype, const lwl_bfht_linear_job* jobs, int64_t count, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- fused latent gradient
  * Replaces the grad_latent branch of _BlockFHTLinearFn.backward (reference
  * latent_weight_lab/block_fht.py:339-352: grad_weight = grad^T @ input formed

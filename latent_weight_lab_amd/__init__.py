@@ -12,6 +12,7 @@ from .block_fht import (
     block_fht_linear_forward,
     block_fht_slice,
     flush_block_fht_weight_cache,
+    forward_fused_grouped,
     lowbias32,
     next_power_of_two,
     prepare_block_fht_weight_cache,
@@ -34,6 +35,7 @@ __all__ = [
     "block_fht_slice",
     "fixed_fht_mix",
     "flush_block_fht_weight_cache",
+    "forward_fused_grouped",
     "lowbias32",
     "next_power_of_two",
     "prepare_block_fht_weight_cache",

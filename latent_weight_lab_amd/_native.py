@@ -50,6 +50,22 @@ class WeightJob(ctypes.Structure):
     ]
 
 
+class LinearJob(ctypes.Structure):
+    """``lwl_bfht_linear_job``: one matrix of a grouped fused-linear call."""
+    _fields_ = [
+        ("input", ctypes.c_void_p),
+        ("latent", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("tokens", ctypes.c_int64),
+        ("in_features", ctypes.c_int64),
+        ("latent_size", ctypes.c_int64),
+        ("out_features", ctypes.c_int64),
+        ("layers", ctypes.c_int64),
+        ("seed", ctypes.c_int64),
+        ("weight_scale", ctypes.c_double),
+    ]
+
+
 class BlockFHTArgumentError(ValueError, RuntimeError):
     """Invalid argument.  The reference raises ValueError from its Python
     checks and RuntimeError from its extension's TORCH_CHECKs; this is both."""
@@ -69,6 +85,7 @@ def _bind(lib) -> None:
     i64, i32, sz, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p
     dbl, u32p = ctypes.c_double, ctypes.POINTER(ctypes.c_uint32)
     jobp = ctypes.POINTER(WeightJob)
+    ljobp = ctypes.POINTER(LinearJob)
     sigs = {
         "lwl_last_error": (ctypes.c_char_p, []),
         "lwl_abi_version": (i32, []),
@@ -81,6 +98,9 @@ def _bind(lib) -> None:
         "lwl_bfht_linear_forward_workspace_size": (sz, [i64, i64, i64, i64]),
         "lwl_bfht_linear_forward": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, dbl, vp, vp, sz, vp]),
         "lwl_bfht_check_linear_forward": (i32, [i32, i64, i64, i64, i64, i64]),
+        "lwl_bfht_check_linear_jobs": (i32, [i32, ljobp, i64]),
+        "lwl_bfht_linear_forward_grouped_workspace_size": (sz, [i32, ljobp, i64]),
+        "lwl_bfht_linear_forward_grouped": (i32, [i32, ljobp, i64, vp, sz, vp]),
         "lwl_bfht_linear_backward_latent_workspace_size": (sz, [i64, i64, i64, i64]),
         "lwl_bfht_linear_backward_latent": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, dbl, vp, vp, sz, vp]),
         "lwl_bfht_check_linear_backward_latent": (i32, [i32, i64, i64, i64, i64, i64]),

@@ -10,9 +10,11 @@ reference, all widenings:
   block 2^15, which run on the matrix cores: bf16 operands at every radix-32
   stage (9 roundings at 3 layers), float32 accumulation;
 * blocks of any size 2^0 .. 2^23 (reference CUDA: 2^5 .. 2^23);
-* the fused linear accepts any ``in_features <= block_size``
-  (reference: ``block_size % in_features == 0`` and block_size <= 2^14,
-  ``block_fht.py:273``);
+* the fused linear keeps the reference's own domain (float32 / float16 /
+  bfloat16, ``block_size <= 2^14``, ``block_size % in_features == 0``,
+  ``block_fht.py:263-273``) and adds bf16 latents of block 2^15 with
+  ``in_features % 8 == 0`` in 528..5120, rows straddling blocks (matrix cores);
+  several matrices can run in one grouped call (``forward_fused_grouped``);
 * latent gradients are summed over blocks in a fixed order (deterministic).
 
 There is no CPU path: CPU tensors raise RuntimeError.
@@ -97,14 +99,16 @@ def block_fht_linear_forward(input: torch.Tensor, latent: torch.Tensor, out_feat
     """``input @ (weight_scale * W)^T`` with ``W = BlockFHT(latent)[: in*out].view(out, in)``
     (reference ``block_fht.py:251-288``).
 
-    With ``fused=True`` (default) shapes the fused kernel takes (bf16 latents of block
-    2^15, ``in_features % 8 == 0``, 528..5120) generate W on chip for every token range
-    and contract it there, so only the latent and the activations live in HBM.  Other
-    shapes, or ``fused=False``, generate W once into a transient buffer (one launch,
-    ``weight_scale`` folded in) and call ``F.linear`` — the reference's fallback
-    (``:282-288``).  On MI355X that second route is the faster one at every batch size
-    measured (it costs the transient W, ~1 µs of HBM traffic per GPT-2 matrix), so callers
-    that can hold W pass ``fused=False``.  Both routes are differentiable in the input and
+    With ``fused=True`` (default) shapes a fused kernel takes — the reference's own domain
+    (float32 / float16 / bfloat16 latents of block <= 2^14 with ``block % in_features ==
+    0``), and bf16 latents of block 2^15 with ``in_features % 8 == 0`` in 528..5120 — generate
+    W on chip for every token range and contract it there, so only the latent and the
+    activations live in HBM.  Other shapes, or ``fused=False``, generate W once into a
+    transient buffer (one launch, ``weight_scale`` folded in) and call ``F.linear`` — the
+    reference's fallback (``:282-288``).  For one GPT-2 matrix at a time that second route
+    is the faster one on MI355X (it costs the transient W, ~1 µs of HBM traffic per
+    matrix); at decode batch sizes ``forward_fused_grouped`` runs many matrices' fused
+    kernels together and beats both.  Both routes are differentiable in the input and
     the latent, as the reference's fallback is: the fused one through ``_FusedLinearFn``
     (W regenerated in the backward), the other through ``block_fht_slice``.
     """
@@ -439,6 +443,41 @@ class BlockFHTLinear(nn.Module):
         # options applied in torch around the grouped kernels (the plain case
         # scales, casts and accumulates inside them)
         return self.modulation_alpha != 0.0 or self.output_gain is not None or self.input_gain is not None
+
+
+def forward_fused_grouped(modules: list["BlockFHTLinear"], inputs: list[torch.Tensor],
+                          weight_scale: float = 1.0) -> list[torch.Tensor]:
+    """``[m.forward_fused(x, weight_scale) for m, x in zip(modules, inputs)]`` with every
+    plain module (no gains, spectral correction, modulation or residual base) in one
+    grouped fused-linear call (``lwl_bfht_linear_forward_grouped``): at decode batch
+    sizes one matrix fills a fraction of the chip, and the grouped launch runs all of
+    them together (not in the reference, which calls ``ext.linear_forward`` per matrix,
+    ``block_fht.py:274``).  Outputs equal the per-module calls bit for bit.  Modules the
+    fused kernels do not take, other modules, and calls that record gradients run
+    ``forward_fused`` one by one."""
+    if len(modules) != len(inputs):
+        raise ValueError("modules and inputs must have the same length")
+    outs: list[torch.Tensor | None] = [None] * len(modules)
+    grouped, specs = [], []
+    for i, (m, x) in enumerate(zip(modules, inputs)):
+        g = m.generator
+        plain = not (m._needs_dense_path() or m.modulation_alpha != 0.0)
+        flat = x.reshape(-1, m.in_features)
+        records = torch.is_grad_enabled() and (g.latent.requires_grad or x.requires_grad)
+        if (plain and not records and flat.is_cuda and g.latent.is_cuda
+                and ops.linear_supported(m.in_features, m.out_features, g.latent, flat)
+                and (not specs or flat.dtype == specs[0][0].dtype)):
+            grouped.append(i)
+            specs.append((flat, g.latent, m.out_features, g.layers, g.seed, weight_scale * m.weight_scale))
+        else:
+            outs[i] = m.forward_fused(x, weight_scale=weight_scale)
+    if specs:
+        for i, y in zip(grouped, ops.linear_forward_grouped(specs)):
+            m, x = modules[i], inputs[i]
+            if m.bias is not None:
+                y = y + m.bias
+            outs[i] = y.reshape(*x.shape[:-1], m.out_features)
+    return outs
 
 
 def _cacheable(module: "BlockFHTLinear") -> bool:

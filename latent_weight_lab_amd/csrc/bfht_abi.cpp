@@ -240,6 +240,38 @@ lwl::LinearBwdArgs plan_linear_bwd(int64_t tokens, int64_t in_features, int64_t 
   return a;
 }
 
+// Grouped fused linear: every job checked as a single call; outputs disjoint.
+int check_linear_jobs(int dtype, const lwl_bfht_linear_job* jobs, int64_t count, bool need_ptrs,
+                      std::vector<lwl::LinearArgs>* out) {
+  if (count < 0) return fail(LWL_ERR_INVALID, "job count must be non-negative");
+  if (count > 0 && !jobs) return fail(LWL_ERR_INVALID, "jobs must be non-null");
+  std::vector<lwl::LinearArgs> v((size_t)count);
+  const int64_t esize = dtype == LWL_DTYPE_F32 ? 4 : 2;
+  for (int64_t i = 0; i < count; ++i) {
+    const lwl_bfht_linear_job& j = jobs[i];
+    const int rc = check_linear(dtype, j.tokens, j.in_features, j.latent_size, j.out_features, j.layers);
+    if (rc) return fail(rc, "job %lld: %s", (long long)i, g_last_error.c_str());
+    if (need_ptrs && j.tokens > 0 && (!j.input || !j.latent || !j.out))
+      return fail(LWL_ERR_INVALID, "job %lld: input, latent and out must be non-null", (long long)i);
+    v[(size_t)i] = plan_linear(dtype, j.tokens, j.in_features, j.latent_size, j.out_features, j.layers, j.seed,
+                               j.weight_scale);
+    v[(size_t)i].x = j.input;
+    v[(size_t)i].latent = j.latent;
+    v[(size_t)i].out = j.out;
+  }
+  if (need_ptrs)
+    for (int64_t a = 0; a < count; ++a)
+      for (int64_t b = a + 1; b < count; ++b) {
+        const uintptr_t x0 = (uintptr_t)jobs[a].out, y0 = (uintptr_t)jobs[b].out;
+        const uintptr_t x1 = x0 + (uintptr_t)(jobs[a].tokens * jobs[a].out_features * esize);
+        const uintptr_t y1 = y0 + (uintptr_t)(jobs[b].tokens * jobs[b].out_features * esize);
+        if (x1 > x0 && y1 > y0 && x0 < y1 && y0 < x1)
+          return fail(LWL_ERR_INVALID, "jobs %lld and %lld write overlapping outputs", (long long)a, (long long)b);
+      }
+  if (out) *out = std::move(v);
+  return LWL_OK;
+}
+
 int check_workspace(size_t need, const void* ws, size_t have) {
   if (need == 0) return LWL_OK;
   if (ws == nullptr || have < need)
@@ -419,6 +451,60 @@ int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, in
   const hipError_t e = linear_uses_mfma(a) ? lwl::launch_linear(a, (hipStream_t)stream)
                                            : lwl::launch_linear_small(a, (hipStream_t)stream);
   return hip_status(e, "lwl_bfht_linear_forward");
+}
+
+int lwl_bfht_check_linear_jobs(int dtype, const lwl_bfht_linear_job* jobs, int64_t count) {
+  const int rc = check_linear_jobs(dtype, jobs, count, true, nullptr);
+  return rc ? rc : ok();
+}
+
+// Grouped workspace: the grouped jobs' partial rows side by side (one launch
+// reads them all), then one region that the jobs running as single launches
+// reuse one after another (the largest of their workspaces).
+bool job_grouped(const lwl::LinearArgs& a) { return a.tokens > 0 && linear_uses_mfma(a) && lwl::linear_groupable(a); }
+
+size_t grouped_ws(const std::vector<lwl::LinearArgs>& v) {
+  size_t together = 0, single = 0;
+  for (const auto& a : v) {
+    if (a.tokens == 0) continue;
+    if (job_grouped(a)) together += linear_ws(a);
+    else single = std::max(single, linear_ws(a));
+  }
+  return together + single;
+}
+
+size_t lwl_bfht_linear_forward_grouped_workspace_size(int dtype, const lwl_bfht_linear_job* jobs, int64_t count) {
+  std::vector<lwl::LinearArgs> v;
+  if (check_linear_jobs(dtype, jobs, count, false, &v)) return 0;
+  return grouped_ws(v);
+}
+
+int lwl_bfht_linear_forward_grouped(int dtype, const lwl_bfht_linear_job* jobs, int64_t count, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  std::vector<lwl::LinearArgs> v;
+  int rc = check_linear_jobs(dtype, jobs, count, true, &v);
+  if (rc) return rc;
+  rc = check_workspace(grouped_ws(v), workspace, workspace_bytes);
+  if (rc) return rc;
+  // grouped jobs: their own partial-row slices (256-byte multiples, in job
+  // order); the others: one shared region after them, used in turn on the stream
+  std::vector<lwl::LinearArgs> grouped;
+  size_t off = 0;
+  for (auto& a : v)
+    if (job_grouped(a)) {
+      a.work = (unsigned char*)workspace + off;
+      off += linear_ws(a);
+      grouped.push_back(a);
+    }
+  for (auto& a : v) {
+    if (a.tokens == 0 || job_grouped(a)) continue;
+    a.work = linear_ws(a) ? (unsigned char*)workspace + off : nullptr;
+    const hipError_t e = linear_uses_mfma(a) ? lwl::launch_linear(a, (hipStream_t)stream)
+                                             : lwl::launch_linear_small(a, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_status(e, "lwl_bfht_linear_forward_grouped");
+  }
+  return hip_status(lwl::launch_linear_grouped(grouped.data(), (int64_t)grouped.size(), (hipStream_t)stream),
+                    "lwl_bfht_linear_forward_grouped");
 }
 
 int lwl_bfht_check_linear_backward_latent(int dtype, int64_t tokens, int64_t in_features,

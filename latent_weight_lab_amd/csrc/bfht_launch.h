@@ -79,6 +79,32 @@ int linear_token_splits(const LinearArgs& a);     // needs blocks_per_wg
 size_t linear_workspace_bytes(const LinearArgs& a);
 hipError_t launch_linear(const LinearArgs& a, hipStream_t s);
 
+// Several fused linears in few launches (bfht_linear.hip): jobs the
+// matrix-core kernel takes with one generated block per workgroup (batches
+// below its tiled-x size) run in one launch per (layers, row tiles) class of
+// up to kLinearGroupMax jobs, each job exactly as its single launch computes it
+// (same work items, same partial-row sums), with its own `work` (partial rows,
+// linear_workspace_bytes).
+constexpr int kLinearGroupMax = 32;
+struct LinearGroupJob {
+  const __bf16* x;
+  const __bf16* latent;
+  __bf16* out;
+  float* partial;
+  int32_t tokens, in_f, out_f, n;
+  uint32_t seed32;
+  float scale;
+  int32_t nblocks, pitch, token_split;
+};
+struct LinearGroupTable {  // passed by value; prefix counts workgroups, cprefix combine workgroups
+  int32_t count;
+  int32_t prefix[kLinearGroupMax + 1];
+  int32_t cprefix[kLinearGroupMax + 1];
+  LinearGroupJob job[kLinearGroupMax];
+};
+bool linear_groupable(const LinearArgs& a);
+hipError_t launch_linear_grouped(const LinearArgs* jobs, int64_t count, hipStream_t s);
+
 // The reference extension's own fused-linear domain (bfht_linear_small.hip):
 // float32 / float16 / bfloat16 latents, B <= 2^14, B % in_features == 0, so no
 // row straddles two blocks.  Blocks generated in float32 into LDS and

@@ -26,7 +26,9 @@
 // block per 8-token tile and requires block_size % in_features == 0).
 #include "bfht_mfma_chain.h"
 
+#include <climits>
 #include <type_traits>
+#include <vector>
 
 namespace lwl {
 namespace {
@@ -169,27 +171,17 @@ __global__ __launch_bounds__(256) void bfht_linear_tile_x(const __bf16* __restri
   }
 }
 
+// One work item of the fused linear: generated blocks tile*KB .. tile*KB + KB - 1
+// against token split `split` of token_split (every thread of the workgroup
+// calls it; `lds` is the workgroup's kLinearLdsBytes).  `pitch` table rows
+// (>= the tile's output rows; 16*NT when that fits in the LDS, else exact and
+// the last row tile masked on read).
 template <int L, int NT, bool kTiled, int KB, int KG = kGroup, int KD = kDepth>
-__global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __restrict__ x,
-                                                               const __bf16* __restrict__ latent,
-                                                               __bf16* __restrict__ out,
-                                                               float* __restrict__ partial, int tokens,
-                                                               int in_f, int out_f, int n, uint32_t seed32,
-                                                               float scale, int token_split, int64_t nblocks,
-                                                               int pitch) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kLinearLdsBytes];
-  // XCD-aware work order: workgroup i runs on XCD i % 8, and work item
-  // p = split * ntiles + tile (split-major) goes to XCD p / per_xcd, so each
-  // XCD's L2 holds the x rows of one or two token splits instead of all of x.
-  const int64_t ntiles = (nblocks + KB - 1) / KB;
-  const int64_t nwork = ntiles * token_split;
-  const int64_t per_xcd = (nwork + kXcds - 1) / kXcds;
-  const int64_t p = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-  if (p >= nwork) return;  // uniform: the grid is rounded up to whole XCD rows
-  const int split = (int)(p / ntiles);
-  const int64_t tile = p - (int64_t)split * ntiles;  // blocks tile*KB .. tile*KB + KB - 1
-  // `pitch` table rows (>= the tile's output rows; 16*NT when that
-  // fits in the LDS, else exact and the last row tile masked on read)
+__device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const __bf16* __restrict__ latent,
+                                            __bf16* __restrict__ out, float* __restrict__ partial, int tokens,
+                                            int in_f, int out_f, int n, uint32_t seed32, float scale,
+                                            int token_split, int64_t nblocks, int pitch, int split, int64_t tile,
+                                            unsigned char* lds) {
 
   const int64_t size = (int64_t)in_f * out_f;
   const int64_t g0 = tile * KB * kB;                          // first flat position
@@ -434,6 +426,29 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
     for (int tg = rest0 + KG * wave; tg < tt1; tg += KG * kWaves) pass(std::integral_constant<int, KG>{}, tg, tt1);
   }
 }
+template <int L, int NT, bool kTiled, int KB, int KG = kGroup, int KD = kDepth>
+__global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __restrict__ x,
+                                                               const __bf16* __restrict__ latent,
+                                                               __bf16* __restrict__ out,
+                                                               float* __restrict__ partial, int tokens,
+                                                               int in_f, int out_f, int n, uint32_t seed32,
+                                                               float scale, int token_split, int64_t nblocks,
+                                                               int pitch) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLinearLdsBytes];
+  // XCD-aware work order: workgroup i runs on XCD i % 8, and work item
+  // p = split * ntiles + tile (split-major) goes to XCD p / per_xcd, so each
+  // XCD's L2 holds the x rows of one or two token splits instead of all of x.
+  const int64_t ntiles = (nblocks + KB - 1) / KB;
+  const int64_t nwork = ntiles * token_split;
+  const int64_t per_xcd = (nwork + kXcds - 1) / kXcds;
+  const int64_t p = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (p >= nwork) return;  // uniform: the grid is rounded up to whole XCD rows
+  const int split = (int)(p / ntiles);
+  const int64_t tile = p - (int64_t)split * ntiles;
+  linear_item<L, NT, kTiled, KB, KG, KD>(x, latent, out, partial, tokens, in_f, out_f, n, seed32, scale,
+                                         token_split, nblocks, pitch, split, tile, lds);
+}
+
 // Rows straddling tiles b-1 and b: out[t][o] = scale * (last(b-1)[t] + first(b)[t]).
 __global__ __launch_bounds__(256) void bfht_linear_combine(const float* __restrict__ partial,
                                                            __bf16* __restrict__ out, int tokens, int in_f,
@@ -447,6 +462,41 @@ __global__ __launch_bounds__(256) void bfht_linear_combine(const float* __restri
   const int o = (int)(g0 / in_f);
   const float v = partial[((b - 1) * 2 + 1) * (int64_t)tokens + t] + partial[(b * 2) * (int64_t)tokens + t];
   store_bf16_through(out + (int64_t)t * out_f + o, scale * v);
+}
+
+// Several matrices in one launch (the decode case: each matrix has a few dozen
+// generated blocks, far fewer than the 256 CUs): workgroup i serves job j with
+// prefix[j] <= i < prefix[j + 1], work item i - prefix[j] = split * nblocks +
+// block, as the single-matrix kernel's non-tiled, one-block-per-workgroup path.
+template <int L, int NT>
+__global__ __launch_bounds__(kThreads) void bfht_linear_mfma15_grouped(const LinearGroupTable g) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLinearLdsBytes];
+  const int j = group_job(g, (int)blockIdx.x);
+  const LinearGroupJob& jb = g.job[j];
+  const int64_t p = (int64_t)blockIdx.x - g.prefix[j];
+  const int split = (int)(p / jb.nblocks);
+  const int64_t tile = p - (int64_t)split * jb.nblocks;
+  linear_item<L, NT, false, 1>(jb.x, jb.latent, jb.out, jb.partial, jb.tokens, jb.in_f, jb.out_f, jb.n, jb.seed32,
+                               jb.scale, jb.token_split, jb.nblocks, jb.pitch, split, tile, lds);
+}
+
+// The straddling-row sums of every job of a grouped launch: workgroup i serves
+// job j with cprefix[j] <= i < cprefix[j + 1] (its block boundaries times its
+// 256-token chunks), with the arithmetic of bfht_linear_combine.
+__global__ __launch_bounds__(256) void bfht_linear_combine_grouped(const LinearGroupTable g) {
+  int j = 0;
+  while (j + 1 < g.count && (int)blockIdx.x >= g.cprefix[j + 1]) ++j;
+  const LinearGroupJob& jb = g.job[j];
+  const int chunks = (jb.tokens + 255) / 256;
+  const int q = (int)blockIdx.x - g.cprefix[j];
+  const int64_t b = q / chunks + 1;
+  const int t = (q - (q / chunks) * chunks) * 256 + (int)threadIdx.x;
+  if (t >= jb.tokens || b >= jb.nblocks) return;
+  const int64_t g0 = b * kB;
+  if (g0 % jb.in_f == 0) return;
+  const int o = (int)(g0 / jb.in_f);
+  const float v = jb.partial[((b - 1) * 2 + 1) * (int64_t)jb.tokens + t] + jb.partial[(b * 2) * (int64_t)jb.tokens + t];
+  store_bf16_through(jb.out + (int64_t)t * jb.out_f + o, jb.scale * v);
 }
 
 template <int L, bool kTiled, int KB>
@@ -503,7 +553,102 @@ hipError_t launch_linear_L(const LinearArgs& a, hipStream_t s) {
   return launch_linear_L<L, true>(a, (const __bf16*)tiled, partial, s);
 }
 
+template <int L>
+hipError_t launch_grouped_nt(const LinearGroupTable& g, int nt, hipStream_t s) {
+  const dim3 grid((unsigned)g.prefix[g.count]), block(mfma15::kThreads);
+  switch (nt) {
+    case 1: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 1>), grid, block, 0, s, g); break;
+    case 2: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 2>), grid, block, 0, s, g); break;
+    case 3: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 3>), grid, block, 0, s, g); break;
+    case 4: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 4>), grid, block, 0, s, g); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || g.cprefix[g.count] == 0) return e;
+  hipLaunchKernelGGL(bfht_linear_combine_grouped, dim3((unsigned)g.cprefix[g.count]), dim3(256), 0, s, g);
+  return hipGetLastError();
+}
+
+// One grouped launch (plus its combine) for jobs of one layer count and row-tile count.
+hipError_t launch_group_chunk(const LinearArgs* const* jobs, int count, hipStream_t s) {
+  LinearGroupTable g{};
+  g.count = count;
+  int64_t total = 0, min_tiles = INT64_MAX;
+  for (int i = 0; i < count; ++i) {
+    total += jobs[i]->nblocks_w;
+    const int64_t tt = (jobs[i]->tokens + kTokTile - 1) / kTokTile;
+    min_tiles = tt < min_tiles ? tt : min_tiles;
+  }
+  // one pass over every job's blocks fills the chip when there are >= 256 of
+  // them; otherwise split the tokens, as the single-matrix launch does
+  int64_t split = total >= 256 ? 1 : 256 / total;
+  if (split > min_tiles) split = min_tiles;
+  if (split < 1) split = 1;
+  int64_t wg = 0, cw = 0;
+  for (int i = 0; i < count; ++i) {
+    const LinearArgs& a = *jobs[i];
+    LinearGroupJob& jb = g.job[i];
+    jb.x = (const __bf16*)a.x;
+    jb.latent = (const __bf16*)a.latent;
+    jb.out = (__bf16*)a.out;
+    jb.partial = (float*)a.work;
+    jb.tokens = (int)a.tokens;
+    jb.in_f = (int)a.in_features;
+    jb.out_f = (int)a.out_features;
+    jb.n = (int)a.n;
+    jb.seed32 = a.seed32;
+    jb.scale = a.weight_scale;
+    jb.nblocks = (int)a.nblocks_w;
+    jb.pitch = linear_pitch(a.in_features, 1);
+    jb.token_split = (int)split;
+    g.prefix[i] = (int)wg;
+    g.cprefix[i] = (int)cw;
+    wg += a.nblocks_w * split;
+    cw += (a.nblocks_w - 1) * ((a.tokens + 255) / 256);
+  }
+  g.prefix[count] = (int)wg;
+  g.cprefix[count] = (int)cw;
+  const int nt = (int)linear_row_tiles(jobs[0]->in_features, 1);
+  switch (jobs[0]->layers) {
+    case 1: return launch_grouped_nt<1>(g, nt, s);
+    case 2: return launch_grouped_nt<2>(g, nt, s);
+    case 3: return launch_grouped_nt<3>(g, nt, s);
+  }
+  return hipErrorInvalidValue;
+}
+
 }  // namespace
+
+bool linear_groupable(const LinearArgs& a) {
+  return linear_applicable(a.dtype, a.log_block, a.in_features) && !linear_tiled(a);
+}
+
+hipError_t launch_linear_grouped(const LinearArgs* jobs, int64_t count, hipStream_t s) {
+  // bucket by (layers, row tiles), in job order; at most kLinearGroupMax per launch
+  std::vector<const LinearArgs*> bucket;
+  std::vector<bool> done((size_t)count, false);
+  for (int64_t i = 0; i < count; ++i) {
+    if (done[(size_t)i]) continue;
+    const int L = jobs[i].layers;
+    const int64_t nt = linear_row_tiles(jobs[i].in_features, 1);
+    bucket.clear();
+    for (int64_t k = i; k < count; ++k) {
+      if (done[(size_t)k] || jobs[k].layers != L || linear_row_tiles(jobs[k].in_features, 1) != nt) continue;
+      done[(size_t)k] = true;
+      bucket.push_back(&jobs[k]);
+      if ((int)bucket.size() == kLinearGroupMax) {
+        const hipError_t e = launch_group_chunk(bucket.data(), (int)bucket.size(), s);
+        if (e != hipSuccess) return e;
+        bucket.clear();
+      }
+    }
+    if (!bucket.empty()) {
+      const hipError_t e = launch_group_chunk(bucket.data(), (int)bucket.size(), s);
+      if (e != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
+}
 
 const bool kLinearKernelAvailable = true;
 

@@ -99,6 +99,47 @@ def linear_forward(x2d: torch.Tensor, latent: torch.Tensor, out_features: int, l
     return out
 
 
+def linear_forward_grouped(specs: list[tuple], outs: list[torch.Tensor] | None = None) -> list[torch.Tensor]:
+    """Many fused linears ``x @ (weight_scale * W)^T`` in few launches
+    (``lwl_bfht_linear_forward_grouped``); each result equals its own ``linear_forward`` call
+    bit for bit.  ``specs``: ``(x2d, latent, out_features, layers, seed, weight_scale)`` per
+    matrix, all of one dtype; ``outs``: optional preallocated ``[tokens, out_features]``
+    outputs."""
+    if not specs:
+        return []
+    dev = N.require_cuda(*[t for sp in specs for t in sp[:2]])
+    dtype = specs[0][0].dtype
+    code = N.dtype_code(dtype)
+    jobs, result, keep = [], [], []
+    for i, (x2d, latent, out_features, layers, seed, scale) in enumerate(specs):
+        x2d = x2d.contiguous()
+        latent = latent.contiguous()
+        if x2d.dtype != dtype or latent.dtype != dtype:
+            raise RuntimeError("grouped fused linear: every input and latent must have the same dtype")
+        tokens, in_features = x2d.shape
+        if outs is None:
+            out = torch.empty(tokens, int(out_features), dtype=dtype, device=dev)
+        else:
+            out = outs[i]
+            if out.shape != (tokens, int(out_features)) or out.dtype != dtype or not out.is_contiguous():
+                raise N.BlockFHTArgumentError(f"output {i} must be a contiguous [{tokens}, {out_features}] {dtype}")
+        j = N.LinearJob()
+        j.input, j.latent, j.out = x2d.data_ptr(), latent.data_ptr(), out.data_ptr()
+        j.tokens, j.in_features, j.latent_size = tokens, in_features, latent.numel()
+        j.out_features, j.layers, j.seed, j.weight_scale = int(out_features), int(layers), int(seed), float(scale)
+        jobs.append(j)
+        result.append(out)
+        keep += [x2d, latent]
+    arr = (N.LinearJob * len(jobs))(*jobs)
+    L = N.lib()
+    N.check(L.lwl_bfht_check_linear_jobs(code, arr, len(jobs)))
+    with _device_guard(dev):
+        ws_ptr, ws_size, ws = N.workspace(L.lwl_bfht_linear_forward_grouped_workspace_size(code, arr, len(jobs)), dev)
+        N.check(L.lwl_bfht_linear_forward_grouped(code, arr, len(jobs), ws_ptr, ws_size, N.stream_ptr(dev)))
+    del ws, keep
+    return result
+
+
 def linear_backward_latent_supported(in_features: int, out_features: int, latent: torch.Tensor,
                                      x: torch.Tensor, grad: torch.Tensor) -> bool:
     """Whether the fused latent gradient takes this shape (else grad_weight is formed in HBM)."""

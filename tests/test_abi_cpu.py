@@ -328,3 +328,37 @@ def test_fht_mix_validation(args, code, msg):
     rc = N.lib().lwl_fht_check_mix(*args)
     assert rc == code
     assert msg in N.lib().lwl_last_error().decode()
+
+
+def linear_job(tokens, in_f, out_f, n, layers=3, out=0x100000, inp=0x10000, lat=0x20000):
+    j = N.LinearJob()
+    j.input, j.latent, j.out = inp, lat, out
+    j.tokens, j.in_features, j.latent_size, j.out_features = tokens, in_f, n, out_f
+    j.layers, j.seed, j.weight_scale = layers, 1, 1.0
+    return j
+
+
+def test_linear_jobs_validation():
+    lib = N.lib()
+    ok = [linear_job(1, 768, 2304, 32768, out=0x100000), linear_job(1, 3072, 768, 32768, out=0x200000)]
+    arr = (N.LinearJob * 2)(*ok)
+    assert lib.lwl_bfht_check_linear_jobs(2, arr, 2) == N.LWL_OK
+    # overlapping outputs (the second starts inside the first's 2304 bf16 values)
+    arr = (N.LinearJob * 2)(linear_job(1, 768, 2304, 32768, out=0x100000), linear_job(1, 768, 768, 32768, out=0x100010))
+    assert lib.lwl_bfht_check_linear_jobs(2, arr, 2) == N.LWL_ERR_INVALID
+    assert "overlapping" in lib.lwl_last_error().decode()
+    # a job outside every fused kernel names its index
+    arr = (N.LinearJob * 2)(linear_job(1, 768, 2304, 32768), linear_job(1, 768, 64, 16384, out=0x200000))
+    assert lib.lwl_bfht_check_linear_jobs(2, arr, 2) == N.LWL_ERR_UNSUPPORTED
+    assert lib.lwl_last_error().decode().startswith("job 1:")
+    # workspace: the grouped jobs' (fewer than 256 tokens) side by side, plus the largest of the jobs
+    # that run as single calls one after another (300 and 400 tokens: the tiled-x path)
+    one = lib.lwl_bfht_linear_forward_workspace_size(300, 1024, 300, 32768)
+    big = lib.lwl_bfht_linear_forward_workspace_size(400, 1024, 300, 32768)
+    two = lib.lwl_bfht_linear_forward_workspace_size(17, 768, 768, 32768)
+    three = lib.lwl_bfht_linear_forward_workspace_size(5, 3072, 768, 32768)
+    arr = (N.LinearJob * 4)(linear_job(300, 1024, 300, 32768), linear_job(17, 768, 768, 32768, out=0x9000000),
+                            linear_job(400, 1024, 300, 32768, out=0x20000000),
+                            linear_job(5, 3072, 768, 32768, out=0x30000000))
+    assert one < big
+    assert lib.lwl_bfht_linear_forward_grouped_workspace_size(2, arr, 4) == two + three + big
