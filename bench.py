@@ -329,6 +329,34 @@ def extra_configs(abi, steps, warmup, only):
                 lin[f"{inf}x{outf}"] = {"error": f"{type(exc).__name__}: {exc}"}
         res["c4_linear"] = lin
 
+    # the reference extension's own fused-linear domain (block <= 2^14, block % in == 0): its profiling
+    # case (scripts/profile_fused_once.py: 1024 -> 4096, float16, latent 16384, layers 2, scale 0.5) at one
+    # token and at 4096, fused (W generated into LDS in float32, never stored) vs a dense float16 GEMM on
+    # the materialized weight
+    if want("c4_ref_domain"):
+        from latent_weight_lab_amd import block_fht_slice
+
+        rows = {}
+        for dt, tag in ((torch.float16, "f16"), (torch.float32, "f32")):
+            for tokens in (1, 4096):
+                try:
+                    torch.manual_seed(0)
+                    latent = torch.randn(16384).to(dt).cuda()
+                    x = torch.randn(tokens, 1024, generator=torch.Generator().manual_seed(1)).to(dt).cuda()
+                    out = torch.empty(tokens, 4096, dtype=dt, device="cuda")
+                    ws = abi.linear_ws(tokens, 1024, 4096, 16384, "cuda")
+                    with torch.no_grad():
+                        w = block_fht_slice(latent, 1024 * 4096, 2, 123, 0, 1024 * 4096).view(4096, 1024) * 0.5
+                    fused = time_graph(torch, lambda: abi.linear(x, latent, out, 4096, 2, 123, 0.5, ws), 20, 3)
+                    dense = time_graph(torch, lambda: torch.nn.functional.linear(x, w), 20, 3)
+                    rows[f"{tag}_tokens_{tokens}"] = {"fused_ms": round(fused * 1e3, 4), "dense_gemm_ms": round(dense * 1e3, 4),
+                                                      "fused_over_dense": fused / dense,
+                                                      "fused_TFLOPs": 2 * tokens * 1024 * 4096 / fused / 1e12}
+                    del latent, x, out, ws, w
+                except Exception as exc:  # noqa: BLE001
+                    rows[f"{tag}_tokens_{tokens}"] = {"error": f"{type(exc).__name__}: {exc}"}
+        res["c4_ref_domain"] = rows
+
     # config 4 training step, latent gradient: fused (grad_weight formed per block on chip) vs
     # grad_weight = g^T x on hipBLASLt in HBM followed by the generator backward
     if want("c4_linear_bwd"):

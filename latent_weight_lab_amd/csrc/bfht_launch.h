@@ -85,7 +85,7 @@ hipError_t launch_linear(const LinearArgs& a, hipStream_t s);
 // up to kLinearGroupMax jobs, each job exactly as its single launch computes it
 // (same work items, same partial-row sums), with its own `work` (partial rows,
 // linear_workspace_bytes).
-constexpr int kLinearGroupMax = 32;
+constexpr int kLinearGroupMax = 48;  // the table stays below the 4 KiB of kernel arguments
 struct LinearGroupJob {
   const __bf16* x;
   const __bf16* latent;
@@ -102,6 +102,7 @@ struct LinearGroupTable {  // passed by value; prefix counts workgroups, cprefix
   int32_t cprefix[kLinearGroupMax + 1];
   LinearGroupJob job[kLinearGroupMax];
 };
+static_assert(sizeof(LinearGroupTable) <= 4000, "grouped linear table fits the kernel arguments");
 bool linear_groupable(const LinearArgs& a);
 hipError_t launch_linear_grouped(const LinearArgs* jobs, int64_t count, hipStream_t s);
 

@@ -26,6 +26,7 @@
 // block per 8-token tile and requires block_size % in_features == 0).
 #include "bfht_mfma_chain.h"
 
+#include <algorithm>
 #include <climits>
 #include <type_traits>
 #include <vector>
@@ -569,8 +570,20 @@ hipError_t launch_grouped_nt(const LinearGroupTable& g, int nt, hipStream_t s) {
   return hipGetLastError();
 }
 
-// One grouped launch (plus its combine) for jobs of one layer count and row-tile count.
-hipError_t launch_group_chunk(const LinearArgs* const* jobs, int count, hipStream_t s) {
+// Whether a job's k-major table can be read as `nt` row tiles: the contraction
+// reads rows up to 16 nt - 1 of every k chunk (rows past the job's own are
+// never stored), so the last chunk's reads reach 16 nt - pitch rows past its
+// table; they must stay inside the workgroup's LDS.
+bool table_reads_fit(const LinearArgs& a, int nt) {
+  const int64_t pitch = linear_pitch(a.in_features, 1);
+  const int64_t steps = linear_steps(a.in_features);
+  const int64_t last = (4 * steps - 1) * pitch + (16 * nt - 1) + (4 * steps - 1) / 4;  // highest slot read
+  return (last + 1) * 16 <= kLinearLdsBytes;
+}
+
+// One grouped launch (plus its combine) for jobs of one layer count, read as
+// `nt` row tiles (the largest of the jobs').
+hipError_t launch_group_chunk(const LinearArgs* const* jobs, int count, int nt, hipStream_t s) {
   LinearGroupTable g{};
   g.count = count;
   int64_t total = 0, min_tiles = INT64_MAX;
@@ -608,7 +621,6 @@ hipError_t launch_group_chunk(const LinearArgs* const* jobs, int count, hipStrea
   }
   g.prefix[count] = (int)wg;
   g.cprefix[count] = (int)cw;
-  const int nt = (int)linear_row_tiles(jobs[0]->in_features, 1);
   switch (jobs[0]->layers) {
     case 1: return launch_grouped_nt<1>(g, nt, s);
     case 2: return launch_grouped_nt<2>(g, nt, s);
@@ -624,30 +636,47 @@ bool linear_groupable(const LinearArgs& a) {
 }
 
 hipError_t launch_linear_grouped(const LinearArgs* jobs, int64_t count, hipStream_t s) {
-  // bucket by (layers, row tiles), in job order; at most kLinearGroupMax per launch
-  std::vector<const LinearArgs*> bucket;
+  // Buckets in job order: one per layer count, read as the largest row-tile
+  // count among the pending jobs of that layer count (the extra row tiles of
+  // smaller jobs cost MFMAs on rows that are never stored, little at the batch
+  // sizes grouped here); jobs whose table cannot be read that wide wait for a
+  // later bucket, and a bucket that would be empty falls back to the first
+  // pending job's own row-tile count (which its single launch reads, so it
+  // fits).  Every round launches at least one job.  At most kLinearGroupMax
+  // jobs per launch.
   std::vector<bool> done((size_t)count, false);
-  for (int64_t i = 0; i < count; ++i) {
-    if (done[(size_t)i]) continue;
+  std::vector<const LinearArgs*> bucket;
+  auto tiles = [&](int64_t k) { return (int)linear_row_tiles(jobs[k].in_features, 1); };
+  for (;;) {
+    int64_t i = 0;
+    while (i < count && done[(size_t)i]) ++i;
+    if (i == count) return hipSuccess;
     const int L = jobs[i].layers;
-    const int64_t nt = linear_row_tiles(jobs[i].in_features, 1);
+    int nt = 0;
+    for (int64_t k = i; k < count; ++k)
+      if (!done[(size_t)k] && jobs[k].layers == L) nt = std::max(nt, tiles(k));
+    auto take = [&](int64_t k, int w) {
+      return !done[(size_t)k] && jobs[k].layers == L && tiles(k) <= w && table_reads_fit(jobs[k], w);
+    };
+    bool any = false;
+    for (int64_t k = i; k < count && !any; ++k) any = take(k, nt);
+    if (!any) nt = tiles(i);
     bucket.clear();
     for (int64_t k = i; k < count; ++k) {
-      if (done[(size_t)k] || jobs[k].layers != L || linear_row_tiles(jobs[k].in_features, 1) != nt) continue;
+      if (!take(k, nt) && !(k == i && !any)) continue;
       done[(size_t)k] = true;
       bucket.push_back(&jobs[k]);
       if ((int)bucket.size() == kLinearGroupMax) {
-        const hipError_t e = launch_group_chunk(bucket.data(), (int)bucket.size(), s);
+        const hipError_t e = launch_group_chunk(bucket.data(), (int)bucket.size(), nt, s);
         if (e != hipSuccess) return e;
         bucket.clear();
       }
     }
     if (!bucket.empty()) {
-      const hipError_t e = launch_group_chunk(bucket.data(), (int)bucket.size(), s);
+      const hipError_t e = launch_group_chunk(bucket.data(), (int)bucket.size(), nt, s);
       if (e != hipSuccess) return e;
     }
   }
-  return hipSuccess;
 }
 
 const bool kLinearKernelAvailable = true;
