@@ -60,10 +60,13 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTiles = 4;
 constexpr int kChunks = kB / 8;  // 16-byte chunks of 8 bf16 in one block
-// Exchange buffers: 4096 16-byte chunks, stored as two 32 KiB halves (bytes
-// 0-7 of every chunk, then bytes 8-15), so that the 8-byte writes and reads
-// of consecutive lanes cover consecutive LDS bytes (any gap between lanes
-// costs LDS cycles in proportion); two buffers back to back (128 KiB).
+// Exchange buffers: 4096 16-byte chunks of 8 bf16, stored by 8-byte halves in
+// groups of 32 chunks: 256 bytes of the groups' low halves, then 256 bytes of
+// their high halves (exchange_slot).  The 8-byte writes and reads of 32
+// consecutive lanes then cover 256 consecutive LDS bytes (any gap between
+// lanes costs LDS cycles in proportion), and the two halves of a chunk sit 256
+// bytes apart, so one ds_read2_b64 fetches a whole MFMA operand into
+// consecutive registers; two buffers back to back (128 KiB).
 constexpr int kXBufBytes = kChunks * 16;
 constexpr int kLdsBytes = 2 * kXBufBytes;
 // Sign-word table after the exchange buffers: the words of sign layers 1..L
@@ -189,7 +192,7 @@ struct Ctx {
   uint32_t base0, base1;  // sign-word index bases in S0 and S1
   uint32_t gw0, gw1;      // 0xc2b2ae35 * (base + 1): the word term of the hash input
   int p4;                 // position bit p4 of this wave in S1
-  int wid, rid;           // exchange chunk-id bases (write / read side)
+  int wid, rid;           // exchange slot bases (write / read side)
 };
 
 __device__ __forceinline__ Ctx make_ctx(uint32_t seed32, int64_t block) {
@@ -206,8 +209,13 @@ __device__ __forceinline__ Ctx make_ctx(uint32_t seed32, int64_t block) {
   x.gw0 = 0xc2b2ae35u * (x.base0 + 1u);
   x.gw1 = 0xc2b2ae35u * (x.base1 + 1u);
   x.p4 = x.wave & 1;
-  x.wid = x.lane32 + (x.l5 << 8) + ((x.wave >> 1) << 10);
-  x.rid = x.lane32 + (x.wave << 7) + (x.l5 << 10);
+  // exchange_slot of the chunk ids below, without their r / (t, c) terms
+  x.wid = x.lane32 + ((x.wave & 1) << 5) + (x.l5 << 9) + ((x.wave >> 1) << 11);
+  x.rid = x.lane32 + (x.wave << 8) + (x.l5 << 11);
+  // Opaque to the compiler: knowing their range, it ORs a buffer's base (64
+  // KiB) into every address instead of adding it once and folding the rest
+  // into the LDS instructions' offset fields.
+  asm("" : "+v"(x.wid), "+v"(x.rid));
   return x;
 }
 
@@ -277,30 +285,36 @@ __device__ __forceinline__ void stage_rows(f32x16 (&acc)[kTiles], const u32x4 (&
 // 8-byte half (its 4 tiles at register r), the half being wave bit 0:
 //   write: id = lane32 + (r&7)<<5 + l5<<8 + (r>>3)<<9 + (wave>>1)<<10, half = wave & 1
 //   read:  id = lane32 + t<<5 + wave<<7 + l5<<10 + c<<11 (whole chunk = B operand)
-// Half h of chunk id is 8-byte slot h * kChunks + id.
+// Half h of chunk id is 8-byte slot exchange_slot(id, h).
+__host__ __device__ constexpr int exchange_slot(int id, int h) { return (id & 31) + (h << 5) + ((id >> 5) << 6); }
+
 __device__ __forceinline__ void exchange_write(const f32x16 (&acc)[kTiles], u32x2* xbuf, const Ctx& x) {
-  u32x2* half = xbuf + (x.wave & 1) * kChunks + x.wid;
+  u32x2* half = xbuf + x.wid;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     u32x2 v;
     v[0] = pk(acc[0][r], acc[1][r]);
     v[1] = pk(acc[2][r], acc[3][r]);
-    half[((r & 7) << 5) + ((r >> 3) << 9)] = v;
+    half[((r & 7) << 6) + ((r >> 3) << 10)] = v;
   }
 }
 
 __device__ __forceinline__ void exchange_read_stage_c(f32x16 (&acc)[kTiles], const u32x4 (&h)[2],
                                                       const u32x2* xbuf, const Ctx& x) {
   u32x4 b[kTiles][2];
-  const u32x2* lo_half = xbuf + x.rid;
+  const u32x2* rd = xbuf + x.rid;
 #pragma unroll
   for (int t = 0; t < kTiles; ++t)
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const int id = (t << 5) + (c << 11);
-      const u32x2 lo = lo_half[id], hi = lo_half[kChunks + id];
+      const int s = (t << 6) + (c << 12);
+      const u32x2 lo = rd[s], hi = rd[s + 32];
       b[t][c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
+  // All eight reads in flight before the first MFMA: left to itself the
+  // compiler reuses one register set, and each read then waits out the LDS
+  // latency alone.
+  __builtin_amdgcn_sched_barrier(0);
   const f32x16 zero = {};
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) {
@@ -308,6 +322,28 @@ __device__ __forceinline__ void exchange_read_stage_c(f32x16 (&acc)[kTiles], con
     acc[t] = mfma(h[1], b[t][1], d);
   }
 }
+
+// The slot bases above, checked against the chunk-id formulas.
+constexpr bool exchange_slots_consistent() {
+  for (int lane = 0; lane < 64; ++lane)
+    for (int wave = 0; wave < kWaves; ++wave) {
+      const int lane32 = lane & 31, l5 = lane >> 5;
+      const int wid = lane32 + ((wave & 1) << 5) + (l5 << 9) + ((wave >> 1) << 11);
+      const int rid = lane32 + (wave << 8) + (l5 << 11);
+      for (int r = 0; r < 16; ++r) {
+        const int id = lane32 + ((r & 7) << 5) + (l5 << 8) + ((r >> 3) << 9) + ((wave >> 1) << 10);
+        if (wid + ((r & 7) << 6) + ((r >> 3) << 10) != exchange_slot(id, wave & 1)) return false;
+      }
+      for (int t = 0; t < kTiles; ++t)
+        for (int c = 0; c < 2; ++c) {
+          const int id = lane32 + (t << 5) + (wave << 7) + (l5 << 10) + (c << 11);
+          const int s = rid + (t << 6) + (c << 12);
+          if (s != exchange_slot(id, 0) || s + 32 != exchange_slot(id, 1)) return false;
+        }
+    }
+  return true;
+}
+static_assert(exchange_slots_consistent(), "exchange slot bases disagree with the chunk layout");
 
 // Fills the sign-word table (bytes kLdsBytes.. of the chain's LDS): slot j - 1
 // holds the 1024 inverted words of sign layer sign_layer(j), j = 1..L, two per
@@ -337,9 +373,11 @@ __device__ __forceinline__ void fill_words(const Ctx& x, uint32_t* wtab, SignLay
 template <bool kOdd, bool kPermuted>
 __device__ __forceinline__ void read_words(const Ctx& x, const uint32_t* wtab, int slot, uint32_t (&nw)[4]) {
   const uint32_t* t = wtab + slot * kWordsPerLayer;
+  uint32_t base = kOdd ? x.base1 : x.base0;
+  asm("" : "+v"(base));  // as the exchange bases: table offsets fold into the reads
 #pragma unroll
   for (int s = 0; s < (kOdd ? 4 : 2); ++s) {
-    const uint32_t v = kOdd ? t[x.base1 + (s << 8)] : t[x.base0 + (s << 6)];
+    const uint32_t v = t[base + (s << (kOdd ? 8 : 6))];
     nw[s] = (kOdd && kPermuted) ? (v >> (8 * x.p4)) : v;
   }
   if (!kOdd) nw[2] = nw[3] = 0;
