@@ -133,11 +133,16 @@ int lwl_bfht_backward_noalloc(const void* grad_out, int dtype, int64_t latent_si
  * <= B works (rows may straddle blocks; partial rows are summed in a fixed
  * order through the workspace).  B <= 2^15.
  *
- * Takes bfloat16 latents of block 2^15 with in_features % 8 == 0 and
- * 528 <= in_features <= 5120: the generated weight is rounded to bf16 and the
- * contraction runs on MFMA with float32 accumulation.  Other shapes return
- * LWL_ERR_UNSUPPORTED and the caller generates the weight and calls a GEMM,
- * as the reference's fallback does (block_fht.py:263-288).
+ * Two domains:
+ *  (a) bfloat16 latents of block 2^15 with in_features % 8 == 0 and
+ *      528 <= in_features <= 5120: the generated weight is rounded to bf16 and
+ *      the contraction runs on MFMA with float32 accumulation;
+ *  (b) the reference extension's own domain (gate block_fht.py:263-273):
+ *      float32, float16 or bfloat16, block <= 2^14, block % in_features == 0:
+ *      the weight is generated in float32 and contracted in float32, as the
+ *      reference's kernel does; no workspace.
+ * Other shapes return LWL_ERR_UNSUPPORTED and the caller generates the weight
+ * and calls a GEMM, as the reference's fallback does (block_fht.py:263-288).
  */
 size_t lwl_bfht_linear_forward_workspace_size(int64_t tokens, int64_t in_features,
                                               int64_t out_features, int64_t latent_size);
@@ -150,6 +155,40 @@ int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, in
 int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features,
                                   int64_t latent_size, int64_t out_features, int64_t layers);
 
+/* ---------------------------------------------------------------- fused linear with epilogue
+ * Replaces BlockFHTLinear.forward_fused's tail (reference block_fht.py:493-500:
+ * the modulation term, the residual base and the bias, each a separate torch op
+ * after ext.linear_forward) with the store of the fused kernels:
+ *
+ *   out[t, o] = base[t, o] + weight_scale * sum_i input[t, i] * W[o, i]
+ *             + row_sum_scale * (*row_sum_coef) * sum_i input[t, i] + bias[o]
+ *
+ * summed in float32 in that order and rounded once to `dtype` (the reference
+ * rounds after each op, so results agree to the I/O type's rounding).  Terms
+ * whose pointer is NULL are left out; bias [out_features] and base
+ * [tokens, out_features] (the residual base's input @ base_weight^T) are in
+ * `dtype`; row_sum_coef is one float32 on the device (the module's
+ * modulation_alpha * offset, read by the kernel, so the caller never waits on
+ * it).  With epilogue NULL this is lwl_bfht_linear_forward, bit for bit.  Same
+ * domains and checks; the workspace (query with the same arguments) adds
+ * tokens float32 row sums when row_sum_coef is set.
+ */
+typedef struct lwl_bfht_linear_epilogue {
+  const void* bias;          /* [out_features], dtype, or NULL */
+  const void* base;          /* [tokens, out_features], dtype, or NULL */
+  const float* row_sum_coef; /* one float32 on the device, or NULL */
+  double row_sum_scale;      /* host factor of the row-sum term */
+} lwl_bfht_linear_epilogue;
+
+size_t lwl_bfht_linear_forward_ex_workspace_size(int dtype, int64_t tokens, int64_t in_features,
+                                                 int64_t out_features, int64_t latent_size,
+                                                 const lwl_bfht_linear_epilogue* epilogue);
+int lwl_bfht_linear_forward_ex(const void* input, const void* latent, int dtype, int64_t tokens,
+                               int64_t in_features, int64_t latent_size, int64_t out_features,
+                               int64_t layers, int64_t seed, double weight_scale,
+                               const lwl_bfht_linear_epilogue* epilogue, void* out, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- fused linear, grouped
  * Several lwl_bfht_linear_forward calls in few launches (no reference
  * counterpart: the reference calls ext.linear_forward once per matrix,
@@ -158,9 +197,11 @@ int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features
  * its own lwl_bfht_linear_forward call bit for bit.  At decode batch sizes a
  * GPT-2 matrix has 18..72 generated blocks, so one matrix per launch leaves
  * most of the chip idle; jobs the bf16 matrix-core kernel takes with fewer
- * than 256 tokens run together, one launch per (layers, row tiles per block)
- * class of up to 32 jobs; other jobs run as their single calls.  All jobs
- * share `dtype`; outputs must not overlap; inputs and latents may be shared.
+ * than 256 tokens run together, one launch per layer count for up to 48 jobs;
+ * other jobs run as their single calls.  All jobs share `dtype`; outputs must
+ * not overlap; inputs and latents may be shared.  A job's `epilogue` (NULL:
+ * none) is that of lwl_bfht_linear_forward_ex; jobs whose epilogue has only a
+ * bias still run grouped, jobs with a base or a row-sum term as single calls.
  * Workspace (query with the same jobs): the grouped jobs' own workspaces side
  * by side, plus the largest workspace of the jobs that run as single calls
  * (those run one after another on the stream and share it).
@@ -176,6 +217,7 @@ typedef struct lwl_bfht_linear_job {
   int64_t layers;
   int64_t seed;
   double weight_scale;
+  const lwl_bfht_linear_epilogue* epilogue; /* or NULL */
 } lwl_bfht_linear_job;
 
 /* Host-only check of `count` jobs (each as lwl_bfht_check_linear_forward, plus disjoint outputs). */

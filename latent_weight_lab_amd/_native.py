@@ -50,6 +50,17 @@ class WeightJob(ctypes.Structure):
     ]
 
 
+class LinearEpilogue(ctypes.Structure):
+    """``lwl_bfht_linear_epilogue``: out = base + weight_scale * x @ W^T
+    + row_sum_scale * (*row_sum_coef) * x.sum(-1) + bias, one rounding."""
+    _fields_ = [
+        ("bias", ctypes.c_void_p),
+        ("base", ctypes.c_void_p),
+        ("row_sum_coef", ctypes.c_void_p),
+        ("row_sum_scale", ctypes.c_double),
+    ]
+
+
 class LinearJob(ctypes.Structure):
     """``lwl_bfht_linear_job``: one matrix of a grouped fused-linear call."""
     _fields_ = [
@@ -63,6 +74,7 @@ class LinearJob(ctypes.Structure):
         ("layers", ctypes.c_int64),
         ("seed", ctypes.c_int64),
         ("weight_scale", ctypes.c_double),
+        ("epilogue", ctypes.POINTER(LinearEpilogue)),
     ]
 
 
@@ -86,6 +98,7 @@ def _bind(lib) -> None:
     dbl, u32p = ctypes.c_double, ctypes.POINTER(ctypes.c_uint32)
     jobp = ctypes.POINTER(WeightJob)
     ljobp = ctypes.POINTER(LinearJob)
+    epip = ctypes.POINTER(LinearEpilogue)
     sigs = {
         "lwl_last_error": (ctypes.c_char_p, []),
         "lwl_abi_version": (i32, []),
@@ -98,6 +111,8 @@ def _bind(lib) -> None:
         "lwl_bfht_linear_forward_workspace_size": (sz, [i64, i64, i64, i64]),
         "lwl_bfht_linear_forward": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, dbl, vp, vp, sz, vp]),
         "lwl_bfht_check_linear_forward": (i32, [i32, i64, i64, i64, i64, i64]),
+        "lwl_bfht_linear_forward_ex_workspace_size": (sz, [i32, i64, i64, i64, i64, epip]),
+        "lwl_bfht_linear_forward_ex": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, dbl, epip, vp, vp, sz, vp]),
         "lwl_bfht_check_linear_jobs": (i32, [i32, ljobp, i64]),
         "lwl_bfht_linear_forward_grouped_workspace_size": (sz, [i32, ljobp, i64]),
         "lwl_bfht_linear_forward_grouped": (i32, [i32, ljobp, i64, vp, sz, vp]),

@@ -361,14 +361,20 @@ class BlockFHTLinear(nn.Module):
                                        self.fused_latent_grad)
 
     def forward_fused(self, input: torch.Tensor, weight_scale: float = 1.0) -> torch.Tensor:
-        """Inference forward (reference ``block_fht.py:482-501``): the fused kernel where it
-        applies (W never stored), else W generated once and one GEMM that also adds the
-        bias when no modulation or residual term comes between; otherwise the reference's
-        sequence of terms."""
+        """Inference forward (reference ``block_fht.py:482-501``).  Where a fused kernel takes
+        the shape and no gradient is recorded: one fused launch whose stores also add the
+        modulation term, the residual base and the bias (``lwl_bfht_linear_forward_ex``; W
+        never stored, one rounding to the output dtype instead of one per term).  Recording
+        gradients: the fused (or generated) linear with the reference's sequence of terms
+        after it, the bias in the GEMM's epilogue when nothing comes between."""
         if self.output_gain is not None or self.input_gain is not None or self.spectral_core is not None:
             return F.linear(input, self.weight.to(dtype=input.dtype), self.bias)
         g = self.generator
         scale = weight_scale * self.weight_scale
+        fused = self._fused_epilogue_args(input, scale)
+        if fused is not None:
+            flat, args, kwargs = fused
+            return ops.linear_forward(flat, *args, **kwargs).reshape(*input.shape[:-1], self.out_features)
         if self.modulation_alpha == 0.0 and self.residual_base_weight is None:
             # the bias rides in the GEMM's epilogue
             return _generated_linear(input, g.latent, self.out_features, g.layers, g.seed, scale, self.bias, True)
@@ -382,6 +388,39 @@ class BlockFHTLinear(nn.Module):
         if self.bias is not None:
             out = out + self.bias
         return out
+
+    def _fused_epilogue_args(self, input: torch.Tensor, scale: float):
+        """``(flat input, ops.linear_forward positional args, epilogue kwargs)`` of
+        ``forward_fused`` as one fused launch, or None where that route does not apply
+        (gradients recorded, no fused kernel for the shape, a bias of another dtype).
+        The terms follow the reference's tail (``block_fht.py:493-500``): with a residual
+        base, ``out = base + s * (x W'^T + m * x.sum(-1))`` (s = residual_base_scale,
+        folded into weight_scale and the row-sum factor), then ``+ bias``; m is the
+        modulation rounded to the output dtype, as the reference rounds it."""
+        g = self.generator
+        if input.dim() < 2 or not (input.is_cuda and g.latent.is_cuda):
+            return None
+        bias = self.bias
+        if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (g.latent, input, bias)):
+            return None
+        flat = input.reshape(-1, self.in_features)
+        if not ops.linear_supported(self.in_features, self.out_features, g.latent, flat):
+            return None
+        if bias is not None and bias.dtype != flat.dtype:
+            return None
+        kwargs = {}
+        if bias is not None:
+            kwargs["bias"] = bias.detach()
+        out_scale = 1.0
+        if self.residual_base_weight is not None:
+            base_weight = self.residual_base_weight.to(device=flat.device, dtype=flat.dtype)
+            kwargs["base"] = F.linear(flat, base_weight)
+            out_scale = self.residual_base_scale
+        if self.modulation_alpha != 0.0:
+            kwargs["row_sum_coef"] = (self.modulation_alpha * self._modulation_offset()).detach().to(dtype=flat.dtype)
+            kwargs["row_sum_scale"] = out_scale
+        args = (g.latent, self.out_features, g.layers, g.seed, scale * out_scale)
+        return flat, args, kwargs
 
     def materialize_weight_cache(self, dtype: torch.dtype | None = None) -> None:
         """Reference ``block_fht.py:503-512``."""
@@ -447,36 +486,31 @@ class BlockFHTLinear(nn.Module):
 
 def forward_fused_grouped(modules: list["BlockFHTLinear"], inputs: list[torch.Tensor],
                           weight_scale: float = 1.0) -> list[torch.Tensor]:
-    """``[m.forward_fused(x, weight_scale) for m, x in zip(modules, inputs)]`` with every
-    plain module (no gains, spectral correction, modulation or residual base) in one
-    grouped fused-linear call (``lwl_bfht_linear_forward_grouped``): at decode batch
-    sizes one matrix fills a fraction of the chip, and the grouped launch runs all of
-    them together (not in the reference, which calls ``ext.linear_forward`` per matrix,
-    ``block_fht.py:274``).  Outputs equal the per-module calls bit for bit.  Modules the
-    fused kernels do not take, other modules, and calls that record gradients run
-    ``forward_fused`` one by one."""
+    """``[m.forward_fused(x, weight_scale) for m, x in zip(modules, inputs)]`` in one
+    grouped fused-linear call (``lwl_bfht_linear_forward_grouped``) for every module that
+    ``forward_fused`` would run as one fused launch: at decode batch sizes one matrix fills
+    a fraction of the chip, and the grouped launch runs all of them together (not in the
+    reference, which calls ``ext.linear_forward`` per matrix, ``block_fht.py:274``).  Each
+    job carries its module's epilogue (bias in the grouped kernels; modulation or residual
+    base make it a single launch inside the call).  Outputs equal the per-module calls bit
+    for bit.  Other modules, and calls that record gradients, run ``forward_fused`` one
+    by one."""
     if len(modules) != len(inputs):
         raise ValueError("modules and inputs must have the same length")
     outs: list[torch.Tensor | None] = [None] * len(modules)
     grouped, specs = [], []
     for i, (m, x) in enumerate(zip(modules, inputs)):
-        g = m.generator
-        plain = not (m._needs_dense_path() or m.modulation_alpha != 0.0)
-        flat = x.reshape(-1, m.in_features)
-        records = torch.is_grad_enabled() and (g.latent.requires_grad or x.requires_grad)
-        if (plain and not records and flat.is_cuda and g.latent.is_cuda
-                and ops.linear_supported(m.in_features, m.out_features, g.latent, flat)
-                and (not specs or flat.dtype == specs[0][0].dtype)):
+        direct = not (m.output_gain is not None or m.input_gain is not None or m.spectral_core is not None)
+        fused = m._fused_epilogue_args(x, weight_scale * m.weight_scale) if direct else None
+        if fused is not None and (not specs or fused[0].dtype == specs[0][0].dtype):
+            flat, args, kwargs = fused
             grouped.append(i)
-            specs.append((flat, g.latent, m.out_features, g.layers, g.seed, weight_scale * m.weight_scale))
+            specs.append((flat, *args, kwargs))
         else:
             outs[i] = m.forward_fused(x, weight_scale=weight_scale)
     if specs:
         for i, y in zip(grouped, ops.linear_forward_grouped(specs)):
-            m, x = modules[i], inputs[i]
-            if m.bias is not None:
-                y = y + m.bias
-            outs[i] = y.reshape(*x.shape[:-1], m.out_features)
+            outs[i] = y.reshape(*inputs[i].shape[:-1], modules[i].out_features)
     return outs
 
 

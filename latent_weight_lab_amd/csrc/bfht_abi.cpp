@@ -195,6 +195,32 @@ size_t linear_ws(const lwl::LinearArgs& a) {
   return linear_uses_mfma(a) ? align_up(lwl::linear_workspace_bytes(a)) : 0;
 }
 
+// Epilogue (lwl_bfht_linear_forward_ex): the kernels' form of it, and the
+// workspace it adds after linear_ws (float32 row sums of x, with a row-sum term).
+lwl::LinearEpi epilogue_of(const lwl_bfht_linear_epilogue* ep) {
+  lwl::LinearEpi e{};
+  if (!ep) return e;
+  e.bias = ep->bias;
+  e.base = ep->base;
+  e.coef = ep->row_sum_coef;
+  e.cscale = (float)ep->row_sum_scale;
+  return e;
+}
+size_t row_sum_ws(const lwl::LinearArgs& a) { return a.epi.coef ? align_up((size_t)a.tokens * sizeof(float)) : 0; }
+size_t linear_ex_ws(const lwl::LinearArgs& a) { return linear_ws(a) + row_sum_ws(a); }
+
+// Launches one fused linear (a.x, a.latent, a.out, a.epi set; a.work at least
+// linear_ex_ws bytes): the row sums first when the epilogue has a row-sum term.
+hipError_t launch_linear_ex(lwl::LinearArgs a, hipStream_t s) {
+  if (a.epi.coef) {
+    float* xsum = (float*)((unsigned char*)a.work + linear_ws(a));
+    const hipError_t e = lwl::launch_row_sums(a, xsum, s);
+    if (e != hipSuccess) return e;
+    a.epi.xsum = xsum;
+  }
+  return linear_uses_mfma(a) ? lwl::launch_linear(a, s) : lwl::launch_linear_small(a, s);
+}
+
 // Fused latent-gradient checks (no reference counterpart: the reference forms
 // grad_weight in HBM, block_fht.py:339-352).
 int check_linear_bwd(int dtype, int64_t tokens, int64_t in_features, int64_t latent_size, int64_t out_features,
@@ -258,6 +284,7 @@ int check_linear_jobs(int dtype, const lwl_bfht_linear_job* jobs, int64_t count,
     v[(size_t)i].x = j.input;
     v[(size_t)i].latent = j.latent;
     v[(size_t)i].out = j.out;
+    v[(size_t)i].epi = epilogue_of(j.epilogue);
   }
   if (need_ptrs)
     for (int64_t a = 0; a < count; ++a)
@@ -337,7 +364,7 @@ extern "C" {
 
 const char* lwl_last_error(void) { return g_last_error.c_str(); }
 
-int lwl_abi_version(void) { return 1; }
+int lwl_abi_version(void) { return 2; }
 
 int lwl_bfht_check_forward(int dtype, int64_t latent_size, int64_t output_size, int64_t layers,
                            int64_t start, int64_t stop) {
@@ -435,6 +462,24 @@ int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, in
                             int64_t in_features, int64_t latent_size, int64_t out_features,
                             int64_t layers, int64_t seed, double weight_scale, void* out,
                             void* workspace, size_t workspace_bytes, void* stream) {
+  return lwl_bfht_linear_forward_ex(input, latent, dtype, tokens, in_features, latent_size, out_features, layers,
+                                    seed, weight_scale, nullptr, out, workspace, workspace_bytes, stream);
+}
+
+size_t lwl_bfht_linear_forward_ex_workspace_size(int dtype, int64_t tokens, int64_t in_features,
+                                                 int64_t out_features, int64_t latent_size,
+                                                 const lwl_bfht_linear_epilogue* epilogue) {
+  if (check_linear(dtype, tokens, in_features, latent_size, out_features, 1)) return 0;
+  lwl::LinearArgs a = plan_linear(dtype, tokens, in_features, latent_size, out_features, 1, 0, 1.0);
+  a.epi = epilogue_of(epilogue);
+  return linear_ex_ws(a);
+}
+
+int lwl_bfht_linear_forward_ex(const void* input, const void* latent, int dtype, int64_t tokens,
+                               int64_t in_features, int64_t latent_size, int64_t out_features,
+                               int64_t layers, int64_t seed, double weight_scale,
+                               const lwl_bfht_linear_epilogue* epilogue, void* out, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   int rc = check_linear(dtype, tokens, in_features, latent_size, out_features, layers);
   if (rc) return rc;
   if (tokens == 0) return ok();
@@ -442,15 +487,14 @@ int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, in
     return fail(LWL_ERR_INVALID, "input, latent and out must be non-null");
   lwl::LinearArgs a = plan_linear(dtype, tokens, in_features, latent_size, out_features, layers,
                                   seed, weight_scale);
-  rc = check_workspace(linear_ws(a), workspace, workspace_bytes);
+  a.epi = epilogue_of(epilogue);
+  rc = check_workspace(linear_ex_ws(a), workspace, workspace_bytes);
   if (rc) return rc;
   a.x = input;
   a.latent = latent;
   a.out = out;
   a.work = workspace;
-  const hipError_t e = linear_uses_mfma(a) ? lwl::launch_linear(a, (hipStream_t)stream)
-                                           : lwl::launch_linear_small(a, (hipStream_t)stream);
-  return hip_status(e, "lwl_bfht_linear_forward");
+  return hip_status(launch_linear_ex(a, (hipStream_t)stream), "lwl_bfht_linear_forward");
 }
 
 int lwl_bfht_check_linear_jobs(int dtype, const lwl_bfht_linear_job* jobs, int64_t count) {
@@ -461,14 +505,18 @@ int lwl_bfht_check_linear_jobs(int dtype, const lwl_bfht_linear_job* jobs, int64
 // Grouped workspace: the grouped jobs' partial rows side by side (one launch
 // reads them all), then one region that the jobs running as single launches
 // reuse one after another (the largest of their workspaces).
-bool job_grouped(const lwl::LinearArgs& a) { return a.tokens > 0 && linear_uses_mfma(a) && lwl::linear_groupable(a); }
+// Grouped: the matrix-core kernel's jobs below its tiled-x batch whose epilogue
+// is at most a bias (the grouped table carries one bias pointer per job).
+bool job_grouped(const lwl::LinearArgs& a) {
+  return a.tokens > 0 && linear_uses_mfma(a) && lwl::linear_groupable(a) && !a.epi.base && !a.epi.coef;
+}
 
 size_t grouped_ws(const std::vector<lwl::LinearArgs>& v) {
   size_t together = 0, single = 0;
   for (const auto& a : v) {
     if (a.tokens == 0) continue;
     if (job_grouped(a)) together += linear_ws(a);
-    else single = std::max(single, linear_ws(a));
+    else single = std::max(single, linear_ex_ws(a));
   }
   return together + single;
 }
@@ -498,9 +546,8 @@ int lwl_bfht_linear_forward_grouped(int dtype, const lwl_bfht_linear_job* jobs, 
     }
   for (auto& a : v) {
     if (a.tokens == 0 || job_grouped(a)) continue;
-    a.work = linear_ws(a) ? (unsigned char*)workspace + off : nullptr;
-    const hipError_t e = linear_uses_mfma(a) ? lwl::launch_linear(a, (hipStream_t)stream)
-                                             : lwl::launch_linear_small(a, (hipStream_t)stream);
+    a.work = linear_ex_ws(a) ? (unsigned char*)workspace + off : nullptr;
+    const hipError_t e = launch_linear_ex(a, (hipStream_t)stream);
     if (e != hipSuccess) return hip_status(e, "lwl_bfht_linear_forward_grouped");
   }
   return hip_status(lwl::launch_linear_grouped(grouped.data(), (int64_t)grouped.size(), (hipStream_t)stream),

@@ -65,6 +65,19 @@ __device__ __forceinline__ T from_f32(float v) {
 
 __device__ __forceinline__ int lds_index(int p) { return p + (p >> 5); }
 
+// The fused linear's epilogue (lwl_bfht_linear_forward_ex) after the product v:
+// + the row-sum term, + base, + bias, each a float32 add in that order and none
+// contracted into an FMA, so every kernel that stores an output rounds alike.
+// Absent terms are skipped rather than added as 0 (which turns -0 into +0).
+__device__ __forceinline__ float linear_epilogue(float v, bool has_xs, float xs, bool has_base, float base,
+                                                 bool has_bias, float bias) {
+#pragma clang fp contract(off)
+  if (has_xs) v = v + xs;
+  if (has_base) v = v + base;
+  if (has_bias) v = v + bias;
+  return v;
+}
+
 // Job of workgroup `wg` in a grouped launch (uniform across the workgroup):
 // the table's prefix sums count workgroups, so each workgroup serves one job.
 template <class Table>

@@ -48,6 +48,18 @@ hipError_t launch_mfma15(const BfhtArgs& a, hipStream_t s, bool forward);
 hipError_t launch_sign_words(uint32_t seed32, int64_t block, int layer, int64_t first_word,
                              int64_t nwords, uint32_t* out, hipStream_t s);
 
+// Epilogue of the fused linear (lwl_bfht_linear_forward_ex): the stored value
+// is v = scale * acc, then + cscale * (*coef) * xsum[t] (coef set), + base[t, o]
+// (base set), + bias[o] (bias set), in float32 in that order.  xsum holds the
+// float32 row sums of x (launch_row_sums) when coef is set.
+struct LinearEpi {
+  const void* bias;   // [out], the I/O dtype
+  const void* base;   // [tokens, out], the I/O dtype
+  const float* coef;  // one float32 on the device
+  const float* xsum;  // [tokens]
+  float cscale;
+};
+
 struct LinearArgs {
   int dtype;
   const void* x;       // [tokens, in]
@@ -62,7 +74,12 @@ struct LinearArgs {
   float weight_scale;
   int blocks_per_wg;   // generated blocks per workgroup (linear_blocks_per_wg)
   int token_splits;
+  LinearEpi epi;       // all null: plain out = weight_scale * x @ W^T
 };
+
+// Float32 row sums of x [tokens, in] into xsum, one wave per row in a fixed
+// order (bfht_linear_small.hip).
+hipError_t launch_row_sums(const LinearArgs& a, float* xsum, hipStream_t s);
 
 // Fused linear limits: the generated block (<= 2^15) and its row layout live
 // in LDS; in_features bounds the padded row length.
@@ -81,29 +98,31 @@ hipError_t launch_linear(const LinearArgs& a, hipStream_t s);
 
 // Several fused linears in few launches (bfht_linear.hip): jobs the
 // matrix-core kernel takes with one generated block per workgroup (batches
-// below its tiled-x size) run in one launch per (layers, row tiles) class of
-// up to kLinearGroupMax jobs, each job exactly as its single launch computes it
+// below its tiled-x size) run in one launch per layer count of up to
+// kLinearGroupMax jobs, each job exactly as its single launch computes it
 // (same work items, same partial-row sums), with its own `work` (partial rows,
-// linear_workspace_bytes).
+// linear_workspace_bytes, inside one workspace) and at most a bias as epilogue.
 constexpr int kLinearGroupMax = 48;  // the table stays below the 4 KiB of kernel arguments
 struct LinearGroupJob {
   const __bf16* x;
   const __bf16* latent;
   __bf16* out;
-  float* partial;
+  const __bf16* bias;      // or nullptr
   int32_t tokens, in_f, out_f, n;
   uint32_t seed32;
   float scale;
   int32_t nblocks, pitch, token_split;
+  uint32_t partial_off;    // floats from LinearGroupTable::partial
 };
 struct LinearGroupTable {  // passed by value; prefix counts workgroups, cprefix combine workgroups
+  float* partial;          // the lowest of the jobs' `work`
   int32_t count;
   int32_t prefix[kLinearGroupMax + 1];
   int32_t cprefix[kLinearGroupMax + 1];
   LinearGroupJob job[kLinearGroupMax];
 };
 static_assert(sizeof(LinearGroupTable) <= 4000, "grouped linear table fits the kernel arguments");
-bool linear_groupable(const LinearArgs& a);
+bool linear_groupable(const LinearArgs& a);  // shape only; the caller checks the epilogue
 hipError_t launch_linear_grouped(const LinearArgs* jobs, int64_t count, hipStream_t s);
 
 // The reference extension's own fused-linear domain (bfht_linear_small.hip):

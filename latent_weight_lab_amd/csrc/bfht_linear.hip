@@ -52,6 +52,12 @@ __device__ __forceinline__ void store_bf16_through(__bf16* p, float v) {
   asm volatile("global_store_short %0, %1, off sc0 sc1" ::"v"(p), "v"(bits) : "memory");
 }
 
+// The bf16 at byte offset `off` of a buffer, as float (0 past its end).
+__device__ __forceinline__ float bf16_at(__amdgpu_buffer_rsrc_t r, int off) {
+  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  return (float)__builtin_bit_cast(__bf16, h);
+}
+
 __device__ __forceinline__ f32x4v mfma16(u32x4 a, u32x4 b, f32x4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                  0, 0, 0);
@@ -176,13 +182,14 @@ __global__ __launch_bounds__(256) void bfht_linear_tile_x(const __bf16* __restri
 // against token split `split` of token_split (every thread of the workgroup
 // calls it; `lds` is the workgroup's kLinearLdsBytes).  `pitch` table rows
 // (>= the tile's output rows; 16*NT when that fits in the LDS, else exact and
-// the last row tile masked on read).
-template <int L, int NT, bool kTiled, int KB, int KG = kGroup, int KD = kDepth>
+// the last row tile masked on read).  kEpi: the stores apply `ep` (a separate
+// instantiation, so the plain kernels carry none of its code or registers).
+template <int L, int NT, bool kTiled, int KB, bool kEpi, int KG = kGroup, int KD = kDepth>
 __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const __bf16* __restrict__ latent,
                                             __bf16* __restrict__ out, float* __restrict__ partial, int tokens,
                                             int in_f, int out_f, int n, uint32_t seed32, float scale,
                                             int token_split, int64_t nblocks, int pitch, int split, int64_t tile,
-                                            unsigned char* lds) {
+                                            const LinearEpi& ep, unsigned char* lds) {
 
   const int64_t size = (int64_t)in_f * out_f;
   const int64_t g0 = tile * KB * kB;                          // first flat position
@@ -295,6 +302,11 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
   // o_last, so no load waits on a mask before the next step's MFMAs.
   auto brd = [&](const u32x4* b, int nt) -> u32x4 { return b[16 * nt]; };
   constexpr uint32_t kOff = 0x80000000u;  // voffset that reads 0
+  // epilogue: which terms, the row-sum coefficient (one scalar load), the bias
+  const bool has_xs = kEpi && ep.xsum != nullptr, has_base = kEpi && ep.base != nullptr,
+             has_bias = kEpi && ep.bias != nullptr;
+  const float cx = has_xs ? ep.cscale * *ep.coef : 0.f;
+  const auto bias_r = rsrc(has_bias ? ep.bias : (const void*)out, has_bias ? (uint32_t)(out_f * 2) : 0u);
 
   // A pass takes G consecutive token tiles (16 G tokens) of this wave: per k
   // step it reads the NT W tiles once from LDS and issues G * NT MFMAs; x is
@@ -372,6 +384,7 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     // Branch-free stores: each token tile gets buffer resources over its own rows
     // of out and of the partials (tokens past the end fall outside them), and an
     // element that does not belong in a destination gets the offset that drops it.
+    // The epilogue's inputs are read the same way (out-of-range reads give 0).
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int tt = tg + g;
@@ -381,18 +394,28 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       const auto o_r = rsrc(out + (int64_t)t0 * out_f, (uint32_t)(nt_tok * out_f * 2));
       const auto pf_r = rsrc(part_first + t0, (uint32_t)(nt_tok * 4));
       const auto pl_r = rsrc(part_last + t0, (uint32_t)(nt_tok * 4));
+      const auto xs_r = rsrc(has_xs ? (const void*)(ep.xsum + t0) : (const void*)out, has_xs ? (uint32_t)(nt_tok * 4) : 0u);
+      const auto b_r = rsrc(has_base ? (const __bf16*)ep.base + (int64_t)t0 * out_f : out,
+                            has_base ? (uint32_t)(nt_tok * out_f * 2) : 0u);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int o = o_first + 16 * nt + l16;
         const bool is_first = first_partial && o == o_first;
         const bool is_last = last_partial && o == o_last;
         const bool is_out = o <= o_last && !is_first && !is_last;
+        const float bias_o = has_bias ? bf16_at(bias_r, o * 2) : 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = 4 * kq + r;
-          const float v = acc[g][nt][r];
-          const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)(scale * v));
-          __builtin_amdgcn_raw_buffer_store_b16(b, o_r, is_out ? (m * out_f + o) * 2 : (int)kOff, 0, 0);
+          const int off = is_out ? (m * out_f + o) * 2 : (int)kOff;
+          float v = scale * acc[g][nt][r];
+          if constexpr (kEpi) {
+            const float xs = has_xs ? cx * __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xs_r, m * 4, 0, 0)) : 0.f;
+            const float base_v = has_base ? bf16_at(b_r, off) : 0.f;
+            v = linear_epilogue(v, has_xs, xs, has_base, base_v, has_bias, bias_o);
+          }
+          const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)v);
+          __builtin_amdgcn_raw_buffer_store_b16(b, o_r, off, 0, 0);
         }
         // partial rows: the first row of the tile (nt 0, l16 0) and its last row
         if (nt == 0 || 16 * (nt + 1) > o_last - o_first) {
@@ -427,14 +450,14 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     for (int tg = rest0 + KG * wave; tg < tt1; tg += KG * kWaves) pass(std::integral_constant<int, KG>{}, tg, tt1);
   }
 }
-template <int L, int NT, bool kTiled, int KB, int KG = kGroup, int KD = kDepth>
+template <int L, int NT, bool kTiled, int KB, bool kEpi, int KG = kGroup, int KD = kDepth>
 __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __restrict__ x,
                                                                const __bf16* __restrict__ latent,
                                                                __bf16* __restrict__ out,
                                                                float* __restrict__ partial, int tokens,
                                                                int in_f, int out_f, int n, uint32_t seed32,
                                                                float scale, int token_split, int64_t nblocks,
-                                                               int pitch) {
+                                                               int pitch, LinearEpi ep) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLinearLdsBytes];
   // XCD-aware work order: workgroup i runs on XCD i % 8, and work item
   // p = split * ntiles + tile (split-major) goes to XCD p / per_xcd, so each
@@ -446,30 +469,42 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __r
   if (p >= nwork) return;  // uniform: the grid is rounded up to whole XCD rows
   const int split = (int)(p / ntiles);
   const int64_t tile = p - (int64_t)split * ntiles;
-  linear_item<L, NT, kTiled, KB, KG, KD>(x, latent, out, partial, tokens, in_f, out_f, n, seed32, scale,
-                                         token_split, nblocks, pitch, split, tile, lds);
+  linear_item<L, NT, kTiled, KB, kEpi, KG, KD>(x, latent, out, partial, tokens, in_f, out_f, n, seed32, scale,
+                                               token_split, nblocks, pitch, split, tile, ep, lds);
 }
 
-// Rows straddling tiles b-1 and b: out[t][o] = scale * (last(b-1)[t] + first(b)[t]).
+// Output (t, o) of a straddling row from its two partial dot products, with the epilogue.
+__device__ __forceinline__ float combine_value(float p_last, float p_first, float scale, const LinearEpi& ep, int t,
+                                               int o, int out_f) {
+  const bool has_xs = ep.xsum != nullptr, has_base = ep.base != nullptr, has_bias = ep.bias != nullptr;
+  const float xs = has_xs ? ep.cscale * *ep.coef * ep.xsum[t] : 0.f;
+  const float base_v = has_base ? (float)((const __bf16*)ep.base)[(int64_t)t * out_f + o] : 0.f;
+  const float bias_o = has_bias ? (float)((const __bf16*)ep.bias)[o] : 0.f;
+  return linear_epilogue(scale * (p_last + p_first), has_xs, xs, has_base, base_v, has_bias, bias_o);
+}
+
+// Rows straddling tiles b-1 and b: out[t][o] = scale * (last(b-1)[t] + first(b)[t]) + epilogue.
 __global__ __launch_bounds__(256) void bfht_linear_combine(const float* __restrict__ partial,
                                                            __bf16* __restrict__ out, int tokens, int in_f,
                                                            int out_f, int64_t ntiles, int64_t tile_len,
-                                                           float scale) {
+                                                           float scale, LinearEpi ep) {
   const int t = blockIdx.x * 256 + threadIdx.x;
   const int64_t b = (int64_t)blockIdx.y + 1;
   if (t >= tokens || b >= ntiles) return;
   const int64_t g0 = b * tile_len;
   if (g0 % in_f == 0) return;
   const int o = (int)(g0 / in_f);
-  const float v = partial[((b - 1) * 2 + 1) * (int64_t)tokens + t] + partial[(b * 2) * (int64_t)tokens + t];
-  store_bf16_through(out + (int64_t)t * out_f + o, scale * v);
+  const float v = combine_value(partial[((b - 1) * 2 + 1) * (int64_t)tokens + t], partial[(b * 2) * (int64_t)tokens + t],
+                                scale, ep, t, o, out_f);
+  store_bf16_through(out + (int64_t)t * out_f + o, v);
 }
 
 // Several matrices in one launch (the decode case: each matrix has a few dozen
 // generated blocks, far fewer than the 256 CUs): workgroup i serves job j with
 // prefix[j] <= i < prefix[j + 1], work item i - prefix[j] = split * nblocks +
-// block, as the single-matrix kernel's non-tiled, one-block-per-workgroup path.
-template <int L, int NT>
+// block, as the single-matrix kernel's non-tiled, one-block-per-workgroup path
+// (kBias: some job has a bias, applied as the single call's epilogue).
+template <int L, int NT, bool kBias>
 __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15_grouped(const LinearGroupTable g) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLinearLdsBytes];
   const int j = group_job(g, (int)blockIdx.x);
@@ -477,8 +512,9 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15_grouped(const Lin
   const int64_t p = (int64_t)blockIdx.x - g.prefix[j];
   const int split = (int)(p / jb.nblocks);
   const int64_t tile = p - (int64_t)split * jb.nblocks;
-  linear_item<L, NT, false, 1>(jb.x, jb.latent, jb.out, jb.partial, jb.tokens, jb.in_f, jb.out_f, jb.n, jb.seed32,
-                               jb.scale, jb.token_split, jb.nblocks, jb.pitch, split, tile, lds);
+  const LinearEpi ep{jb.bias, nullptr, nullptr, nullptr, 0.f};
+  linear_item<L, NT, false, 1, kBias>(jb.x, jb.latent, jb.out, g.partial + jb.partial_off, jb.tokens, jb.in_f, jb.out_f,
+                               jb.n, jb.seed32, jb.scale, jb.token_split, jb.nblocks, jb.pitch, split, tile, ep, lds);
 }
 
 // The straddling-row sums of every job of a grouped launch: workgroup i serves
@@ -496,11 +532,14 @@ __global__ __launch_bounds__(256) void bfht_linear_combine_grouped(const LinearG
   const int64_t g0 = b * kB;
   if (g0 % jb.in_f == 0) return;
   const int o = (int)(g0 / jb.in_f);
-  const float v = jb.partial[((b - 1) * 2 + 1) * (int64_t)jb.tokens + t] + jb.partial[(b * 2) * (int64_t)jb.tokens + t];
-  store_bf16_through(jb.out + (int64_t)t * jb.out_f + o, jb.scale * v);
+  const float* partial = g.partial + jb.partial_off;
+  const LinearEpi ep{jb.bias, nullptr, nullptr, nullptr, 0.f};
+  const float v = combine_value(partial[((b - 1) * 2 + 1) * (int64_t)jb.tokens + t], partial[(b * 2) * (int64_t)jb.tokens + t],
+                                jb.scale, ep, t, o, jb.out_f);
+  store_bf16_through(jb.out + (int64_t)t * jb.out_f + o, v);
 }
 
-template <int L, bool kTiled, int KB>
+template <int L, bool kTiled, int KB, bool kEpi>
 hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
   const int nt = (int)linear_row_tiles(a.in_features, KB);
   const int64_t ntiles = (a.nblocks_w + KB - 1) / KB;
@@ -510,10 +549,10 @@ hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial
   auto* lat = (const __bf16*)a.latent;
   auto* o = (__bf16*)a.out;
 #define LWL_LIN(NT)                                                                                               \
-  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT, kTiled, KB>), \
+  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT, kTiled, KB, kEpi>), \
                      grid, block, 0, s, x, lat, o, partial,                                                      \
                      (int)a.tokens, (int)a.in_features, (int)a.out_features, (int)a.n, a.seed32, a.weight_scale, \
-                     a.token_splits, a.nblocks_w, pitch)
+                     a.token_splits, a.nblocks_w, pitch, a.epi)
   switch (nt) {
     case 1: LWL_LIN(1); break;
     case 2: LWL_LIN(2); break;
@@ -528,15 +567,21 @@ hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial
   if (e != hipSuccess || ntiles < 2) return e;
   hipLaunchKernelGGL(bfht_linear_combine, dim3((unsigned)((a.tokens + 255) / 256), (unsigned)(ntiles - 1)),
                      dim3(256), 0, s, (const float*)partial, o, (int)a.tokens, (int)a.in_features,
-                     (int)a.out_features, ntiles, (int64_t)KB * mfma15::kB, a.weight_scale);
+                     (int)a.out_features, ntiles, (int64_t)KB * mfma15::kB, a.weight_scale, a.epi);
   return hipGetLastError();
+}
+
+template <int L, bool kTiled, bool kEpi>
+hipError_t launch_linear_e(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
+  if constexpr (kTiled)
+    if (a.blocks_per_wg == 2) return launch_linear_kb<L, true, 2, kEpi>(a, x, partial, s);
+  return launch_linear_kb<L, kTiled, 1, kEpi>(a, x, partial, s);
 }
 
 template <int L, bool kTiled>
 hipError_t launch_linear_L(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
-  if constexpr (kTiled)
-    if (a.blocks_per_wg == 2) return launch_linear_kb<L, true, 2>(a, x, partial, s);
-  return launch_linear_kb<L, kTiled, 1>(a, x, partial, s);
+  if (a.epi.bias || a.epi.base || a.epi.xsum) return launch_linear_e<L, kTiled, true>(a, x, partial, s);
+  return launch_linear_e<L, kTiled, false>(a, x, partial, s);
 }
 
 template <int L>
@@ -554,16 +599,25 @@ hipError_t launch_linear_L(const LinearArgs& a, hipStream_t s) {
   return launch_linear_L<L, true>(a, (const __bf16*)tiled, partial, s);
 }
 
-template <int L>
-hipError_t launch_grouped_nt(const LinearGroupTable& g, int nt, hipStream_t s) {
+template <int L, bool kBias>
+hipError_t launch_grouped_b(const LinearGroupTable& g, int nt, hipStream_t s) {
   const dim3 grid((unsigned)g.prefix[g.count]), block(mfma15::kThreads);
   switch (nt) {
-    case 1: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 1>), grid, block, 0, s, g); break;
-    case 2: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 2>), grid, block, 0, s, g); break;
-    case 3: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 3>), grid, block, 0, s, g); break;
-    case 4: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 4>), grid, block, 0, s, g); break;
+    case 1: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 1, kBias>), grid, block, 0, s, g); break;
+    case 2: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 2, kBias>), grid, block, 0, s, g); break;
+    case 3: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 3, kBias>), grid, block, 0, s, g); break;
+    case 4: hipLaunchKernelGGL((bfht_linear_mfma15_grouped<L, 4, kBias>), grid, block, 0, s, g); break;
     default: return hipErrorInvalidValue;
   }
+  return hipSuccess;
+}
+
+template <int L>
+hipError_t launch_grouped_nt(const LinearGroupTable& g, int nt, hipStream_t s) {
+  bool bias = false;
+  for (int i = 0; i < g.count; ++i) bias = bias || g.job[i].bias;
+  const hipError_t e0 = bias ? launch_grouped_b<L, true>(g, nt, s) : launch_grouped_b<L, false>(g, nt, s);
+  if (e0 != hipSuccess) return e0;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || g.cprefix[g.count] == 0) return e;
   hipLaunchKernelGGL(bfht_linear_combine_grouped, dim3((unsigned)g.cprefix[g.count]), dim3(256), 0, s, g);
@@ -597,6 +651,11 @@ hipError_t launch_group_chunk(const LinearArgs* const* jobs, int count, int nt, 
   int64_t split = total >= 256 ? 1 : 256 / total;
   if (split > min_tiles) split = min_tiles;
   if (split < 1) split = 1;
+  // partial rows: offsets from the lowest `work` (every job's lies in one
+  // 256-byte-aligned workspace)
+  g.partial = (float*)jobs[0]->work;
+  for (int i = 1; i < count; ++i)
+    if ((float*)jobs[i]->work < g.partial) g.partial = (float*)jobs[i]->work;
   int64_t wg = 0, cw = 0;
   for (int i = 0; i < count; ++i) {
     const LinearArgs& a = *jobs[i];
@@ -604,7 +663,8 @@ hipError_t launch_group_chunk(const LinearArgs* const* jobs, int count, int nt, 
     jb.x = (const __bf16*)a.x;
     jb.latent = (const __bf16*)a.latent;
     jb.out = (__bf16*)a.out;
-    jb.partial = (float*)a.work;
+    jb.bias = (const __bf16*)a.epi.bias;
+    jb.partial_off = (uint32_t)((float*)a.work - g.partial);
     jb.tokens = (int)a.tokens;
     jb.in_f = (int)a.in_features;
     jb.out_f = (int)a.out_features;

@@ -56,7 +56,7 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small(const T* __rest
                                                                  const T* __restrict__ latent, T* __restrict__ out,
                                                                  int tokens, int in_f, int log_in, int out_f, int n,
                                                                  int64_t nblocks, uint32_t seed32, int layers,
-                                                                 float scale, int token_split) {
+                                                                 float scale, int token_split, LinearEpi ep) {
   using Gm = Geo<LB>;
   using SG = SmallLinearGeo<LB>;
   __shared__ float smem[SG::kLdsFloats];
@@ -91,6 +91,12 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small(const T* __rest
   const int npairs = (q1 - q0) * rows;
   const auto x_r = tile_rsrc(x, (uint64_t)tokens * in_f * sizeof(T));
   const auto o_r = tile_rsrc(out, (uint64_t)tokens * out_f * sizeof(T));
+  // epilogue terms (uniform); absent inputs get empty resources
+  const bool has_xs = ep.xsum != nullptr, has_base = ep.base != nullptr, has_bias = ep.bias != nullptr;
+  const float cx = has_xs ? ep.cscale * *ep.coef : 0.f;
+  const auto xs_r = tile_rsrc(has_xs ? (const void*)ep.xsum : (const void*)out, has_xs ? (uint64_t)tokens * 4 : 0);
+  const auto b_r = tile_rsrc(has_base ? ep.base : (const void*)out, has_base ? (uint64_t)tokens * out_f * sizeof(T) : 0);
+  const auto bias_r = tile_rsrc(has_bias ? ep.bias : (const void*)out, has_bias ? (uint64_t)out_f * sizeof(T) : 0);
   // A team's lanes share `pr`, so the shuffles below only read lanes that run
   // the same iteration.
   for (int pr = team; pr < npairs; pr += nteams) {
@@ -111,11 +117,38 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small(const T* __rest
     for (int u = 0; u < kQuad; ++u)
       for (int s = ks >> 1; s >= 1; s >>= 1) acc[u] += __shfl_xor(acc[u], s, 64);
     if (j == 0) {
+      const int o = row0 + r;
+      const float bias_o = has_bias ? buf_load<T>(bias_r, o) : 0.f;
 #pragma unroll
-      for (int u = 0; u < kQuad; ++u)
-        buf_store<T>(acc[u], o_r, t0 + u < tokens ? (t0 + u) * out_f + row0 + r : -1);
+      for (int u = 0; u < kQuad; ++u) {
+        const int t = t0 + u;
+        const int i = t < tokens ? t * out_f + o : -1;  // -1: loads read 0, the store is dropped
+        const float xs = has_xs ? cx * buf_load<float>(xs_r, t < tokens ? t : -1) : 0.f;
+        const float base_v = has_base ? buf_load<T>(b_r, i) : 0.f;
+        buf_store<T>(linear_epilogue(acc[u], has_xs, xs, has_base, base_v, has_bias, bias_o), o_r, i);
+      }
     }
   }
+}
+
+// Float32 sums of the rows of x (the fused linear's row-sum term): one wave per
+// row, lanes striding over k with eight loads in flight, then a fixed butterfly.
+template <class T>
+__global__ __launch_bounds__(256) void bfht_row_sums(const T* __restrict__ x, int tokens, int in_f,
+                                                     float* __restrict__ xsum) {
+  const int t = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar: uniform resource
+  if (t >= tokens) return;
+  const int lane = threadIdx.x & 63;
+  const auto x_r = tile_rsrc(x + (int64_t)t * in_f, (uint64_t)in_f * sizeof(T));  // k >= in_f reads 0
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < in_f; k0 += 8 * 64) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s[u] += buf_load<T>(x_r, k0 + 64 * u + lane);
+  }
+  float v = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  if (lane == 0) xsum[t] = v;
 }
 
 template <int LB, class T>
@@ -127,7 +160,7 @@ hipError_t launch_small_lb(const LinearArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((bfht_linear_small<LB, T>), dim3((unsigned)wtiles, (unsigned)a.token_splits), dim3(Gm::WG), 0,
                      s, (const T*)a.x, (const T*)a.latent, (T*)a.out, (int)a.tokens, (int)a.in_features, log_in,
                      (int)a.out_features, (int)a.n, a.nblocks_w, a.seed32, a.layers, a.weight_scale,
-                     a.token_splits);
+                     a.token_splits, a.epi);
   return hipGetLastError();
 }
 
@@ -157,6 +190,21 @@ int linear_small_token_splits(const LinearArgs& a) {
   if (split > cap) split = cap;
   if (split > 65535) split = 65535;
   return (int)(split < 1 ? 1 : split);
+}
+
+hipError_t launch_row_sums(const LinearArgs& a, float* xsum, hipStream_t s) {
+  if (a.tokens == 0) return hipSuccess;
+  const dim3 grid((unsigned)((a.tokens + 3) / 4)), block(256);
+  switch (a.dtype) {
+    case kF32: hipLaunchKernelGGL(bfht_row_sums<float>, grid, block, 0, s, (const float*)a.x, (int)a.tokens,
+                                  (int)a.in_features, xsum); break;
+    case kF16: hipLaunchKernelGGL(bfht_row_sums<f16>, grid, block, 0, s, (const f16*)a.x, (int)a.tokens,
+                                  (int)a.in_features, xsum); break;
+    case kBF16: hipLaunchKernelGGL(bfht_row_sums<bf16>, grid, block, 0, s, (const bf16*)a.x, (int)a.tokens,
+                                   (int)a.in_features, xsum); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_linear_small(const LinearArgs& a, hipStream_t s) {

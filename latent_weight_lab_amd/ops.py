@@ -73,10 +73,42 @@ def linear_supported(in_features: int, out_features: int, latent: torch.Tensor, 
                                                  in_features, latent.numel(), out_features, 1) == N.LWL_OK
 
 
+def _epilogue(tokens: int, out_features: int, dtype: torch.dtype, dev, bias=None, base=None,
+              row_sum_coef=None, row_sum_scale: float = 1.0):
+    """The ``lwl_bfht_linear_epilogue`` of the given terms (None: no epilogue) and the
+    tensors it points to (to keep alive until the launch is queued)."""
+    if bias is None and base is None and row_sum_coef is None:
+        return None, []
+    ep, keep = N.LinearEpilogue(), []
+    if bias is not None:
+        if bias.dtype != dtype or bias.numel() != out_features or bias.device != dev:
+            raise N.BlockFHTArgumentError(f"fused linear bias must be {out_features} values of {dtype} on {dev}")
+        bias = bias.contiguous()
+        ep.bias = bias.data_ptr()
+        keep.append(bias)
+    if base is not None:
+        if base.dtype != dtype or tuple(base.shape) != (tokens, out_features) or base.device != dev:
+            raise N.BlockFHTArgumentError(f"fused linear base must be a [{tokens}, {out_features}] {dtype} on {dev}")
+        base = base.contiguous()
+        ep.base = base.data_ptr()
+        keep.append(base)
+    if row_sum_coef is not None:
+        coef = row_sum_coef.detach().reshape(1).to(device=dev, dtype=torch.float32)
+        ep.row_sum_coef = coef.data_ptr()
+        ep.row_sum_scale = float(row_sum_scale)
+        keep.append(coef)
+    return ep, keep
+
+
 def linear_forward(x2d: torch.Tensor, latent: torch.Tensor, out_features: int, layers: int, seed: int,
-                   weight_scale: float) -> torch.Tensor:
+                   weight_scale: float, bias: torch.Tensor | None = None, base: torch.Tensor | None = None,
+                   row_sum_coef: torch.Tensor | None = None, row_sum_scale: float = 1.0) -> torch.Tensor:
     """Fused ``x @ (weight_scale * W)^T`` with W generated on chip (reference
-    ext.linear_forward, ``csrc/block_fht_ext_cuda.cu:624-681``)."""
+    ext.linear_forward, ``csrc/block_fht_ext_cuda.cu:624-681``).  With any of ``bias``
+    ``[out]``, ``base`` ``[tokens, out]`` (both of x's dtype) or ``row_sum_coef`` (a device
+    scalar) the kernels' stores add ``base + row_sum_scale * row_sum_coef * x.sum(-1) + bias``
+    in float32 before the one rounding (``lwl_bfht_linear_forward_ex``; reference
+    ``forward_fused``'s tail, ``block_fht.py:493-500``)."""
     dev = N.require_cuda(x2d, latent)
     x2d = x2d.contiguous()
     latent = latent.contiguous()
@@ -89,13 +121,15 @@ def linear_forward(x2d: torch.Tensor, latent: torch.Tensor, out_features: int, l
     out = torch.empty(tokens, out_features, dtype=x2d.dtype, device=dev)
     if tokens == 0:
         return out
+    ep, keep = _epilogue(tokens, out_features, x2d.dtype, dev, bias, base, row_sum_coef, row_sum_scale)
+    epp = ctypes.byref(ep) if ep is not None else None
     with _device_guard(dev):
-        need = L.lwl_bfht_linear_forward_workspace_size(tokens, in_features, out_features, latent.numel())
+        need = L.lwl_bfht_linear_forward_ex_workspace_size(code, tokens, in_features, out_features, latent.numel(), epp)
         ws_ptr, ws_size, ws = N.workspace(need, dev)
-        N.check(L.lwl_bfht_linear_forward(x2d.data_ptr(), latent.data_ptr(), code, tokens, in_features,
-                                          latent.numel(), out_features, layers, seed, float(weight_scale),
-                                          out.data_ptr(), ws_ptr, ws_size, N.stream_ptr(dev)))
-    del ws
+        N.check(L.lwl_bfht_linear_forward_ex(x2d.data_ptr(), latent.data_ptr(), code, tokens, in_features,
+                                             latent.numel(), out_features, layers, seed, float(weight_scale), epp,
+                                             out.data_ptr(), ws_ptr, ws_size, N.stream_ptr(dev)))
+    del ws, keep
     return out
 
 
@@ -103,15 +137,18 @@ def linear_forward_grouped(specs: list[tuple], outs: list[torch.Tensor] | None =
     """Many fused linears ``x @ (weight_scale * W)^T`` in few launches
     (``lwl_bfht_linear_forward_grouped``); each result equals its own ``linear_forward`` call
     bit for bit.  ``specs``: ``(x2d, latent, out_features, layers, seed, weight_scale)`` per
-    matrix, all of one dtype; ``outs``: optional preallocated ``[tokens, out_features]``
-    outputs."""
+    matrix, all of one dtype, optionally followed by a dict of ``linear_forward``'s epilogue
+    arguments (``bias``, ``base``, ``row_sum_coef``, ``row_sum_scale``); ``outs``: optional
+    preallocated ``[tokens, out_features]`` outputs."""
     if not specs:
         return []
     dev = N.require_cuda(*[t for sp in specs for t in sp[:2]])
     dtype = specs[0][0].dtype
     code = N.dtype_code(dtype)
-    jobs, result, keep = [], [], []
-    for i, (x2d, latent, out_features, layers, seed, scale) in enumerate(specs):
+    jobs, result, keep, epis = [], [], [], []
+    for i, spec in enumerate(specs):
+        x2d, latent, out_features, layers, seed, scale = spec[:6]
+        extra = spec[6] if len(spec) > 6 and spec[6] else {}
         x2d = x2d.contiguous()
         latent = latent.contiguous()
         if x2d.dtype != dtype or latent.dtype != dtype:
@@ -127,6 +164,11 @@ def linear_forward_grouped(specs: list[tuple], outs: list[torch.Tensor] | None =
         j.input, j.latent, j.out = x2d.data_ptr(), latent.data_ptr(), out.data_ptr()
         j.tokens, j.in_features, j.latent_size = tokens, in_features, latent.numel()
         j.out_features, j.layers, j.seed, j.weight_scale = int(out_features), int(layers), int(seed), float(scale)
+        ep, ep_keep = _epilogue(tokens, int(out_features), dtype, dev, **extra)
+        if ep is not None:
+            j.epilogue = ctypes.pointer(ep)
+            epis.append(ep)
+            keep += ep_keep
         jobs.append(j)
         result.append(out)
         keep += [x2d, latent]
@@ -136,7 +178,7 @@ def linear_forward_grouped(specs: list[tuple], outs: list[torch.Tensor] | None =
     with _device_guard(dev):
         ws_ptr, ws_size, ws = N.workspace(L.lwl_bfht_linear_forward_grouped_workspace_size(code, arr, len(jobs)), dev)
         N.check(L.lwl_bfht_linear_forward_grouped(code, arr, len(jobs), ws_ptr, ws_size, N.stream_ptr(dev)))
-    del ws, keep
+    del ws, keep, epis
     return result
 
 

@@ -38,7 +38,7 @@ def test_library_shares_torch_hip_runtime():
 
 
 def test_abi_version():
-    assert N.lib().lwl_abi_version() == 1
+    assert N.lib().lwl_abi_version() == 2
 
 
 @pytest.mark.parametrize(
@@ -362,3 +362,45 @@ def test_linear_jobs_validation():
                             linear_job(5, 3072, 768, 32768, out=0x30000000))
     assert one < big
     assert lib.lwl_bfht_linear_forward_grouped_workspace_size(2, arr, 4) == two + three + big
+
+
+def test_linear_job_and_epilogue_structs_match_header():
+    # lwl_bfht_linear_job: 3 pointers, 6 int64, double, epilogue pointer;
+    # lwl_bfht_linear_epilogue: 3 pointers, double
+    assert N.LinearJob.weight_scale.offset == 72 and N.LinearJob.epilogue.offset == 80
+    assert ctypes_sizeof(N.LinearJob) == 88
+    assert N.LinearEpilogue.row_sum_scale.offset == 24 and ctypes_sizeof(N.LinearEpilogue) == 32
+
+
+def test_linear_epilogue_workspace_size():
+    import ctypes
+
+    lib = N.lib()
+    ep = N.LinearEpilogue()
+    ep.bias, ep.base = 0x1000, 0x2000
+    # no epilogue, or one without a row-sum term: the plain call's workspace
+    for shape in [(4096, 768, 3072, 32768), (300, 1000, 450, 32768), (300, 1024, 4096, 16384)]:
+        plain = lib.lwl_bfht_linear_forward_workspace_size(*shape)
+        assert lib.lwl_bfht_linear_forward_ex_workspace_size(2, *shape, None) == plain
+        assert lib.lwl_bfht_linear_forward_ex_workspace_size(2, *shape, ctypes.byref(ep)) == plain
+    # a row-sum term adds the float32 row sums of x, 256-byte aligned, after it
+    ep.row_sum_coef = 0x3000
+    plain = lib.lwl_bfht_linear_forward_workspace_size(4096, 768, 3072, 32768)
+    assert lib.lwl_bfht_linear_forward_ex_workspace_size(2, 4096, 768, 3072, 32768, ctypes.byref(ep)) == plain + 4096 * 4
+    assert lib.lwl_bfht_linear_forward_ex_workspace_size(0, 37, 64, 200, 4096, ctypes.byref(ep)) == 256
+    # the dtype matters for the domain: float32 at block 2^15 takes no fused kernel
+    assert lib.lwl_bfht_linear_forward_ex_workspace_size(0, 4096, 768, 3072, 32768, None) == 0
+    assert lib.lwl_bfht_check_linear_forward(0, 4096, 768, 32768, 3072, 3) == N.LWL_ERR_UNSUPPORTED
+    # grouped: a bias-only job stays grouped (its partial rows in the shared region); a job with a
+    # row-sum term runs as a single launch with its row sums after its own workspace
+    j1 = linear_job(17, 768, 768, 32768, out=0x9000000)
+    j2 = linear_job(5, 3072, 768, 32768, out=0x30000000)
+    bias_ep = N.LinearEpilogue()
+    bias_ep.bias = 0x1000
+    j1.epilogue = ctypes.pointer(bias_ep)
+    j2.epilogue = ctypes.pointer(ep)
+    two = lib.lwl_bfht_linear_forward_workspace_size(17, 768, 768, 32768)
+    three = lib.lwl_bfht_linear_forward_workspace_size(5, 3072, 768, 32768)
+    arr = (N.LinearJob * 2)(j1, j2)
+    assert lib.lwl_bfht_check_linear_jobs(2, arr, 2) == N.LWL_OK
+    assert lib.lwl_bfht_linear_forward_grouped_workspace_size(2, arr, 2) == two + three + 256
