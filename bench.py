@@ -415,6 +415,15 @@ def extra_configs(abi, steps, warmup, only):
         except Exception as exc:  # noqa: BLE001
             res["c8_mix"] = {"error": f"{type(exc).__name__}: {exc}"}
 
+    # forward_fused's tail (bias, modulation row-sum term, residual base) in the fused kernels'
+    # stores (lwl_bfht_linear_forward_ex) vs the reference's sequence of torch ops after the
+    # fused linear (block_fht.py:493-500), config-4 shapes
+    if want("c4_epilogue"):
+        try:
+            res["c4_epilogue"] = epilogue_bench(torch)
+        except Exception as exc:  # noqa: BLE001
+            res["c4_epilogue"] = {"error": f"{type(exc).__name__}: {exc}"}
+
     # config 5: 12-layer GPT-2-small linear stack (qkv, proj, fc, fc-proj per layer = 48 matrices,
     # latents of 32768 bf16, seeds 100+i), forward only, fused vs dense on materialized weights
     if want("c5_stack"):
@@ -545,6 +554,42 @@ def stack_bench(abi, torch):
         except Exception as exc:  # noqa: BLE001
             row["error"] = f"{type(exc).__name__}: {exc}"
         out[f"tokens_{tokens}"] = row
+    return out
+
+
+def epilogue_bench(torch):
+    from latent_weight_lab_amd import ops
+
+    out = {}
+    for tokens in (64, 4096):
+        for inf, outf in ((768, 3072), (3072, 768)):
+            g = torch.Generator().manual_seed(5)
+            lat = torch.randn(32768, generator=g).to(torch.bfloat16).cuda()
+            x = torch.randn(tokens, inf, generator=g).to(torch.bfloat16).cuda()
+            bias = torch.randn(outf, generator=g).to(torch.bfloat16).cuda()
+            base = torch.randn(tokens, outf, generator=g).to(torch.bfloat16).cuda()
+            mod = torch.tensor([1e-3], dtype=torch.bfloat16).cuda()
+            rbs = 0.5
+
+            def fused():
+                ops.linear_forward(x, lat, outf, 3, 3, rbs, bias=bias, base=base, row_sum_coef=mod,
+                                   row_sum_scale=rbs)
+
+            def sequence():
+                y = ops.linear_forward(x, lat, outf, 3, 3, 1.0)
+                y = y + mod * x.sum(dim=-1, keepdim=True)
+                y = base + rbs * y
+                y + bias
+
+            def plain():
+                ops.linear_forward(x, lat, outf, 3, 3, 1.0)
+
+            f = time_graph(torch, fused, 20, 3)
+            q = time_graph(torch, sequence, 20, 3)
+            p = time_graph(torch, plain, 20, 3)
+            out[f"{inf}x{outf}_tokens_{tokens}"] = {
+                "fused_epilogue_ms": round(f * 1e3, 4), "sequence_ms": round(q * 1e3, 4),
+                "plain_ms": round(p * 1e3, 4), "sequence_over_fused": q / f}
     return out
 
 

@@ -397,25 +397,37 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       const auto xs_r = rsrc(has_xs ? (const void*)(ep.xsum + t0) : (const void*)out, has_xs ? (uint32_t)(nt_tok * 4) : 0u);
       const auto b_r = rsrc(has_base ? (const __bf16*)ep.base + (int64_t)t0 * out_f : out,
                             has_base ? (uint32_t)(nt_tok * out_f * 2) : 0u);
+      auto out_off = [&](int nt, int r) {  // byte offset of (token 4 kq + r, row tile nt) in out, or kOff
+        const int o = o_first + 16 * nt + l16;
+        const bool is_out = o <= o_last && !(first_partial && o == o_first) && !(last_partial && o == o_last);
+        return is_out ? ((4 * kq + r) * out_f + o) * 2 : (int)kOff;
+      };
+      // The epilogue's inputs of the whole token tile are loaded before its
+      // first store: a load issued after a store that may alias it waits for
+      // that store, which would serialize one memory round trip per element.
+      float xs[4] = {0.f, 0.f, 0.f, 0.f}, base_v[NT][4], bias_v[NT];
+      if constexpr (kEpi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (has_xs) xs[r] = cx * __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xs_r, (4 * kq + r) * 4, 0, 0));
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          bias_v[nt] = has_bias ? bf16_at(bias_r, (o_first + 16 * nt + l16) * 2) : 0.f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) base_v[nt][r] = has_base ? bf16_at(b_r, out_off(nt, r)) : 0.f;
+        }
+      }
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int o = o_first + 16 * nt + l16;
         const bool is_first = first_partial && o == o_first;
         const bool is_last = last_partial && o == o_last;
-        const bool is_out = o <= o_last && !is_first && !is_last;
-        const float bias_o = has_bias ? bf16_at(bias_r, o * 2) : 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int m = 4 * kq + r;
-          const int off = is_out ? (m * out_f + o) * 2 : (int)kOff;
           float v = scale * acc[g][nt][r];
-          if constexpr (kEpi) {
-            const float xs = has_xs ? cx * __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xs_r, m * 4, 0, 0)) : 0.f;
-            const float base_v = has_base ? bf16_at(b_r, off) : 0.f;
-            v = linear_epilogue(v, has_xs, xs, has_base, base_v, has_bias, bias_o);
-          }
+          if constexpr (kEpi) v = linear_epilogue(v, has_xs, xs[r], has_base, base_v[nt][r], has_bias, bias_v[nt]);
           const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)v);
-          __builtin_amdgcn_raw_buffer_store_b16(b, o_r, off, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(b, o_r, out_off(nt, r), 0, 0);
         }
         // partial rows: the first row of the tile (nt 0, l16 0) and its last row
         if (nt == 0 || 16 * (nt + 1) > o_last - o_first) {
