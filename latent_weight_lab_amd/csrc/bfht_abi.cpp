@@ -183,6 +183,8 @@ lwl::LinearArgs plan_linear(int dtype, int64_t tokens, int64_t in_features, int6
   if (linear_uses_mfma(a)) {
     a.blocks_per_wg = lwl::linear_blocks_per_wg(a);
     a.token_splits = lwl::linear_token_splits(a);
+  } else if (lwl::linear_small_mm_applicable(a)) {
+    a.token_splits = lwl::linear_small_mm_token_splits(a);
   } else {
     a.token_splits = lwl::linear_small_token_splits(a);
   }
@@ -218,7 +220,8 @@ hipError_t launch_linear_ex(lwl::LinearArgs a, hipStream_t s) {
     if (e != hipSuccess) return e;
     a.epi.xsum = xsum;
   }
-  return linear_uses_mfma(a) ? lwl::launch_linear(a, s) : lwl::launch_linear_small(a, s);
+  if (linear_uses_mfma(a)) return lwl::launch_linear(a, s);
+  return lwl::linear_small_mm_applicable(a) ? lwl::launch_linear_small_mm(a, s) : lwl::launch_linear_small(a, s);
 }
 
 // Fused latent-gradient checks (no reference counterpart: the reference forms

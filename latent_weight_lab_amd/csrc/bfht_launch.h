@@ -133,6 +133,15 @@ constexpr int kLinearSmallMaxLog = 14;
 bool linear_small_applicable(int dtype, int log_block, int64_t in_features);
 int linear_small_token_splits(const LinearArgs& a);  // needs tokens, log_block, nblocks_w
 hipError_t launch_linear_small(const LinearArgs& a, hipStream_t s);
+// The same domain at batches of kLinearMmMinTokens and more, contracted on the
+// matrix cores (bfht_linear_small_mm.hip): blocks of 2^5 .. 2^14, in_features a
+// multiple of 32 (16-bit I/O) or 16 (float32) with at least 16 rows per
+// 32768-weight (16384 for float32) workgroup tile.  No workspace.
+constexpr int kLinearMmMinLog = 5;
+constexpr int64_t kLinearMmMinTokens = 64;
+bool linear_small_mm_applicable(const LinearArgs& a);  // needs dtype, log_block, in/out features, tokens
+int linear_small_mm_token_splits(const LinearArgs& a);
+hipError_t launch_linear_small_mm(const LinearArgs& a, hipStream_t s);
 
 // Fused latent gradient of BlockFHTLinear (bfht_linear_bwd.hip):
 // grad_latent = weight_scale * T^T(grad^T x) with grad^T x formed per block on

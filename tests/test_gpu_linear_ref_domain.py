@@ -68,6 +68,13 @@ CASES = [
     (70, 2, 300, 3, 2, 5, 1.0),        # block 2^2: 256 blocks per workgroup
     (1000, 32, 2000, 500, 3, 6, 0.75),  # block 2^9 (16 rows of 32), 16 blocks per workgroup
     (3, 4096, 3, 8000, 2, 12, 1.0),    # block 2^13, out smaller than one block
+    # from 64 tokens the contraction runs on the matrix cores (bfht_linear_small_mm) where
+    # in_features is a multiple of 32 (16 for float32) with >= 16 rows per workgroup tile
+    (256, 64, 200, 4096, 3, -3, 1.0),   # block 2^12: 200 of 512 table rows, 13 row tiles
+    (100, 256, 1000, 2000, 2, 5, 1.0),  # block 2^11, ragged token tiles
+    (64, 2048, 40, 16384, 3, 7, 1.0),   # 16 rows per 16-bit tile; float32 (8 rows) stays on VALU
+    (2048, 128, 512, 1024, 2, 9, 0.5),  # block 2^10, token splits
+    (80, 16, 64, 64, 1, 10, 1.0),       # in 16: float32 on the matrix cores, 16-bit on VALU
 ]
 
 
