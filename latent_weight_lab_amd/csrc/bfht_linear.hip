@@ -227,9 +227,7 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       uint32_t nw[2][4];
       run_chain2<L>(acc, c, lds, src, [](int i) { return i; }, nw);
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[kb][k] = out_chunk<L>(acc[kb], nw[kb], c[kb], k);
+      for (int kb = 0; kb < KB; ++kb) out_chunks<L>(acc[kb], nw[kb], c[kb], v[kb]);
     } else {  // one block (KB = 1, or the last tile of an odd block count)
       const Ctx c = make_ctx(seed32, tile * KB);
       u32x4 src[kTiles][2];
@@ -237,8 +235,7 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       f32x16 acc[kTiles];
       uint32_t nw[4];
       run_chain<L>(acc, c, lds, src, [](int i) { return i; }, nw);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[0][k] = out_chunk<L>(acc, nw, c, k);
+      out_chunks<L>(acc, nw, c, v[0]);
     }
     __syncthreads();  // every wave has read its last exchange
     // Zero exactly the entries of the tile's rows that the scatter leaves out

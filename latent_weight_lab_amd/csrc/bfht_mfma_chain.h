@@ -253,6 +253,42 @@ __device__ __forceinline__ uint32_t operand_mask(const uint32_t (&nw)[4], int t,
   return (nw[c] << (15 - b)) & kPairSign;
 }
 
+// Word pair {lo, hi} shifted left by s as one 64-bit value: one v_lshlrev_b64
+// (full rate on gfx950, where LLVM would split a constant 64-bit shift into two
+// 32-bit instructions).  The bits of lo shifted into hi land below bit s, and
+// for s <= 15 below the pair-sign bits 15 and 31, so each dword of the result
+// AND kPairSign is its own word's mask.
+__device__ __forceinline__ u32x2 shl_pair(uint64_t pair, int s) {
+  uint64_t r;
+  asm("v_lshlrev_b64 %0, %1, %2" : "=v"(r) : "s"(s), "v"(pair));
+  return u32x2{(uint32_t)r, (uint32_t)(r >> 32)};
+}
+
+// Stage a's sign masks in pairs: instructions c = 0 and c = 1 of one VGPR v
+// share the shift (15 - b) of operand_mask, so one 64-bit shift of their two
+// words gives both.  Pairs: S0 {nw[0], nw[1]}; S1 {nw[0], nw[2]} (v = 0, 1) and
+// {nw[1], nw[3]} (v = 2, 3).
+template <bool kOdd>
+__device__ __forceinline__ void sign_pairs(const uint32_t (&nw)[4], uint64_t (&pairs)[2]) {
+  if (kOdd) {
+    pairs[0] = (uint64_t)nw[0] | ((uint64_t)nw[2] << 32);
+    pairs[1] = (uint64_t)nw[1] | ((uint64_t)nw[3] << 32);
+  } else {
+    pairs[0] = pairs[1] = (uint64_t)nw[0] | ((uint64_t)nw[1] << 32);
+  }
+}
+// a[c][v] ^= operand_mask<kOdd>(nw, t, c, v) for both c, from the pairs above
+template <bool kOdd>
+__device__ __forceinline__ void sign_operands(u32x4 (&a)[2], const uint64_t (&pairs)[2], int t) {
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int b = kOdd ? (t | ((v & 1) << 2)) : ((v >> 1) | ((v & 1) << 1) | (t << 2));
+    const u32x2 m = shl_pair(pairs[kOdd ? (v >> 1) : 0], 15 - b);
+    a[0][v] ^= m[0] & kPairSign;
+    a[1][v] ^= m[1] & kPairSign;
+  }
+}
+
 __device__ __forceinline__ u32x4 pack8(const f32x16& a, int base) {
   u32x4 r;
   r[0] = pk(a[base + 0], a[base + 1]);
@@ -267,15 +303,12 @@ template <bool kSigned, bool kOdd>
 __device__ __forceinline__ void stage_rows(f32x16 (&acc)[kTiles], const u32x4 (&h)[2],
                                            const uint32_t (&nw)[4]) {
   const f32x16 zero = {};
+  uint64_t pairs[2];
+  if (kSigned) sign_pairs<kOdd>(nw, pairs);
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) {
     u32x4 a[2] = {pack8(acc[t], 0), pack8(acc[t], 8)};
-    if (kSigned) {
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<kOdd>(nw, t, c, v);
-    }
+    if (kSigned) sign_operands<kOdd>(a, pairs, t);
     f32x16 d = mfma(a[0], h[0], zero);
     acc[t] = mfma(a[1], h[1], d);
   }
@@ -416,13 +449,12 @@ __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, u
   for (int i = 0; i < L; ++i) {
     const bool odd = i & 1;
     if (i == 0) {
+      uint64_t pairs[2];
+      sign_pairs<false>(nw[0], pairs);
 #pragma unroll
       for (int t = 0; t < kTiles; ++t) {
         u32x4 a[2] = {src[t][0], src[t][1]};
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<false>(nw[0], t, c, v);
+        sign_operands<false>(a, pairs, t);
         f32x16 d = mfma(a[0], hq4[0], zero);
         acc[t] = mfma(a[1], hq4[1], d);
       }
@@ -483,13 +515,12 @@ __device__ __forceinline__ void run_chain2(f32x16 (&acc)[2][kTiles], const Ctx (
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       if (i == 0) {
+        uint64_t pairs[2];
+        sign_pairs<false>(nw[b][0], pairs);
 #pragma unroll
         for (int t = 0; t < kTiles; ++t) {
           u32x4 a[2] = {src[t][0], src[t][1]};
-#pragma unroll
-          for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) a[c][v] ^= operand_mask<false>(nw[b][0], t, c, v);
+          sign_operands<false>(a, pairs, t);
           f32x16 d = mfma(a[0], hq4[0], zero);
           acc[b][t] = mfma(a[1], hq4[1], d);
         }
@@ -596,6 +627,60 @@ __device__ __forceinline__ u32x4 out_chunk(const f32x16 (&acc)[kTiles], const ui
   return v;
 }
 
+// All eight output chunks of this lane, as out_chunk gives them one by one,
+// with the sign masks in pairs (shl_pair): in S1 chunks k and k + 2 (words
+// k >> 1 and k >> 1 + 1), in S0 chunks k and k + 4 (words 0 and 1) share every
+// mask's shift.
+template <int L>
+__device__ __forceinline__ void out_chunks(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4], const Ctx& x,
+                                           u32x4 (&v)[8]) {
+  if constexpr (L % 2 == 1) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = swap_idx04(nw[j]) >> x.p4;
+    const uint64_t pair[2] = {(uint64_t)w[0] | ((uint64_t)w[1] << 32), (uint64_t)w[2] | ((uint64_t)w[3] << 32)};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int r0 = (k & 1) | ((k >> 1) << 2);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = r0 | ((q >> 1) << 1);
+        v[k][q] = pk(acc[2 * (q & 1)][r], acc[2 * (q & 1) + 1][r]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if ((k >> 1) & 1) continue;  // chunk k + 2 takes the pair's high word
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int b = ((q & 1) << 1) | ((q >> 1) << 2) | ((k & 1) << 3);
+        const u32x2 m = shl_pair(pair[k >> 2], 15 - b);
+        v[k][q] ^= m[0] & kPairSign;
+        v[k + 2][q] ^= m[1] & kPairSign;
+      }
+    }
+  } else {
+    const uint64_t pair = (uint64_t)swap_idx04(nw[0]) | ((uint64_t)swap_idx04(nw[1]) << 32);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t = (q >> 1) + 2 * (k & 1);
+        const int r = 2 * (q & 1) + 4 * ((k >> 1) & 1) + 8 * (k >> 2);
+        v[k][q] = pk(acc[t][r], acc[t][r + 1]);
+      }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int b = ((k >> 1) & 1) | ((q & 1) << 1) | ((q >> 1) << 2) | ((k & 1) << 3);
+        const u32x2 m = shl_pair(pair, 15 - b);
+        v[k][q] ^= m[0] & kPairSign;
+        v[k + 4][q] ^= m[1] & kPairSign;
+      }
+  }
+}
+
 // Slot of 16-byte output chunk c in the staging buffer.  The lanes of one
 // staging write hold chunks 4 apart (c = 4 * lane32 + const); XOR-ing bits
 // 3-4 into bits 0-1 spreads any 8 consecutive lanes over the 8 16-byte bank
@@ -609,8 +694,10 @@ __device__ __forceinline__ int stage_slot(int c) { return c ^ ((c >> 3) & 3); }
 template <int L>
 __device__ __forceinline__ void stage_output(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4], const Ctx& x,
                                              u32x4* stage) {
+  u32x4 v[8];
+  out_chunks<L>(acc, nw, x, v);
 #pragma unroll
-  for (int k = 0; k < 8; ++k) stage[stage_slot(out_chunk_pos<L>(x, k) >> 3)] = out_chunk<L>(acc, nw, x, k);
+  for (int k = 0; k < 8; ++k) stage[stage_slot(out_chunk_pos<L>(x, k) >> 3)] = v[k];
 }
 
 // Backward tail: applies D_0 (inverted words `nw` of the chain's last sign
