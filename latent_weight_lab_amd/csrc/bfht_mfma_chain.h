@@ -240,19 +240,6 @@ __device__ __forceinline__ void layer_words(const Ctx& x, int layer, uint32_t (&
   if (!kOdd) nw[2] = nw[3] = 0;
 }
 
-// XOR mask of stage-a operand VGPR v (pair j = 2v, 2v+1) of tile t, instruction c.
-//   S0: j0 = p0 (pair), j1 = p1, j2 = p4, c = p11, t = (p2, p3)
-//   S1: j0 = p3 (pair), j1 = p2, j2 = p13, c = p14, t = (p0, p1)
-template <bool kOdd>
-__device__ __forceinline__ uint32_t operand_mask(const uint32_t (&nw)[4], int t, int c, int v) {
-  if (kOdd) {
-    const int b = t | ((v & 1) << 2);  // + 8*p4, folded into the word
-    return (nw[(v >> 1) + 2 * c] << (15 - b)) & kPairSign;
-  }
-  const int b = (v >> 1) | ((v & 1) << 1) | (t << 2);
-  return (nw[c] << (15 - b)) & kPairSign;
-}
-
 // Word pair {lo, hi} shifted left by s as one 64-bit value: one v_lshlrev_b64
 // (full rate on gfx950, where LLVM would split a constant 64-bit shift into two
 // 32-bit instructions).  The bits of lo shifted into hi land below bit s, and
@@ -264,10 +251,16 @@ __device__ __forceinline__ u32x2 shl_pair(uint64_t pair, int s) {
   return u32x2{(uint32_t)r, (uint32_t)(r >> 32)};
 }
 
-// Stage a's sign masks in pairs: instructions c = 0 and c = 1 of one VGPR v
-// share the shift (15 - b) of operand_mask, so one 64-bit shift of their two
-// words gives both.  Pairs: S0 {nw[0], nw[1]}; S1 {nw[0], nw[2]} (v = 0, 1) and
-// {nw[1], nw[3]} (v = 2, 3).
+// Sign masks of stage a's operands.  VGPR v of instruction c of tile t holds
+// the packed pair j = (2v, 2v+1):
+//   S0: j0 = p0 (pair), j1 = p1, j2 = p4, c = p11, t = (p2, p3)
+//   S1: j0 = p3 (pair), j1 = p2, j2 = p13, c = p14, t = (p0, p1)
+// and its XOR mask is (word << (15 - b)) & kPairSign with b the pair-layout bit
+// of its low element: S0 word nw[c], b = (v >> 1) | (v & 1) << 1 | t << 2; S1
+// word nw[(v >> 1) + 2c], b = t | (v & 1) << 2 (+ 8 p4, folded into the word).
+// Instructions c = 0 and c = 1 of one VGPR share the shift, so one 64-bit shift
+// of their two words gives both.  Pairs: S0 {nw[0], nw[1]}; S1 {nw[0], nw[2]}
+// (v = 0, 1) and {nw[1], nw[3]} (v = 2, 3).
 template <bool kOdd>
 __device__ __forceinline__ void sign_pairs(const uint32_t (&nw)[4], uint64_t (&pairs)[2]) {
   if (kOdd) {
@@ -277,7 +270,7 @@ __device__ __forceinline__ void sign_pairs(const uint32_t (&nw)[4], uint64_t (&p
     pairs[0] = pairs[1] = (uint64_t)nw[0] | ((uint64_t)nw[1] << 32);
   }
 }
-// a[c][v] ^= operand_mask<kOdd>(nw, t, c, v) for both c, from the pairs above
+// a[c][v] ^= its mask, for both c, from the pairs above
 template <bool kOdd>
 __device__ __forceinline__ void sign_operands(u32x4 (&a)[2], const uint64_t (&pairs)[2], int t) {
 #pragma unroll
@@ -598,39 +591,15 @@ __device__ __forceinline__ int out_chunk_pos(const Ctx& x, int k) {
            (x.wave << 12);
 }
 
-template <int L>
-__device__ __forceinline__ u32x4 out_chunk(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4], const Ctx& x,
-                                           int k) {
-  u32x4 v;
-  if constexpr (L % 2 == 1) {
-    // VGPR q: p1 = q&1 (tile bit 1), p2 = q>>1 (register bit 1); pair = p0 (tile bit 0).
-    // Pair-layout bit of the low element: p4 + 2p1 + 4p2 + 8p3, p4 folded into the word.
-    const int r0 = (k & 1) | ((k >> 1) << 2);
-    const uint32_t w = swap_idx04(nw[k >> 1]) >> x.p4;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = r0 | ((q >> 1) << 1);
-      const int b = ((q & 1) << 1) | ((q >> 1) << 2) | ((k & 1) << 3);
-      v[q] = pk(acc[2 * (q & 1)][r], acc[2 * (q & 1) + 1][r]) ^ ((w << (15 - b)) & kPairSign);
-    }
-  } else {
-    // VGPR q: tile (q>>1) + 2*p3, register pair 2*(q&1) + 4*p4 + 8*p11 (+1); pair = p0.
-    const uint32_t w = swap_idx04(nw[k >> 2]);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int t = (q >> 1) + 2 * (k & 1);
-      const int r = 2 * (q & 1) + 4 * ((k >> 1) & 1) + 8 * (k >> 2);
-      const int b = ((k >> 1) & 1) | ((q & 1) << 1) | ((q >> 1) << 2) | ((k & 1) << 3);
-      v[q] = pk(acc[t][r], acc[t][r + 1]) ^ ((w << (15 - b)) & kPairSign);
-    }
-  }
-  return v;
-}
-
-// All eight output chunks of this lane, as out_chunk gives them one by one,
-// with the sign masks in pairs (shl_pair): in S1 chunks k and k + 2 (words
-// k >> 1 and k >> 1 + 1), in S0 chunks k and k + 4 (words 0 and 1) share every
-// mask's shift.
+// All eight output chunks of this lane, packed and signed by the last sign layer.
+//   S1: VGPR q of chunk k holds register r = (k & 1) | (q >> 1) << 1 | (k >> 1) << 2
+//       of tiles 2 (q & 1) and 2 (q & 1) + 1 (p1 = q & 1, p2 = q >> 1, pair = p0);
+//       word nw[k >> 1] (pair layout, pre-shifted by p4), bit b = 2 (q & 1) + 4 (q >> 1) + 8 (k & 1).
+//   S0: VGPR q of chunk k holds registers r, r + 1 of tile (q >> 1) + 2 (k & 1),
+//       r = 2 (q & 1) + 4 ((k >> 1) & 1) + 8 (k >> 2) (pair = p0); word nw[k >> 2],
+//       bit b = ((k >> 1) & 1) + 2 (q & 1) + 4 (q >> 1) + 8 (k & 1).
+// The masks come in pairs (shl_pair): in S1 chunks k and k + 2 (words k >> 1 and
+// k >> 1 + 1), in S0 chunks k and k + 4 (words 0 and 1) share every shift.
 template <int L>
 __device__ __forceinline__ void out_chunks(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4], const Ctx& x,
                                            u32x4 (&v)[8]) {
