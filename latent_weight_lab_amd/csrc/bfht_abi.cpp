@@ -191,10 +191,11 @@ lwl::LinearArgs plan_linear(int dtype, int64_t tokens, int64_t in_features, int6
   return a;
 }
 
-// Workspace: the matrix-core kernel's partial rows and tiled x; the small-block
-// kernel needs none.
+// Workspace: the block-2^15 kernel's partial rows and tiled x; in the
+// reference's domain the tiled x of the matrix-core kernel (256 tokens and
+// more), else none.
 size_t linear_ws(const lwl::LinearArgs& a) {
-  return linear_uses_mfma(a) ? align_up(lwl::linear_workspace_bytes(a)) : 0;
+  return align_up(linear_uses_mfma(a) ? lwl::linear_workspace_bytes(a) : lwl::linear_small_mm_workspace_bytes(a));
 }
 
 // Epilogue (lwl_bfht_linear_forward_ex): the kernels' form of it, and the
@@ -453,12 +454,14 @@ int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features
 
 size_t lwl_bfht_linear_forward_workspace_size(int64_t tokens, int64_t in_features,
                                               int64_t out_features, int64_t latent_size) {
-  // The query has no dtype: it returns what the bfloat16 matrix-core kernel
-  // needs when it takes the shape (other dtypes then run the small-block kernel,
-  // which needs none), else 0.
-  if (check_linear(LWL_DTYPE_BF16, tokens, in_features, latent_size, out_features, 1)) return 0;
-  return linear_ws(plan_linear(LWL_DTYPE_BF16, tokens, in_features, latent_size, out_features, 1, 0,
-                               1.0));
+  // The query has no dtype (as ext.linear_forward has none): it returns the
+  // most any dtype needs for the shape (float32 in the reference's domain, whose
+  // tiled x copy is twice the 16-bit one), 0 where no fused kernel takes it.
+  size_t most = 0;
+  for (int dtype : {LWL_DTYPE_F32, LWL_DTYPE_F16, LWL_DTYPE_BF16})
+    if (!check_linear(dtype, tokens, in_features, latent_size, out_features, 1))
+      most = std::max(most, linear_ws(plan_linear(dtype, tokens, in_features, latent_size, out_features, 1, 0, 1.0)));
+  return most;
 }
 
 int lwl_bfht_linear_forward(const void* input, const void* latent, int dtype, int64_t tokens,

@@ -123,6 +123,12 @@ struct LinearGroupTable {  // passed by value; prefix counts workgroups, cprefix
 };
 static_assert(sizeof(LinearGroupTable) <= 4000, "grouped linear table fits the kernel arguments");
 bool linear_groupable(const LinearArgs& a);  // shape only; the caller checks the epilogue
+// x [tokens, row_bytes] re-laid out in MFMA A-operand order (bfht_linear.hip):
+// per 16-token tile and 64-byte step of k, one 1 KiB group of 16-byte chunks,
+// chunk (l & 15) + 16 (l >> 4) = bytes 64 s + 16 (l >> 4) .. + 15 of row
+// 16 T + (l & 15); rows past tokens and bytes past the row read 0.  row_bytes
+// % 16 == 0; the copy takes ceil(tokens / 16) * ceil(row_bytes / 64) KiB.
+hipError_t launch_tile_x(const void* x, void* xt, int64_t tokens, int64_t row_bytes, hipStream_t s);
 hipError_t launch_linear_grouped(const LinearArgs* jobs, int64_t count, hipStream_t s);
 
 // The reference extension's own fused-linear domain (bfht_linear_small.hip):
@@ -136,11 +142,13 @@ hipError_t launch_linear_small(const LinearArgs& a, hipStream_t s);
 // The same domain at batches of kLinearMmMinTokens and more, contracted on the
 // matrix cores (bfht_linear_small_mm.hip): blocks of 2^5 .. 2^14, in_features a
 // multiple of 32 (16-bit I/O) or 16 (float32) with at least 16 rows per
-// 32768-weight (16384 for float32) workgroup tile.  No workspace.
+// 32768-weight (16384 for float32) workgroup tile.
 constexpr int kLinearMmMinLog = 5;
 constexpr int64_t kLinearMmMinTokens = 64;
 bool linear_small_mm_applicable(const LinearArgs& a);  // needs dtype, log_block, in/out features, tokens
 int linear_small_mm_token_splits(const LinearArgs& a);
+// From 256 tokens its workspace holds x re-laid out (launch_tile_x); else none.
+size_t linear_small_mm_workspace_bytes(const LinearArgs& a);
 hipError_t launch_linear_small_mm(const LinearArgs& a, hipStream_t s);
 
 // Fused latent gradient of BlockFHTLinear (bfht_linear_bwd.hip):

@@ -144,31 +144,33 @@ size_t partial_bytes(const LinearArgs& a) {
   return ((size_t)ntiles * 2 * (size_t)a.tokens * sizeof(float) + 255) / 256 * 256;
 }
 
-// One wave per (token tile T, run of kTileSteps k steps): lane l reads
-// x[16 T + (l & 15)][32 s + 8 (l >> 4) .. +7] for every step s of the run (all
-// loads in flight before the first store; each pair of steps reads 16 whole
-// 128-byte row segments) and writes the 1 KiB chunk group of each step.  The
-// copy is stored write-through: the fused kernel reads it from other XCDs, and
-// streaming it out during the kernel avoids a serial L2 write-back at its end.
+// One wave per (token tile T, run of kTileSteps k steps): lane l reads the
+// 16 bytes at byte 64 s + 16 (l >> 4) of row 16 T + (l & 15) for every step s of
+// the run (all loads in flight before the first store; each pair of steps reads
+// 16 whole 128-byte row segments) and writes the 1 KiB chunk group of each
+// step: the MFMA A operands of 16 tokens x 64 bytes of k (32 bf16 / f16 values,
+// or 16 float32).  The copy is stored write-through: the fused kernel reads it
+// from other XCDs, and streaming it out during the kernel avoids a serial L2
+// write-back at its end.
 constexpr int kTileSteps = 8;
 
-__global__ __launch_bounds__(256) void bfht_linear_tile_x(const __bf16* __restrict__ x, u32x4* __restrict__ xt,
-                                                          int tokens, int in_f, int steps, int runs, int waves) {
+__global__ __launch_bounds__(256) void bfht_linear_tile_x(const unsigned char* __restrict__ x, u32x4* __restrict__ xt,
+                                                          int tokens, int row_bytes, int steps, int runs, int waves) {
   const int wv = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar: uniform resources
   if (wv >= waves) return;
   const int tt = wv / runs;
   const int s0 = (wv - tt * runs) * kTileSteps;
-  const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * in_f * 2));
+  const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * row_bytes));
   const auto xt_r = rsrc(xt, (uint32_t)((int64_t)(tt + 1) * steps * 1024));
   const int lane = threadIdx.x & 63;
   const int t = tt * kTokTile + (lane & 15);
-  const int k0 = kKStep * s0 + 8 * (lane >> 4);
+  const int k0 = 64 * s0 + 16 * (lane >> 4);
   u32x4 v[kTileSteps];
 #pragma unroll
   for (int j = 0; j < kTileSteps; ++j) {
-    const int k = k0 + kKStep * j;
-    const bool in_range = t < tokens && k < in_f;  // in_f % 8 == 0: whole chunks
-    v[j] = __builtin_amdgcn_raw_buffer_load_b128(x_r, in_range ? (t * in_f + k) * 2 : (int)0x80000000, 0, 0);
+    const int k = k0 + 64 * j;
+    const bool in_range = t < tokens && k < row_bytes;  // row_bytes % 16 == 0: whole chunks
+    v[j] = __builtin_amdgcn_raw_buffer_load_b128(x_r, in_range ? t * row_bytes + k : (int)0x80000000, 0, 0);
   }
 #pragma unroll
   for (int j = 0; j < kTileSteps; ++j) {
@@ -597,13 +599,8 @@ template <int L>
 hipError_t launch_linear_L(const LinearArgs& a, hipStream_t s) {
   float* partial = (float*)a.work;
   if (!linear_tiled(a)) return launch_linear_L<L, false>(a, (const __bf16*)a.x, partial, s);
-  const XTiling xt = x_tiling(a);
   auto* tiled = reinterpret_cast<u32x4*>((unsigned char*)a.work + partial_bytes(a));
-  const int runs = (xt.steps + kTileSteps - 1) / kTileSteps;
-  const int waves = (int)xt.tiles * runs;
-  hipLaunchKernelGGL(bfht_linear_tile_x, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, (const __bf16*)a.x,
-                     tiled, (int)a.tokens, (int)a.in_features, xt.steps, runs, waves);
-  const hipError_t e = hipGetLastError();
+  const hipError_t e = launch_tile_x(a.x, tiled, a.tokens, a.in_features * 2, s);
   if (e != hipSuccess) return e;
   return launch_linear_L<L, true>(a, (const __bf16*)tiled, partial, s);
 }
@@ -699,6 +696,16 @@ hipError_t launch_group_chunk(const LinearArgs* const* jobs, int count, int nt, 
 }
 
 }  // namespace
+
+hipError_t launch_tile_x(const void* x, void* xt, int64_t tokens, int64_t row_bytes, hipStream_t s) {
+  const int64_t tiles = (tokens + kTokTile - 1) / kTokTile;
+  const int steps = (int)((row_bytes + 63) / 64);
+  const int runs = (steps + kTileSteps - 1) / kTileSteps;
+  const int64_t waves = tiles * runs;
+  hipLaunchKernelGGL(bfht_linear_tile_x, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
+                     (const unsigned char*)x, (u32x4*)xt, (int)tokens, (int)row_bytes, steps, runs, (int)waves);
+  return hipGetLastError();
+}
 
 bool linear_groupable(const LinearArgs& a) {
   return linear_applicable(a.dtype, a.log_block, a.in_features) && !linear_tiled(a);

@@ -2,7 +2,9 @@
 // (float32 / float16 / bfloat16, block B <= 2^14, B % in_features == 0;
 // reference gate latent_weight_lab/block_fht.py:263-273, kernel
 // csrc/block_fht_ext_cuda.cu:225-329) at batches of 64 tokens and more, with
-// the contraction on the matrix cores.
+// the contraction on the matrix cores.  From 256 tokens x is first re-laid out
+// in MFMA operand order (launch_tile_x: one 1 KiB load per 16 tokens and step
+// instead of 16 rows x 64 bytes).
 //
 // A workgroup owns a tile of consecutive generated blocks (32768 weights for
 // 16-bit I/O, 16384 for float32; whole rows, since in_features divides B) and
@@ -95,6 +97,7 @@ constexpr int kMmDepth = 4;  // x prefetch distance in k steps
 
 template <int LB, class T, int kMmRows>
 __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small_mm(const T* __restrict__ x,
+                                                                    const u32x4m* __restrict__ xt,
                                                                     const T* __restrict__ latent,
                                                                     T* __restrict__ out, int tokens, int in_f,
                                                                     int log_in, int out_f, int n, int64_t nblocks,
@@ -138,8 +141,11 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small_mm(const T* __r
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int l16 = lane & 15, kq = lane >> 4;
   constexpr int kWaves = Gm::WG / 64;
-  const int nsteps = in_f / MG::KSTEP;
-  const auto x_r = tile_rsrc(x, (uint64_t)tokens * in_f * sizeof(T));
+  const int nsteps = in_f / MG::KSTEP;  // 64 bytes of k per step
+  // x: the tiled copy (1 KiB per token tile and step) or the row-major input
+  const bool tiled = xt != nullptr;
+  const auto x_r = tiled ? tile_rsrc(xt, (uint64_t)ntt * nsteps * 1024) : tile_rsrc(x, (uint64_t)tokens * in_f * sizeof(T));
+  const uint32_t xstride = tiled ? 1024u : 64u;
   const auto o_r = tile_rsrc(out, (uint64_t)tokens * out_f * sizeof(T));
   const bool has_xs = ep.xsum != nullptr, has_base = ep.base != nullptr, has_bias = ep.bias != nullptr;
   const float cx = has_xs ? ep.cscale * *ep.coef : 0.f;
@@ -155,7 +161,10 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small_mm(const T* __r
 #pragma unroll
     for (int g = 0; g < kMmTok; ++g) {
       const int t = (ttb + g) * 16 + l16;
-      xo[g] = (ttb + g < tt1 && t < tokens) ? (uint32_t)(t * in_f + (MG::KSTEP / 4) * kq) * (uint32_t)sizeof(T) : kOff;
+      if (tiled)
+        xo[g] = ttb + g < tt1 ? (uint32_t)(((ttb + g) * nsteps * 64 + lane) * 16) : kOff;
+      else
+        xo[g] = (ttb + g < tt1 && t < tokens) ? (uint32_t)(t * in_f + (MG::KSTEP / 4) * kq) * (uint32_t)sizeof(T) : kOff;
     }
     // table slot of this lane's row in row tile j, chunk 0 of step s: (4 s + kq) * pitch + 16 (rtb + j) + l16
     const int slot0 = kq * pitch + 16 * rtb + l16;
@@ -165,7 +174,7 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small_mm(const T* __r
 #pragma unroll
       for (int j = 0; j < kMmRows; ++j) acc[g][j] = f32x4m{0.f, 0.f, 0.f, 0.f};
     auto xload = [&](int g, int st) -> u32x4m {  // x of token tile g at step st (past the row: 0)
-      const uint32_t off = (st < nsteps && xo[g] != kOff) ? xo[g] + (uint32_t)(st * MG::KSTEP * (int)sizeof(T)) : kOff;
+      const uint32_t off = (st < nsteps && xo[g] != kOff) ? xo[g] + (uint32_t)st * xstride : kOff;
       return __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)off, 0, 0);
     };
     auto step = [&](const u32x4m (&a)[kMmTok], int st) {
@@ -243,7 +252,7 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small_mm(const T* __r
 }
 
 template <int LB, class T>
-hipError_t launch_mm_lb(const LinearArgs& a, hipStream_t s) {
+hipError_t launch_mm_lb(const LinearArgs& a, const u32x4m* xt, hipStream_t s) {
   using Gm = Geo<LB>;
   using MG = MmGeo<LB, T>;
   const int64_t wtiles = (a.in_features * a.out_features + MG::TILE - 1) / MG::TILE;
@@ -254,7 +263,7 @@ hipError_t launch_mm_lb(const LinearArgs& a, hipStream_t s) {
   const int rt = rows > 32 ? 4 : rows > 16 ? 2 : 1;
 #define LWL_MM(RT)                                                                                              \
   hipLaunchKernelGGL((bfht_linear_small_mm<LB, T, RT>), dim3((unsigned)wtiles, (unsigned)a.token_splits),     \
-                     dim3(Gm::WG), 0, s, (const T*)a.x, (const T*)a.latent, (T*)a.out, (int)a.tokens,          \
+                     dim3(Gm::WG), 0, s, (const T*)a.x, xt, (const T*)a.latent, (T*)a.out, (int)a.tokens,      \
                      (int)a.in_features, log_in, (int)a.out_features, (int)a.n, a.nblocks_w, a.seed32, a.layers, \
                      a.weight_scale, a.token_splits, a.epi)
   switch (rt) {
@@ -267,10 +276,17 @@ hipError_t launch_mm_lb(const LinearArgs& a, hipStream_t s) {
 }
 
 template <class T, int... LBs>
-hipError_t dispatch_mm(const LinearArgs& a, hipStream_t s, std::integer_sequence<int, LBs...>) {
-  using Fn = hipError_t (*)(const LinearArgs&, hipStream_t);
+hipError_t dispatch_mm(const LinearArgs& a, const u32x4m* xt, hipStream_t s, std::integer_sequence<int, LBs...>) {
+  using Fn = hipError_t (*)(const LinearArgs&, const u32x4m*, hipStream_t);
   static const Fn table[] = {&launch_mm_lb<LBs + kLinearMmMinLog, T>...};
-  return table[a.log_block - kLinearMmMinLog](a, s);
+  return table[a.log_block - kLinearMmMinLog](a, xt, s);
+}
+
+// x is read from the tiled copy from this many tokens (as the matrix-core
+// kernel of block 2^15 does), while its offsets stay below 2^31.
+bool mm_tiled(const LinearArgs& a) {
+  const int64_t esize = a.dtype == kF32 ? 4 : 2;
+  return a.tokens >= 256 && (a.tokens + 15) / 16 * (a.in_features * esize / 64) * 1024 < ((int64_t)1 << 31);
 }
 
 }  // namespace
@@ -283,6 +299,12 @@ bool linear_small_mm_applicable(const LinearArgs& a) {
   // whole k steps, and at least one 16-row tile per workgroup (the table's k
   // chunks per row then fit its spare chunks)
   return a.in_features % kstep == 0 && tile / a.in_features >= 16;
+}
+
+size_t linear_small_mm_workspace_bytes(const LinearArgs& a) {
+  if (!linear_small_mm_applicable(a) || !mm_tiled(a)) return 0;
+  const int64_t esize = a.dtype == kF32 ? 4 : 2;
+  return (size_t)((a.tokens + 15) / 16) * (size_t)(a.in_features * esize / 64) * 1024;
 }
 
 int linear_small_mm_token_splits(const LinearArgs& a) {
@@ -301,10 +323,17 @@ int linear_small_mm_token_splits(const LinearArgs& a) {
 
 hipError_t launch_linear_small_mm(const LinearArgs& a, hipStream_t s) {
   using Seq = std::make_integer_sequence<int, kLinearSmallMaxLog - kLinearMmMinLog + 1>;
+  const u32x4m* xt = nullptr;
+  if (mm_tiled(a)) {  // the tiled copy fills the start of the workspace
+    const int64_t esize = a.dtype == kF32 ? 4 : 2;
+    const hipError_t e = launch_tile_x(a.x, a.work, a.tokens, a.in_features * esize, s);
+    if (e != hipSuccess) return e;
+    xt = (const u32x4m*)a.work;
+  }
   switch (a.dtype) {
-    case kF32: return dispatch_mm<float>(a, s, Seq{});
-    case kF16: return dispatch_mm<f16>(a, s, Seq{});
-    case kBF16: return dispatch_mm<bf16>(a, s, Seq{});
+    case kF32: return dispatch_mm<float>(a, xt, s, Seq{});
+    case kF16: return dispatch_mm<f16>(a, xt, s, Seq{});
+    case kBF16: return dispatch_mm<bf16>(a, xt, s, Seq{});
   }
   return hipErrorInvalidValue;
 }

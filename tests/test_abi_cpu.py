@@ -190,9 +190,13 @@ def test_linear_workspace_size():
     # 528 in_features: 125 rows per two blocks exceed the register budget: one block per tile
     partial = (ceil_div(528 * 100, 32768) * 2 * 300 * 4 + 255) // 256 * 256
     assert lib.lwl_bfht_linear_forward_workspace_size(300, 528, 100, 32768) == partial + 19 * 17 * 1024
-    # the reference-domain kernel (block <= 2^14) keeps everything in LDS: no workspace
+    # the reference-domain kernels (block <= 2^14) keep W in LDS; from 256 tokens the matrix-core
+    # one reads x from a copy in MFMA order: ceil(tokens / 16) tiles x (in * 4 bytes / 64) steps of
+    # 1 KiB for float32, the largest of the dtypes (the query has none)
     assert lib.lwl_bfht_linear_forward_workspace_size(5, 8, 6, 32) == 0
-    assert lib.lwl_bfht_linear_forward_workspace_size(300, 1024, 4096, 16384) == 0
+    assert lib.lwl_bfht_linear_forward_workspace_size(255, 1024, 4096, 16384) == 0
+    assert lib.lwl_bfht_linear_forward_workspace_size(300, 1024, 4096, 16384) == 19 * 64 * 1024
+    assert lib.lwl_bfht_linear_forward_ex_workspace_size(1, 300, 1024, 4096, 16384, None) == 19 * 32 * 1024
 
 
 def ceil_div(a, b):
@@ -378,11 +382,12 @@ def test_linear_epilogue_workspace_size():
     lib = N.lib()
     ep = N.LinearEpilogue()
     ep.bias, ep.base = 0x1000, 0x2000
-    # no epilogue, or one without a row-sum term: the plain call's workspace
-    for shape in [(4096, 768, 3072, 32768), (300, 1000, 450, 32768), (300, 1024, 4096, 16384)]:
+    # no epilogue, or one without a row-sum term: the plain call's workspace (the dtype-less
+    # query gives the largest over dtypes: bfloat16 at block 2^15, float32 below)
+    for dtype, shape in [(2, (4096, 768, 3072, 32768)), (2, (300, 1000, 450, 32768)), (0, (300, 1024, 4096, 16384))]:
         plain = lib.lwl_bfht_linear_forward_workspace_size(*shape)
-        assert lib.lwl_bfht_linear_forward_ex_workspace_size(2, *shape, None) == plain
-        assert lib.lwl_bfht_linear_forward_ex_workspace_size(2, *shape, ctypes.byref(ep)) == plain
+        assert lib.lwl_bfht_linear_forward_ex_workspace_size(dtype, *shape, None) == plain
+        assert lib.lwl_bfht_linear_forward_ex_workspace_size(dtype, *shape, ctypes.byref(ep)) == plain
     # a row-sum term adds the float32 row sums of x, 256-byte aligned, after it
     ep.row_sum_coef = 0x3000
     plain = lib.lwl_bfht_linear_forward_workspace_size(4096, 768, 3072, 32768)
