@@ -139,10 +139,16 @@ int lwl_bfht_backward_noalloc(const void* grad_out, int dtype, int64_t latent_si
  *      the contraction runs on MFMA with float32 accumulation;
  *  (b) the reference extension's own domain (gate block_fht.py:263-273):
  *      float32, float16 or bfloat16, block <= 2^14, block % in_features == 0:
- *      the weight is generated in float32 and contracted in float32, as the
- *      reference's kernel does; no workspace.
+ *      the weight is generated in float32; below 64 tokens it is contracted
+ *      in float32 as the reference's kernel does, from 64 tokens on the
+ *      matrix cores (float32: exact float32 products; float16 / bfloat16: the
+ *      weight rounded to the I/O type, as the reference's fallback rounds it).
  * Other shapes return LWL_ERR_UNSUPPORTED and the caller generates the weight
  * and calls a GEMM, as the reference's fallback does (block_fht.py:263-288).
+ * The workspace query has no dtype (as ext.linear_forward has none) and
+ * returns the most any dtype needs for the shape: the block-2^15 kernel's
+ * partial rows and, from 256 tokens, a copy of x in MFMA order (in the
+ * reference's domain only that copy, float32's being the largest).
  */
 size_t lwl_bfht_linear_forward_workspace_size(int64_t tokens, int64_t in_features,
                                               int64_t out_features, int64_t latent_size);
