@@ -43,6 +43,7 @@ constexpr int kXcds = 8;      // MI355X: workgroup i is dispatched to XCD i % 8
 constexpr int kKStep = 32;    // k per MFMA
 constexpr int kGroup = 4;     // token tiles per wave pass (each W read feeds kGroup MFMAs)
 constexpr int kDepth = 4;     // x prefetch distance in k steps (and nsteps' rounding)
+constexpr int kDepthSingle = 12;  // the same for single-tile passes (decode: one token tile per workgroup)
 
 // Scattered bf16 store written through the XCD's L2 (sc0 sc1).  The combine
 // kernel's stores touch one 2-byte element per 128-byte line; written back,
@@ -309,11 +310,16 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
 
   // A pass takes G consecutive token tiles (16 G tokens) of this wave: per k
   // step it reads the NT W tiles once from LDS and issues G * NT MFMAs; x is
-  // prefetched KD steps ahead into a register ring (KD divides kDepth, the
-  // rounding of nsteps).  The loop body has no branches, so the compiler can
-  // count the loads in flight.  Tiles from `tend` on are masked.
+  // prefetched D steps ahead into a register ring.  A single-tile pass (G = 1)
+  // holds kDepthSingle steps in flight: it has few MFMAs per load, and at
+  // decode it is the whole contraction of a workgroup, so its loop would
+  // otherwise wait out one load latency per D steps.  Steps past nsteps (D need
+  // not divide it) load x as 0 and reuse the last step's W, adding 0.  The
+  // loop body has no branches, so the compiler can count the loads in flight.
+  // Tiles from `tend` on are masked.
   auto pass = [&](auto g_const, int tg, int tend) {
     constexpr int G = decltype(g_const)::value;
+    constexpr int D = G == 1 ? kDepthSingle : KD;
     uint32_t xo[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -342,9 +348,9 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     // Issue the first KD steps' loads in slot order, the order the loop
     // refills them in: the wait counts the compiler derives at the loop
     // head then let slot d's data arrive behind the later slots' requests.
-    u32x4 ring[KD][G];
+    u32x4 ring[D][G];
 #pragma unroll
-    for (int d = 0; d < KD; ++d) {
+    for (int d = 0; d < D; ++d) {
 #pragma unroll
       for (int g = 0; g < G; ++g) ring[d][g] = xload(g, d);
       __builtin_amdgcn_sched_barrier(0);
@@ -355,10 +361,10 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     u32x4 bt[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) bt[nt] = brd(bs, nt);
-    for (int s0 = 0; s0 < nsteps; s0 += KD) {
+    for (int s0 = 0; s0 < nsteps; s0 += D) {
 #pragma unroll
-      for (int d = 0; d < KD; ++d) {
-        const int sn = (s0 + d + 1 < nsteps) ? s0 + d + 1 : s0 + d;
+      for (int d = 0; d < D; ++d) {
+        const int sn = (s0 + d + 1 < nsteps) ? s0 + d + 1 : nsteps - 1;
         const u32x4* bsn = brow + sn * (4 * pitch + 1);
         u32x4 bn[NT];
 #pragma unroll
@@ -376,7 +382,7 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
         // loop back-edge, which serialises the whole prefetch.
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int g = 0; g < G; ++g) ring[d][g] = xload(g, s0 + d + KD);
+        for (int g = 0; g < G; ++g) ring[d][g] = xload(g, s0 + d + D);
       }
     }
     // D[m = 4*kq + r][n = l16]: token 16 tt + 4 kq + r, row o_first + 16 nt + l16.
@@ -443,15 +449,15 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
   };
 
   // Whole rounds in which every wave takes KG tiles, then the remainder.  With
-  // three or more row tiles a single-tile pass still issues 3+ MFMAs per load,
-  // so the remainder is split evenly over the waves in single-tile passes (a
-  // round with only some waves busy would leave the CU's other SIMDs idle for a
-  // whole KG-tile pass); with one or two row tiles a single-tile pass waits on
-  // its loads, and the remainder runs as KG-tile passes.
+  // three or more row tiles, or fewer remaining tiles than waves (decode), the
+  // remainder is split evenly over the waves in single-tile passes (a round with
+  // only some waves busy would leave the CU's other SIMDs idle for a whole
+  // KG-tile pass); otherwise, with one or two row tiles, a single-tile pass has
+  // too few MFMAs per load, and the remainder runs as KG-tile passes.
   const int full = (tt1 - tt0) / (KG * kWaves);
   for (int r = 0; r < full; ++r) pass(std::integral_constant<int, KG>{}, tt0 + (r * kWaves + wave) * KG, tt1);
   const int rest0 = tt0 + full * KG * kWaves;
-  if constexpr (NT >= 3) {
+  if (NT >= 3 || tt1 - rest0 <= kWaves) {
     const int per = (tt1 - rest0 + kWaves - 1) / kWaves;
     for (int i = 0; i < per; ++i) {
       const int tt = rest0 + wave * per + i;
@@ -529,17 +535,17 @@ __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15_grouped(const Lin
 }
 
 // The straddling-row sums of every job of a grouped launch: workgroup i serves
-// job j with cprefix[j] <= i < cprefix[j + 1] (its block boundaries times its
-// 256-token chunks), with the arithmetic of bfht_linear_combine.
+// job j with cprefix[j] <= i < cprefix[j + 1], one thread per (block boundary,
+// token) pair of the job, tokens fastest (a decode job's boundaries share one
+// workgroup), with the arithmetic of bfht_linear_combine.
 __global__ __launch_bounds__(256) void bfht_linear_combine_grouped(const LinearGroupTable g) {
   int j = 0;
   while (j + 1 < g.count && (int)blockIdx.x >= g.cprefix[j + 1]) ++j;
   const LinearGroupJob& jb = g.job[j];
-  const int chunks = (jb.tokens + 255) / 256;
-  const int q = (int)blockIdx.x - g.cprefix[j];
-  const int64_t b = q / chunks + 1;
-  const int t = (q - (q / chunks) * chunks) * 256 + (int)threadIdx.x;
-  if (t >= jb.tokens || b >= jb.nblocks) return;
+  const int64_t i = (int64_t)((int)blockIdx.x - g.cprefix[j]) * 256 + threadIdx.x;
+  if (i >= (int64_t)(jb.nblocks - 1) * jb.tokens) return;
+  const int64_t b = i / jb.tokens + 1;
+  const int t = (int)(i - (b - 1) * jb.tokens);
   const int64_t g0 = b * kB;
   if (g0 % jb.in_f == 0) return;
   const int o = (int)(g0 / jb.in_f);
@@ -683,7 +689,7 @@ hipError_t launch_group_chunk(const LinearArgs* const* jobs, int count, int nt, 
     g.prefix[i] = (int)wg;
     g.cprefix[i] = (int)cw;
     wg += a.nblocks_w * split;
-    cw += (a.nblocks_w - 1) * ((a.tokens + 255) / 256);
+    cw += ((a.nblocks_w - 1) * a.tokens + 255) / 256;
   }
   g.prefix[count] = (int)wg;
   g.cprefix[count] = (int)cw;
