@@ -39,6 +39,8 @@ CASES = [
     (torch.float32, 300, 1024, 4096, 16384, 2, 123, 0.5),  # reference domain
     (torch.float16, 37, 64, 200, 4096, 3, -3, 1.0),
     (torch.bfloat16, 37, 64, 200, 4096, 3, -3, 1.0),
+    (torch.float16, 256, 64, 200, 4096, 3, -3, 1.0),      # reference domain on the matrix cores, tiled x
+    (torch.bfloat16, 100, 256, 1000, 2000, 2, 5, 1.0),    # reference domain on the matrix cores, row-major x
 ]
 
 TERMS = [("bias",), ("base",), ("row_sum",), ("bias", "base", "row_sum")]
