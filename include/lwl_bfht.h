@@ -240,15 +240,17 @@ int lwl_bfht_linear_forward_grouped(int dtype, const lwl_bfht_linear_job* jobs, 
  *
  * grad_latent[p] = weight_scale * sum_b (D_0 H D_1 ... H D_L gw_b)[p], p < n,
  * with gw_b = (grad_out^T @ input) flattened, positions b*B .. b*B + B - 1:
- * the same value as lwl_bfht_backward applied to weight_scale * grad_weight,
- * but grad_weight is formed block by block on chip and never written.
- * grad_out [tokens, out_features], input [tokens, in_features], grad_latent [n],
- * all bfloat16 (latent length 16385..32768: block 2^15), in_features % 16 == 0,
- * in_features >= 528.  Each block's tile of grad_weight is rounded to bf16
- * before the transform (the reference casts grad_weight to the latent dtype);
- * the per-(block, token range) rows are summed in a fixed order.
- * The modulation term of the reference (block_fht.py:351-352) is left to the
- * caller.  Workspace: query *_workspace_size with the same shape.
+ * the value lwl_bfht_backward gives for weight_scale * grad_weight, in one
+ * call.  grad_out [tokens, out_features], input [tokens, in_features],
+ * grad_latent [n], all bfloat16 (latent length 16385..32768: block 2^15), any
+ * feature counts (rows off the 16-byte grid take element loads).  grad_weight
+ * is formed by a split-K matrix-core GEMM as float32 partial sums over token
+ * ranges in the workspace, summed in a fixed order, scaled and rounded once to
+ * bf16 (the reference's grad_weight is bf16), then transformed by the
+ * generator's backward; deterministic.  The modulation term of the reference
+ * (block_fht.py:351-352) is left to the caller.  Workspace: query
+ * *_workspace_size with the same shape (at config 4: 3 float32 partials of
+ * in * out, a bf16 copy, the block rows).
  */
 size_t lwl_bfht_linear_backward_latent_workspace_size(int64_t tokens, int64_t in_features,
                                                       int64_t out_features, int64_t latent_size);

@@ -186,8 +186,10 @@ class _BlockFHTLinearFn(torch.autograd.Function):
     """Training linear (reference ``block_fht.py:291-356``): W is generated for
     the forward and again for grad_input; grad_latent goes through the HIP
     backward of the generator, with grad_weight = g^T x either on a library GEMM
-    in HBM (the faster route on MI355X, and the reference's) or, with
-    ``fused_latent_grad``, formed block by block on chip and never stored."""
+    (the reference's route, and its rounding) or, with ``fused_latent_grad``, in
+    one call of the library's latent-gradient entry (its own split-K matrix-core
+    GEMM into float32 partials, then the generator's backward: faster at config-4
+    shapes; grad_weight is rounded once, after weight_scale)."""
 
     @staticmethod
     def forward(ctx, input, latent, bias, in_features, out_features, size, layers, seed, weight_scale,
@@ -218,7 +220,7 @@ class _BlockFHTLinearFn(torch.autograd.Function):
             xl = input_2d.to(dtype=latent.dtype)
             if (ctx.fused_latent_grad and size == in_f * out_f
                     and ops.linear_backward_latent_supported(in_f, out_f, latent, xl, g)):
-                # grad_weight = g^T x formed block by block on chip, never in HBM
+                # grad_weight = g^T x and the generator's backward in one library call
                 grad_latent = ops.linear_backward_latent(g, xl, latent, out_f, layers, seed, scale)
                 if alpha != 0.0:  # sum of grad_weight = sum_t (sum_o g[t, o]) (sum_i x[t, i])
                     gw_sum = (g.float().sum(dim=1) * xl.float().sum(dim=1)).sum()
@@ -279,8 +281,8 @@ class BlockFHTLinear(nn.Module):
         self.weight_scale = float(weight_scale)
         self.modulation_alpha = float(modulation_alpha)
         self.modulation_centered = bool(modulation_centered)
-        # not in the reference: form grad_weight per block on chip in the backward
-        # (lwl_bfht_linear_backward_latent) instead of on a GEMM in HBM
+        # not in the reference: the latent gradient in one library call
+        # (lwl_bfht_linear_backward_latent) instead of a library GEMM + the backward
         self.fused_latent_grad = bool(fused_latent_grad)
         self.latent_init_std = float(latent_init_std)
         self.residual_base_scale = float(residual_base_scale)

@@ -240,16 +240,15 @@ int check_linear_bwd(int dtype, int64_t tokens, int64_t in_features, int64_t lat
   const int lb = log2_pow2_ceil(latent_size);
   if (lb > lwl::kWholeBlockMaxLog || !lwl::linear_bwd_applicable(dtype, lb, in_features))
     return fail(LWL_ERR_UNSUPPORTED,
-                "fused linear latent gradient takes bfloat16 latents of length 16385..32768 (block 2^15) with "
-                "in_features %% 16 == 0 and 528 <= in_features (dtype code %d, latent size %lld, in_features %lld)",
-                dtype, (long long)latent_size, (long long)in_features);
-  const int64_t tpad = (tokens + 31) / 32 * 32;
-  if (tpad * in_features * 2 >= ((int64_t)1 << 31) || tpad * out_features * 2 >= ((int64_t)1 << 31))
+                "fused linear latent gradient takes bfloat16 latents of length 16385..32768 (block 2^15) "
+                "(dtype code %d, latent size %lld)",
+                dtype, (long long)latent_size);
+  // 32-bit buffer offsets: token-major operands, and each float32 partial of grad_weight
+  if (tokens * in_features * 2 >= ((int64_t)1 << 31) || tokens * out_features * 2 >= ((int64_t)1 << 31))
     return fail(LWL_ERR_UNSUPPORTED,
                 "fused linear latent gradient: tokens * in_features and tokens * out_features must stay below 2^30");
-  // the x / g re-layout kernels run one grid row per 128 features
-  if ((in_features + 127) / 128 > 65535 || (out_features + 127) / 128 > 65535)
-    return fail(LWL_ERR_UNSUPPORTED, "fused linear latent gradient: in_features and out_features must stay below 2^23");
+  if (in_features * out_features >= ((int64_t)1 << 29))
+    return fail(LWL_ERR_UNSUPPORTED, "fused linear latent gradient: in_features * out_features must stay below 2^29");
   return LWL_OK;
 }
 

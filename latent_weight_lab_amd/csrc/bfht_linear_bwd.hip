@@ -1,22 +1,36 @@
 // Fused latent gradient of BlockFHTLinear (bf16, block 2^15):
 //
 //   grad_latent = weight_scale * sum_b T_b^T (grad_weight[b*B : (b+1)*B]),
-//   grad_weight = grad^T @ x   ([out, in], never written to memory)
+//   grad_weight = grad^T @ x   ([out, in], flattened row-major = block positions)
 //
-// (reference latent_weight_lab/block_fht.py:339-352: grad_weight = g^T x in HBM,
-// then block_fht_grad_latent).  One workgroup per (generated block b, token
-// range): it contracts the block's rows of g^T x over its tokens on
-// v_mfma_f32_16x16x32_bf16, rounds the tile to bf16 into LDS in block-position
-// order (positions of rows that straddle into a neighbouring block are left to
-// that block's workgroup), runs the adjoint chain of bfht_mfma_chain.h on it
-// and writes weight_scale times its float32 partial latent row.  The rows of
-// all (block, token range) pairs are then summed in a fixed order, so the
-// result does not depend on timing.  The transform is linear, so summing the
-// per-token-range images after the chain equals transforming their sum.
+// (reference latent_weight_lab/block_fht.py:339-352: grad_weight = g^T x in
+// HBM as bf16, then block_fht_grad_latent).  Three steps:
 //
-// Both MFMA operands need 8 consecutive tokens per lane, while x and g are
-// stored token-major: x is re-laid out once into 16-column x 32-token tiles
-// (1 KiB per operand load), g transposed to [out, tokens].
+// 1. bfht_wgrad_gemm: grad_weight in float32 as S token-split partial sums,
+//    P_s = g[T_s]^T x[T_s], on v_mfma_f32_32x32x16_bf16.  Both operands are
+//    stored token-major (g [tokens, out], x [tokens, in]) while the MFMA wants
+//    8 consecutive tokens per lane, so tiles go to LDS as they are (16-byte
+//    global loads along the feature dimension, rows of 64 tokens) and come out
+//    through ds_read_b64_tr_b16, which transposes 16-bit elements across the
+//    16 lanes of a group: lane j of a group receives element (j & 3) of the
+//    8-byte reads of lanes 4e + (j >> 2), e = 0..3.  A lane group reading rows
+//    k0 .. k0 + 3 at features f0 + 4 (lane & 3) therefore leaves lane j with
+//    feature f0 + j at tokens k0 .. k0 + 3: half of an MFMA operand.
+//    Workgroup tile 256 (out) x 128 (in), 8 waves of 64 x 64, token steps of
+//    64 double-buffered in LDS with one barrier per step, the operands of the
+//    next k step read while the current one multiplies; workgroups are
+//    numbered so that consecutive tiles run on the same XCD (shared L2), tile
+//    order minor in the dimension with fewer tiles.  The split count fills the
+//    chip (tiles x splits ~ 256 workgroups).
+// 2. bfht_wgrad_sum: gw = bf16(weight_scale * sum_s P_s), the partials summed
+//    in a fixed order and rounded once (the reference's grad_weight is bf16;
+//    the scale, which it applies to the latent gradient, commutes with the
+//    linear transform), zero-padded to whole blocks.
+// 3. The generator's own backward on gw (launch_bfht: the matrix-core adjoint
+//    chain per block, then the fixed-order block sum), so the result does not
+//    depend on timing.
+#include <algorithm>
+
 #include "bfht_mfma_chain.h"
 
 namespace lwl {
@@ -24,272 +38,323 @@ namespace {
 
 using namespace mfma15;
 
-typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 
-constexpr int kTokStep = 32;  // tokens per MFMA k step
+constexpr int kBM = 256;               // grad_weight rows (out features) per tile
+constexpr int kBN = 128;               // grad_weight columns (in features) per tile
+constexpr int kBK = 64;                // tokens per step
+constexpr int kGemmThreads = 512;      // 8 waves: 4 (rows) x 2 (columns) of 64 x 64
+constexpr int kGPitch = kBM + 32;      // bf16 per LDS row of the g tile (576 bytes)
+constexpr int kXPitch = kBN + 32;      // bf16 per LDS row of the x tile (320 bytes)
+constexpr int kGStage = kBK * kGPitch * 2;
+constexpr int kXStage = kBK * kXPitch * 2;
+constexpr int kStage = kGStage + kXStage;
+constexpr int kGemmLds = 2 * kStage;   // 112 KiB
+constexpr int kGChunks = kBK * kBM / 8 / kGemmThreads;  // 16-byte chunks per thread per step: 4
+constexpr int kXChunks = kBK * kBN / 8 / kGemmThreads;  // 2
+constexpr uint32_t kOff = 0x80000000u;  // buffer offset that reads 0 and drops stores
+// Row pitches of 144 / 80 dwords: the four rows k0 .. k0 + 3 of a transposed
+// read start 16 banks apart, so 32 lanes (two groups, 64 bytes per row) cover
+// all 64 banks once.
+static_assert((kGPitch / 2) % 64 == 16 && (kXPitch / 2) % 64 == 16, "transposed reads must not conflict");
 
-__device__ __forceinline__ f32x4v mfma16(u32x4 a, u32x4 b, f32x4v c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                 0, 0, 0);
+__device__ __forceinline__ u32x2v read_tr(const unsigned char* lds, int byte_off) {
+  typedef __attribute__((address_space(3))) bf16x4v lds_v;
+  lds_v* p = (lds_v*)((__attribute__((address_space(3))) unsigned char*)lds + byte_off);
+  return __builtin_bit_cast(u32x2v, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(p));
+}
+
+// 8 features f .. f + 7 of token row t of a [tokens, ld] bf16 matrix (zero
+// past `rows` or `cols`): one 16-byte load (kVec: ld % 8 == 0, base 16-byte
+// aligned), else 8 element loads.
+template <bool kVec>
+__device__ __forceinline__ u32x4 load_chunk(const __amdgpu_buffer_rsrc_t r, int t, int f, int rows, int cols,
+                                            int ld) {
+  if constexpr (kVec) {
+    const bool ok = t < rows && f < cols;  // cols % 8 == 0: a chunk is all in or all out
+    return __builtin_amdgcn_raw_buffer_load_b128(r, ok ? (t * ld + f) * 2 : (int)kOff, 0, 0);
+  } else {
+    u32x4 v;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const bool ok0 = t < rows && f + e < cols, ok1 = t < rows && f + e + 1 < cols;
+      const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, ok0 ? (t * ld + f + e) * 2 : (int)kOff, 0, 0);
+      const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(r, ok1 ? (t * ld + f + e + 1) * 2 : (int)kOff, 0, 0);
+      v[e >> 1] = (lo & 0xffffu) | (hi << 16);
+    }
+    return v;
+  }
+}
+
+// Partial sums P_s[o][i] = sum over the split's tokens of g[t][o] x[t][i],
+// float32, row-major with row length in_f, split s at part + s * pstride.
+template <bool kVecG, bool kVecX>
+__global__ __launch_bounds__(kGemmThreads) void bfht_wgrad_gemm(const __bf16* __restrict__ g,
+                                                                const __bf16* __restrict__ x,
+                                                                float* __restrict__ part, int tokens, int out_f,
+                                                                int in_f, int tiles_o, int tiles_i, int splits,
+                                                                int steps_per_split, int64_t pstride) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kGemmLds];
+  // XCD-aware numbering: the hardware deals workgroups to the 8 XCDs in turn
+  // (bid % 8); logical ids run consecutively within an XCD
+  const int nwg = tiles_o * tiles_i * splits;
+  const int bid = blockIdx.x, xcd = bid & 7, q = nwg >> 3, rem = nwg & 7;
+  const int logical = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + (bid >> 3);
+  const int ntiles = tiles_o * tiles_i;
+  const int split = logical / ntiles, tile = logical % ntiles;
+  int to, ti;
+  if (tiles_i >= tiles_o) {
+    ti = tile / tiles_o;
+    to = tile % tiles_o;
+  } else {
+    to = tile / tiles_i;
+    ti = tile % tiles_i;
+  }
+  const int o0 = to * kBM, i0 = ti * kBN;
+  const int steps = (tokens + kBK - 1) / kBK;
+  const int s_first = split * steps_per_split;
+  const int s_last = (s_first + steps_per_split < steps) ? s_first + steps_per_split : steps;
+  const int t_end = (s_last * kBK < tokens) ? s_last * kBK : tokens;  // tokens of this split end here
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const auto g_r = rsrc(g, (uint32_t)((int64_t)tokens * out_f * 2));
+  const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * in_f * 2));
+
+  // global -> register -> LDS: g chunk c = tid + 512 h (row c / 32, features 8 (c % 32)),
+  // x chunk c = tid + 512 h (row c / 16, features 8 (c % 16))
+  u32x4 gr[kGChunks], xr[kXChunks];
+  auto load_step = [&](int s) {
+    const int t0 = s * kBK;
+#pragma unroll
+    for (int h = 0; h < kGChunks; ++h) {
+      const int c = tid + kGemmThreads * h;
+      gr[h] = load_chunk<kVecG>(g_r, t0 + (c >> 5), o0 + 8 * (c & 31), t_end, out_f, out_f);
+    }
+#pragma unroll
+    for (int h = 0; h < kXChunks; ++h) {
+      const int c = tid + kGemmThreads * h;
+      xr[h] = load_chunk<kVecX>(x_r, t0 + (c >> 4), i0 + 8 * (c & 15), t_end, in_f, in_f);
+    }
+  };
+  auto store_step = [&](int stage) {
+    unsigned char* sg = lds + stage * kStage;
+    unsigned char* sx = sg + kGStage;
+#pragma unroll
+    for (int h = 0; h < kGChunks; ++h) {
+      const int c = tid + kGemmThreads * h;
+      *reinterpret_cast<u32x4*>(sg + ((c >> 5) * kGPitch + 8 * (c & 31)) * 2) = gr[h];
+    }
+#pragma unroll
+    for (int h = 0; h < kXChunks; ++h) {
+      const int c = tid + kGemmThreads * h;
+      *reinterpret_cast<u32x4*>(sx + ((c >> 4) * kXPitch + 8 * (c & 15)) * 2) = xr[h];
+    }
+  };
+
+  // transposed-read addresses within a stage (bytes): lane group G = lane / 16
+  // supplies MFMA lanes 16 G .. 16 G + 15 (row / column 16 (G & 1) + j of a
+  // 32-wide operand, tokens 8 (G >> 1) + 0..7 of a 16-token k step)
+  const int j = lane & 15, G = lane >> 4;
+  const int krow = 8 * (G >> 1) + (j >> 2);     // + 16 kk + 4 r
+  const int fcol = 16 * (G & 1) + 4 * (j & 3);  // + 32 (tile within the wave)
+  const int wo = wave >> 1, wi = wave & 1;
+  const int a_off = (krow * kGPitch + wo * 64 + fcol) * 2;
+  const int b_off = kGStage + (krow * kXPitch + wi * 64 + fcol) * 2;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+
+  // A operand (g rows) and B operand (x columns) of k step kk: two transposed
+  // reads each, tokens 0-3 and 4-7 of the lane's eight
+  auto read_ops = [&](const unsigned char* st, int kk, u32x4 (&a)[2], u32x4 (&b)[2]) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const u32x2v lo = read_tr(st, a_off + ((16 * kk) * kGPitch + 32 * m) * 2);
+      const u32x2v hi = read_tr(st, a_off + ((16 * kk + 4) * kGPitch + 32 * m) * 2);
+      a[m] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+#pragma unroll
+    for (int nn = 0; nn < 2; ++nn) {
+      const u32x2v lo = read_tr(st, b_off + ((16 * kk) * kXPitch + 32 * nn) * 2);
+      const u32x2v hi = read_tr(st, b_off + ((16 * kk + 4) * kXPitch + 32 * nn) * 2);
+      b[nn] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
+  auto mfmas = [&](const u32x4 (&a)[2], const u32x4 (&b)[2]) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int nn = 0; nn < 2; ++nn) acc[m][nn] = mfma(a[m], b[nn], acc[m][nn]);
+  };
+
+  if (s_first < s_last) {
+    load_step(s_first);
+    store_step(0);
+  }
+  __syncthreads();
+  for (int s = s_first; s < s_last; ++s) {
+    const int cur = (s - s_first) & 1;
+    const bool more = s + 1 < s_last;
+    if (more) load_step(s + 1);  // in flight while this step multiplies
+    const unsigned char* st = lds + cur * kStage;
+    // operands of k step kk + 1 are read while the MFMAs of kk run (two register
+    // sets; the scheduling barriers keep the compiler from folding them into one)
+    u32x4 a0[2], b0[2], a1[2], b1[2];
+    read_ops(st, 0, a0, b0);
+    read_ops(st, 1, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_ops(st, 2, a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_ops(st, 3, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(a1, b1);
+    if (more) store_step(cur ^ 1);  // that stage was last read before the previous barrier
+    __syncthreads();
+  }
+
+  // D[row m][col n] of a 32 x 32 tile: lane holds n = lane % 32, registers
+  // e = 0..15 at m = 8 (e / 4) + 4 (lane / 32) + e % 4
+  float* ps = part + (int64_t)split * pstride;
+  const int n_l = lane & 31, r_l = 4 * (lane >> 5);
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int nn = 0; nn < 2; ++nn) {
+      const int col = i0 + wi * 64 + 32 * nn + n_l;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = o0 + wo * 64 + 32 * m + 8 * (e >> 2) + r_l + (e & 3);
+        if (row < out_f && col < in_f) ps[(int64_t)row * in_f + col] = acc[m][nn][e];
+      }
+    }
+}
+
+// grad_weight for the adjoint: gw[q] = bf16(scale * sum_s P_s[q]) in a fixed
+// order of s, zero for size <= q < total (whole blocks); 8 positions per thread.
+__global__ __launch_bounds__(256) void bfht_wgrad_sum(const float* __restrict__ part, int splits, int64_t pstride,
+                                                      int64_t size, int64_t total, float scale,
+                                                      __bf16* __restrict__ gw) {
+  const int64_t q = 8 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+  if (q >= total) return;
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  if (q < size) {
+    const int off = (int)(q * 4);  // pstride * 4 < 2^31 (host check)
+    for (int sb = 0; sb < splits; sb += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {  // partials past the last read 0 (empty buffer range)
+        const auto p_r = rsrc(part + (int64_t)(sb + u) * pstride, sb + u < splits ? (uint32_t)(pstride * 4) : 0u);
+        s0 += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p_r, off, 0, 0));
+        s1 += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p_r, off + 16, 0, 0));
+      }
+    }
+    if (q + 8 > size) {  // straddles the end of grad_weight (the partials' padding is not written)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (q + e >= size) s0[e] = 0.f;
+        if (q + 4 + e >= size) s1[e] = 0.f;
+      }
+    }
+  }
+  *reinterpret_cast<u32x4*>(gw + q) = u32x4{pk(scale * s0[0], scale * s0[1]), pk(scale * s0[2], scale * s0[3]),
+                                            pk(scale * s1[0], scale * s1[1]), pk(scale * s1[2], scale * s1[3])};
 }
 
 struct BwdPlan {
-  int64_t steps;   // token steps of 32 (tokens zero-padded)
-  int64_t itiles;  // in_features / 16
-  size_t partial_bytes, xt_bytes, gt_bytes;
+  int tiles_o, tiles_i, splits, steps_per_split;
+  int64_t pstride;  // floats between partials (in * out rounded up to 64)
+  int64_t total;    // whole blocks of grad_weight: nblocks * B
+  size_t part_bytes, gw_bytes, rows_bytes;
 };
 
 BwdPlan bwd_plan(const LinearBwdArgs& a) {
   BwdPlan p;
-  p.steps = (a.tokens + kTokStep - 1) / kTokStep;
-  p.itiles = a.in_features / 16;
+  p.tiles_o = (int)((a.out_features + kBM - 1) / kBM);
+  p.tiles_i = (int)((a.in_features + kBN - 1) / kBN);
+  const int64_t tiles = (int64_t)p.tiles_o * p.tiles_i;
+  const int64_t steps = (a.tokens + kBK - 1) / kBK;
+  int64_t want = tiles >= 256 ? 1 : 256 / tiles;  // fill the 256 CUs
+  if (want > steps) want = steps;
+  if (want < 1) want = 1;
+  p.steps_per_split = (int)((steps + want - 1) / want);
+  p.splits = p.steps_per_split > 0 ? (int)((steps + p.steps_per_split - 1) / p.steps_per_split) : 1;
+  if (p.splits < 1) p.splits = 1;
+  const int64_t size = a.in_features * a.out_features;
+  p.pstride = (size + 63) / 64 * 64;
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-  p.partial_bytes = al((size_t)a.nblocks_w * (size_t)a.token_splits * (size_t)a.n * 4);
-  p.xt_bytes = al((size_t)p.itiles * (size_t)p.steps * 1024);
-  p.gt_bytes = al((size_t)a.out_features * (size_t)p.steps * kTokStep * 2);
+  p.total = a.nblocks_w * kB;
+  p.part_bytes = al((size_t)p.splits * (size_t)p.pstride * 4);
+  p.gw_bytes = al((size_t)p.total * 2);
+  // the backward's per-block partial rows (bf16 rows padded to 8 values on the
+  // matrix cores; float32 rows of n on the other whole-block kernels)
+  const size_t row = std::max((size_t)a.n * 4, (size_t)mfma15_part_stride(a.n) * 2);
+  p.rows_bytes = al((size_t)a.nblocks_w * row);
   return p;
-}
-
-// x [tokens, in] -> xt: for column tile I and token step s, 64 16-byte chunks,
-// chunk (l16 + 16*kq) = x[32 s + 8 kq .. +7][16 I + l16] (zero past the end).
-// Grid (steps, ceil(in / 128)); each workgroup moves a 32-token x 128-column
-// tile through LDS: row-contiguous loads, chunk-contiguous stores.
-__global__ __launch_bounds__(256) void bwd_tile_x(const __bf16* __restrict__ x, u32x4* __restrict__ xt,
-                                                  int tokens, int in_f, int steps, int itiles) {
-  constexpr int kPitch = 136;  // bf16 per LDS row (128 + 8: rows start on different banks)
-  __shared__ __attribute__((aligned(16))) uint16_t tile[kTokStep * kPitch];
-  const int s = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
-  const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * in_f * 2));
-  {
-    const int r = t >> 3, cg = t & 7;  // token row, 16-column group
-    const int tok = s * kTokStep + r, col = c * 128 + cg * 16;
-    const bool ok = tok < tokens && col < in_f;  // in % 16 == 0: a group is all in or all out
-    const int off = ok ? (tok * in_f + col) * 2 : (int)0x80000000;
-    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(x_r, off, 0, 0);
-    const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(x_r, ok ? off + 16 : off, 0, 0);
-    u32x4* dst = reinterpret_cast<u32x4*>(tile + r * kPitch + cg * 16);
-    dst[0] = v0;
-    dst[1] = v1;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int q = h * 256 + t;                       // chunk of this workgroup's 8 column tiles
-    const int il = q >> 6, lane = q & 63;
-    const int I = c * 8 + il;
-    const int col = il * 16 + (lane & 15), r0 = 8 * (lane >> 4);
-    u32x4 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v[e] = (uint32_t)tile[(r0 + 2 * e) * kPitch + col] | ((uint32_t)tile[(r0 + 2 * e + 1) * kPitch + col] << 16);
-    if (I < itiles) xt[((int64_t)I * steps + s) * 64 + lane] = v;
-  }
-}
-
-// g [tokens, out] -> gt [out, steps * 32] (token-contiguous rows, zero-padded).
-// Grid (steps, ceil(out / 128)); a 32-token x 128-row tile through LDS.
-__global__ __launch_bounds__(256) void bwd_transpose_g(const __bf16* __restrict__ g, __bf16* __restrict__ gt,
-                                                       int tokens, int out_f, int steps) {
-  constexpr int kPitch = 130;  // bf16 per LDS row (odd word pitch)
-  __shared__ uint16_t tile[kTokStep * kPitch];
-  const int s = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
-  const auto g_r = rsrc(g, (uint32_t)((int64_t)tokens * out_f * 2));
-#pragma unroll
-  for (int h = 0; h < 16; ++h) {  // element (row r, column o): consecutive threads, consecutive o
-    const int idx = h * 256 + t;
-    const int r = idx >> 7, ol = idx & 127;
-    const int tok = s * kTokStep + r, o = c * 128 + ol;
-    const bool ok = tok < tokens && o < out_f;
-    tile[r * kPitch + ol] = __builtin_amdgcn_raw_buffer_load_b16(g_r, ok ? (tok * out_f + o) * 2 : (int)0x80000000,
-                                                                 0, 0);
-  }
-  __syncthreads();
-  const int64_t pitch = (int64_t)steps * kTokStep;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int q = h * 256 + t;
-    const int ol = q >> 2, kq = q & 3;  // row o, token group of 8
-    const int o = c * 128 + ol;
-    u32x4 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v[e] = (uint32_t)tile[(8 * kq + 2 * e) * kPitch + ol] | ((uint32_t)tile[(8 * kq + 2 * e + 1) * kPitch + ol] << 16);
-    if (o < out_f) *reinterpret_cast<u32x4*>(gt + o * pitch + s * kTokStep + 8 * kq) = v;
-  }
-}
-
-// Main kernel.  NT row tiles of 16 per block (rows o_first .. o_last), IC
-// column tiles per wave per pass (NT * IC <= 9 keeps accumulators and two
-// steps of operands in registers): wave w owns column tiles w, w + 8, w + 16,
-// ... and takes them IC at a time; each pass streams the workgroup's token
-// steps once (x tiles are read once per workgroup in total).
-template <int L, int NT, int IC>
-__global__ __launch_bounds__(kThreads) void bfht_linear_bwd_mfma15(const u32x4* __restrict__ xt,
-                                                                   const __bf16* __restrict__ gt,
-                                                                   float* __restrict__ partial, int tokens,
-                                                                   int in_f, int out_f, int n, int steps,
-                                                                   int itiles, uint32_t seed32, float scale,
-                                                                   int token_split) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kChainLdsBytes];
-  const int64_t block = blockIdx.x / token_split;
-  const int split = blockIdx.x % token_split;
-  const int64_t size = (int64_t)in_f * out_f;
-  const int64_t g0 = block * kB;
-  const int64_t g1 = (g0 + kB < size) ? g0 + kB : size;
-  const int o_first = (int)(g0 / in_f);
-  const int o_last = (int)((g1 - 1) / in_f);
-  const int first_off = (int)((int64_t)o_first * in_f - g0);  // in (-in, 0]
-  const int per_split = (steps + token_split - 1) / token_split;
-  const int s0 = split * per_split;
-  const int s1 = (s0 + per_split < steps) ? s0 + per_split : steps;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l16 = lane & 15, kq = lane >> 4;
-  const int64_t pitch = (int64_t)steps * kTokStep;
-  const auto x_r = rsrc(xt, (uint32_t)((int64_t)itiles * steps * 1024));
-  const auto g_r = rsrc(gt, (uint32_t)((int64_t)out_f * pitch * 2));
-  constexpr uint32_t kOff = 0x80000000u;  // voffset that reads 0
-
-  // bf16 image of this block's slice of grad_weight (positions 0 .. B-1), in
-  // exchange buffer 0; positions no row of this workgroup covers stay 0
-  uint16_t* img = reinterpret_cast<uint16_t*>(lds);
-  for (int i = threadIdx.x; i < kB / 8; i += kThreads) reinterpret_cast<u32x4*>(img)[i] = u32x4{0u, 0u, 0u, 0u};
-  __syncthreads();
-
-  // A operand rows (one per row tile): gt row o_first + 16 nt + l16, 8 tokens at 8 kq
-  uint32_t ga[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int o = o_first + 16 * nt + l16;
-    ga[nt] = o < out_f ? (uint32_t)((o * pitch + 8 * kq) * 2) : kOff;
-  }
-  const int ipw = (itiles - wave + kWaves - 1) / kWaves;  // this wave's column tiles
-  for (int j0 = 0; j0 < ipw; j0 += IC) {
-    uint32_t xb[IC];
-#pragma unroll
-    for (int j = 0; j < IC; ++j) {
-      const int I = wave + kWaves * (j0 + j);
-      xb[j] = (j0 + j < ipw) ? (uint32_t)(((int64_t)I * steps * 64 + lane) * 16) : kOff;
-    }
-    f32x4v acc[NT][IC];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-      for (int j = 0; j < IC; ++j) acc[nt][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    // one step of prefetch: operands of step s + 1 load while step s multiplies
-    auto load = [&](int s, u32x4 (&a)[NT], u32x4 (&b)[IC]) {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        a[nt] = __builtin_amdgcn_raw_buffer_load_b128(g_r, (int)ga[nt], s * kTokStep * 2, 0);
-#pragma unroll
-      for (int j = 0; j < IC; ++j) b[j] = __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)xb[j], s * 1024, 0);
-    };
-    u32x4 a0[NT], b0[IC], a1[NT], b1[IC];
-    if (s0 < s1) load(s0, a0, b0);
-    for (int s = s0; s < s1; s += 2) {
-      if (s + 1 < s1) load(s + 1, a1, b1);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int j = 0; j < IC; ++j) acc[nt][j] = mfma16(a0[nt], b0[j], acc[nt][j]);
-      if (s + 1 >= s1) break;
-      if (s + 2 < s1) load(s + 2, a0, b0);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int j = 0; j < IC; ++j) acc[nt][j] = mfma16(a1[nt], b1[j], acc[nt][j]);
-    }
-    // D[m = 4 kq + r][n = l16] = grad_weight[o_first + 16 nt + m][16 I + n] over this token range;
-    // block position of (row o_first + ol, column i) = ol * in + i + first_off
-#pragma unroll
-    for (int j = 0; j < IC; ++j) {
-      if (j0 + j >= ipw) continue;
-      const int i = 16 * (wave + kWaves * (j0 + j)) + l16;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int ol = 16 * nt + 4 * kq + r;
-          const int p = ol * in_f + i + first_off;
-          if (ol <= o_last - o_first && p >= 0 && p < kB)
-            img[p] = __builtin_bit_cast(uint16_t, (__bf16)acc[nt][j][r]);
-        }
-    }
-  }
-  __syncthreads();
-
-  // adjoint chain on the image: D_0 H D_1 ... H D_L, then scale * D_0 row of n
-  const Ctx c = make_ctx(seed32, block);
-  u32x4 src[kTiles][2];
-  load_source(c, [&](int p) -> u32x4 { return *reinterpret_cast<const u32x4*>(img + p); }, src);
-  __syncthreads();  // the image is exchange buffer 0, rewritten by the first layer
-  f32x16 acc[kTiles];
-  uint32_t nw[4];
-  run_chain<L>(acc, c, lds, src, [](int i) { return L - i; }, nw);
-  write_partial_row<L, false>(acc, nw, c, lds, partial + (int64_t)blockIdx.x * n, n, scale);
-}
-
-template <int L>
-hipError_t launch_bwd_main(const LinearBwdArgs& a, const BwdPlan& p, const u32x4* xt, const __bf16* gt,
-                           float* partial, hipStream_t s) {
-  const int nt = (int)((kB + a.in_features - 1) / a.in_features + 1 + 15) / 16;
-  const dim3 grid((unsigned)(a.nblocks_w * a.token_splits)), block(kThreads);
-#define LWL_BWD(NT, IC)                                                                                          \
-  hipLaunchKernelGGL((bfht_linear_bwd_mfma15<L, NT, IC>), grid, block, 0, s, xt, gt, partial, (int)a.tokens,    \
-                     (int)a.in_features, (int)a.out_features, (int)a.n, (int)p.steps, (int)p.itiles, a.seed32,   \
-                     a.weight_scale, a.token_splits)
-  switch (nt) {
-    case 1: LWL_BWD(1, 8); break;
-    case 2: LWL_BWD(2, 4); break;
-    case 3: LWL_BWD(3, 3); break;
-    case 4: LWL_BWD(4, 2); break;
-    default: return hipErrorInvalidValue;
-  }
-#undef LWL_BWD
-  return hipGetLastError();
 }
 
 }  // namespace
 
 bool linear_bwd_applicable(int dtype, int log_block, int64_t in_features) {
-  // bf16 chain at B = 2^15; 16-column tiles (in % 16 == 0); at most 4 row tiles of 16 per block
-  if (dtype != kBF16 || log_block != mfma15::kLog || in_features % 16 != 0 || in_features > mfma15::kB) return false;
-  return ((mfma15::kB + in_features - 1) / in_features + 1 + 15) / 16 <= 4;
+  return dtype == kBF16 && log_block == mfma15::kLog && in_features > 0;
 }
 
-int linear_bwd_token_splits(const LinearBwdArgs& a) {
-  const int64_t steps = (a.tokens + kTokStep - 1) / kTokStep;
-  int64_t split = a.nblocks_w >= 256 ? 1 : 256 / a.nblocks_w;
-  if (split > steps) split = steps;
-  return (int)(split < 1 ? 1 : split);
-}
+int linear_bwd_token_splits(const LinearBwdArgs& a) { return bwd_plan(a).splits; }
 
 size_t linear_bwd_workspace_bytes(const LinearBwdArgs& a) {
   const BwdPlan p = bwd_plan(a);
-  return p.partial_bytes + p.xt_bytes + p.gt_bytes;
+  return p.part_bytes + p.gw_bytes + p.rows_bytes;
 }
 
 hipError_t launch_linear_bwd(const LinearBwdArgs& a, hipStream_t s) {
   const BwdPlan p = bwd_plan(a);
   auto* base = (unsigned char*)a.work;
-  float* partial = (float*)base;
-  auto* xt = (u32x4*)(base + p.partial_bytes);
-  auto* gt = (__bf16*)(base + p.partial_bytes + p.xt_bytes);
-  hipLaunchKernelGGL(bwd_tile_x, dim3((unsigned)p.steps, (unsigned)((a.in_features + 127) / 128)), dim3(256), 0, s,
-                     (const __bf16*)a.x, xt, (int)a.tokens, (int)a.in_features, (int)p.steps, (int)p.itiles);
+  float* part = (float*)base;
+  auto* gw = (__bf16*)(base + p.part_bytes);
+  void* rows = base + p.part_bytes + p.gw_bytes;
+  const bool vec_g = a.out_features % 8 == 0 && (uintptr_t)a.grad % 16 == 0;
+  const bool vec_x = a.in_features % 8 == 0 && (uintptr_t)a.x % 16 == 0;
+  const dim3 grid((unsigned)((int64_t)p.tiles_o * p.tiles_i * p.splits)), block(kGemmThreads);
+#define LWL_WGRAD(VG, VX)                                                                                        \
+  hipLaunchKernelGGL((bfht_wgrad_gemm<VG, VX>), grid, block, 0, s, (const __bf16*)a.grad, (const __bf16*)a.x,   \
+                     part, (int)a.tokens, (int)a.out_features, (int)a.in_features, p.tiles_o, p.tiles_i,         \
+                     p.splits, p.steps_per_split, p.pstride)
+  if (vec_g && vec_x) LWL_WGRAD(true, true);
+  else if (vec_g) LWL_WGRAD(true, false);
+  else if (vec_x) LWL_WGRAD(false, true);
+  else LWL_WGRAD(false, false);
+#undef LWL_WGRAD
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(bwd_transpose_g, dim3((unsigned)p.steps, (unsigned)((a.out_features + 127) / 128)), dim3(256),
-                     0, s, (const __bf16*)a.grad, gt, (int)a.tokens, (int)a.out_features, (int)p.steps);
+  hipLaunchKernelGGL(bfht_wgrad_sum, dim3((unsigned)((p.total / 8 + 255) / 256)), dim3(256), 0, s, part, p.splits,
+                     p.pstride, a.in_features * a.out_features, p.total, a.weight_scale, gw);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  switch (a.layers) {
-    case 1: e = launch_bwd_main<1>(a, p, xt, gt, partial, s); break;
-    case 2: e = launch_bwd_main<2>(a, p, xt, gt, partial, s); break;
-    case 3: e = launch_bwd_main<3>(a, p, xt, gt, partial, s); break;
-    default: return hipErrorInvalidValue;
-  }
-  if (e != hipSuccess) return e;
-  return launch_block_sum(partial, a.nblocks_w * a.token_splits, a.n, a.n, a.grad_latent, kBF16, s);
+  // the generator's backward over whole blocks: adjoint chains, then the fixed-order block sum
+  BfhtArgs b{};
+  b.dtype = kBF16;
+  b.src = gw;
+  b.dst = a.grad_latent;
+  b.work = rows;
+  b.n = a.n;
+  b.log_block = mfma15::kLog;
+  b.first_block = 0;
+  b.nblocks = a.nblocks_w;
+  b.start = 0;
+  b.stop = p.total;
+  b.seed32 = a.seed32;
+  b.layers = a.layers;
+  return launch_bfht(b, s, false);
 }
 
 }  // namespace lwl

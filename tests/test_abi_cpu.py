@@ -210,12 +210,12 @@ def ceil_div(a, b):
         ((2, 4096, 3072, 32768, 768, 3), N.LWL_OK, ""),
         ((2, 0, 768, 32768, 3072, 3), N.LWL_OK, ""),
         ((0, 16, 768, 32768, 3072, 3), N.LWL_ERR_UNSUPPORTED, "bfloat16"),     # fp32: grad_weight in HBM
-        ((2, 16, 520, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "in_features"),    # > 4 row tiles per block
-        ((2, 16, 776, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "in_features"),    # in % 16 != 0
+        ((2, 16, 520, 32768, 64, 3), N.LWL_OK, ""),                          # any in_features
+        ((2, 16, 77, 32768, 33, 3), N.LWL_OK, ""),                           # rows off the 16-byte grid
         ((2, 16, 768, 8192, 64, 3), N.LWL_ERR_UNSUPPORTED, "block 2^15"),      # block 2^13
         ((2, 16, 768, 32768, 64, 0), N.LWL_ERR_INVALID, "layers must be 1, 2, or 3"),
         ((2, 1 << 20, 1024, 32768, 64, 3), N.LWL_ERR_UNSUPPORTED, "2^30"),
-        ((2, 16, 768, 32768, 1 << 24, 3), N.LWL_ERR_UNSUPPORTED, "2^23"),   # > 65535 re-layout grid rows
+        ((2, 16, 768, 32768, 1 << 20, 3), N.LWL_ERR_UNSUPPORTED, "2^29"),   # float32 partials past 2 GiB
     ],
 )
 def test_linear_backward_latent_validation(args, code, msg):
@@ -226,11 +226,14 @@ def test_linear_backward_latent_validation(args, code, msg):
 
 
 def test_linear_backward_latent_workspace_size():
-    # 216 partial rows of 32768 floats (72 blocks x 3 token ranges), x in 48 column tiles x 128
-    # token steps of 1 KiB, g transposed to 3072 rows of 4096 tokens
+    # 72 tiles of 256 x 128 -> 3 token splits of float32 grad_weight partials (3 x 768 x 3072),
+    # their bf16 sum over 72 whole blocks, then the backward's 72 block rows (float32-sized)
     lib = N.lib()
     assert lib.lwl_bfht_linear_backward_latent_workspace_size(4096, 768, 3072, 32768) == (
-        216 * 32768 * 4 + 48 * 128 * 1024 + 3072 * 4096 * 2)
+        3 * 768 * 3072 * 4 + 72 * 32768 * 2 + 72 * 32768 * 4)
+    # 2 x 1 tiles, 4 token steps -> 4 splits of 77 * 300 floats (padded to 64), 1 block
+    assert lib.lwl_bfht_linear_backward_latent_workspace_size(200, 77, 300, 32768) == (
+        4 * ceil_div(77 * 300, 64) * 64 * 4 + 32768 * 2 + 32768 * 4)
 
 
 def weight_job(n, size, ld=0, wd=0, layers=2, ptr=0x10000, **kw):

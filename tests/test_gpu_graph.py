@@ -123,3 +123,18 @@ def test_graph_noalloc_backward_and_mix():
         return [gl, ops.fht_mix(x, signs)]
 
     check_graph(fn)
+
+
+def test_graph_linear_latent_gradient():
+    g = torch.Generator(device="cuda").manual_seed(5)
+    lat = torch.randn(32768, device="cuda", generator=g).to(torch.bfloat16)
+    x = torch.randn(300, 768, device="cuda", generator=g).to(torch.bfloat16)
+    gr = torch.randn(300, 3072, device="cuda", generator=g).to(torch.bfloat16)
+    x77 = torch.randn(50, 77, device="cuda", generator=g).to(torch.bfloat16)
+    g77 = torch.randn(50, 300, device="cuda", generator=g).to(torch.bfloat16)
+
+    def fn():
+        return [ops.linear_backward_latent(gr, x, lat, 3072, 3, 3, 0.5),      # split-K over 5 token steps
+                ops.linear_backward_latent(g77, x77, lat, 300, 2, 13, 1.0)]   # element loads
+
+    check_graph(fn)

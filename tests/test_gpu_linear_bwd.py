@@ -1,11 +1,13 @@
 """GPU parity of the fused BlockFHTLinear latent gradient (the grad_latent branch of
 the reference's _BlockFHTLinearFn.backward, latent_weight_lab/block_fht.py:339-352).
 
-The fused kernel forms grad_weight = grad^T @ input block by block on chip and runs
-the adjoint BlockFHT on it; it is checked against the oracle: grad_weight in float64
-from the same bf16 inputs, then the C oracle's slice backward over size = in * out.
-Bar: bf16 1e-2 relative L2 (the tile of grad_weight is rounded
-to bf16 before the transform, as the reference casts it to the latent dtype).
+The fused path forms grad_weight = grad^T @ input as float32 token-split partial sums
+(split-K matrix-core GEMM) and runs the adjoint BlockFHT on their sum per block; it is
+checked against the oracle: grad_weight in float64 from the same bf16 inputs, then the
+C oracle's slice backward over size = in * out.  Bar: bf16 1e-2 relative L2 (BASELINE
+north star; grad_weight is rounded to bf16 before the transform, as the reference's
+grad_weight is bf16).  Shapes cover row lengths off the 16-byte grid (element loads),
+ragged token splits and partial tiles on both sides.
 """
 from __future__ import annotations
 
@@ -38,6 +40,9 @@ def oracle_grad_latent(g: torch.Tensor, x: torch.Tensor, n: int, layers: int, se
         (33, 528, 77, 20000, 1, -3, 2.0),       # smallest in_features: 4 row tiles per block
         (1, 768, 768, 32768, 3, 9, 1.0),        # a single token
         (257, 2048, 40, 32768, 3, 11, 1.0),     # rows of 2048 (16 per block), 2 row tiles
+        (50, 77, 300, 32768, 2, 13, 1.0),       # in_features off the 16-byte grid (element loads of x)
+        (1000, 1024, 1024, 32768, 2, 7, 1.0),   # 8 token splits, the last one short
+        (70, 40, 2000, 30000, 3, 17, 0.25),     # narrow rows: 2000 tiles rows of 40
     ],
 )
 def test_fused_latent_grad_matches_oracle(tokens, in_f, out_f, n, layers, seed, scale):
