@@ -357,8 +357,9 @@ def extra_configs(abi, steps, warmup, only):
                     rows[f"{tag}_tokens_{tokens}"] = {"error": f"{type(exc).__name__}: {exc}"}
         res["c4_ref_domain"] = rows
 
-    # config 4 training step, latent gradient: fused (grad_weight formed per block on chip) vs
-    # grad_weight = g^T x on hipBLASLt in HBM followed by the generator backward
+    # config 4 training step, latent gradient: one lwl_bfht_linear_backward_latent call (split-K
+    # matrix-core g^T x into float32 partials, their sum, the generator backward) vs the reference's
+    # composition, grad_weight = g^T x on hipBLASLt followed by the generator backward
     if want("c4_linear_bwd"):
         lin = {}
         for inf, outf in ((768, 3072), (3072, 768)):

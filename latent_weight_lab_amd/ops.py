@@ -195,8 +195,9 @@ def linear_backward_latent_supported(in_features: int, out_features: int, latent
 
 def linear_backward_latent(grad2d: torch.Tensor, x2d: torch.Tensor, latent: torch.Tensor, out_features: int,
                            layers: int, seed: int, weight_scale: float) -> torch.Tensor:
-    """``weight_scale * block_fht_grad_latent(latent, (grad2d^T x2d).flatten(), ...)`` with the weight
-    gradient formed block by block on chip (the grad_latent branch of the reference's
+    """``weight_scale * block_fht_grad_latent(latent, (grad2d^T x2d).flatten(), ...)`` in one library
+    call: the weight gradient on the library's split-K matrix-core GEMM (float32 partials in the
+    workspace), then the generator's backward (the grad_latent branch of the reference's
     ``_BlockFHTLinearFn.backward``, ``block_fht.py:339-350``; the modulation term is the caller's)."""
     dev = N.require_cuda(grad2d, x2d, latent)
     grad2d = grad2d.contiguous()

@@ -86,3 +86,19 @@ def test_module_backward_uses_fused_gradient():
     gw = g2.t().float().matmul(x.reshape(-1, 768).float())
     want = block_fht_grad_latent(lin.generator.latent.detach().float(), gw.reshape(-1), 768 * 1024, 3, 21)
     assert O.rel_l2(got, want.double().cpu().numpy()) < 1e-2
+
+
+def test_misaligned_operands_take_element_loads():
+    """x and g as views one element past a 16-byte boundary (the GEMM's element-load path):
+    same values as 16-byte aligned copies, to the bit."""
+    gen = torch.Generator().manual_seed(31)
+    tokens, in_f, out_f, n = 300, 768, 1024, 32768
+    latent = torch.randn(n, generator=gen).to(torch.bfloat16).cuda()
+    xb = torch.randn(tokens * in_f + 1, generator=gen).to(torch.bfloat16).cuda()
+    gb = torch.randn(tokens * out_f + 1, generator=gen).to(torch.bfloat16).cuda()
+    x = xb[1:].view(tokens, in_f)
+    g = gb[1:].view(tokens, out_f)
+    assert x.data_ptr() % 16 == 2 and g.data_ptr() % 16 == 2
+    got = ops.linear_backward_latent(g, x, latent, out_f, 3, 7, 1.0)
+    want = ops.linear_backward_latent(g.clone(), x.clone(), latent, out_f, 3, 7, 1.0)
+    assert torch.equal(got, want)
