@@ -41,6 +41,40 @@ __device__ __forceinline__ void buf_store(float v, __amdgpu_buffer_rsrc_t r, int
                                           1 | 16);
   }
 }
+// The same at element base + c with base >= 0 per lane and c a wave-uniform
+// constant: c goes into the scalar offset, which the range check does not
+// cover, so these are only for accesses known to be in range (whole blocks).
+template <class T>
+__device__ __forceinline__ float buf_load_at(__amdgpu_buffer_rsrc_t r, int base, int c) {
+  const int vo = (int)((uint32_t)base * (uint32_t)sizeof(T)), so = c * (int)sizeof(T);
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+  } else {
+    const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0);
+    return to_f32(__builtin_bit_cast(T, h));
+  }
+}
+template <class T>
+__device__ __forceinline__ void buf_store_at(float v, __amdgpu_buffer_rsrc_t r, int base, int c) {
+  const int vo = (int)((uint32_t)base * (uint32_t)sizeof(T)), so = c * (int)sizeof(T);
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, vo, so, 1 | 16);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), r, vo, so, 1 | 16);
+  }
+}
+// Element base + c with base >= 0 per lane and c >= 0 constant, range-checked
+// (positions past the buffer are dropped / read 0): both in the lane offset,
+// where a small c folds into the instruction's immediate offset.
+template <class T>
+__device__ __forceinline__ void buf_store_nn(float v, __amdgpu_buffer_rsrc_t r, int base, int c) {
+  const int vo = (int)((uint32_t)(base + c) * (uint32_t)sizeof(T));
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, vo, 0, 1 | 16);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), r, vo, 0, 1 | 16);
+  }
+}
 
 // ---------------------------------------------------------------- whole block
 
@@ -129,8 +163,8 @@ __device__ __forceinline__ void block_bwd_small(Load grad, float* __restrict__ p
 // between consecutive groups.  Even layers run the groups in that order, odd
 // layers in reverse, so a layer boundary needs no exchange: the sign layer
 // between them is applied in whatever layout the data is in, from a table of
-// the block's sign words in LDS (hashed once per block, one word per thread and
-// layer).  The block is read and written in the coalesced layout (or, after an
+// the block's inverted sign words in LDS (hashed once per block, one word per
+// thread and layer).  The block is read and written in the coalesced layout (or, after an
 // odd number of layers, in the last group's layout when that keeps 32
 // consecutive positions per half wave).
 template <int LB>
@@ -154,8 +188,10 @@ struct BlockLds {
   static constexpr int FLOATS = Gm::NG > 1 ? Gm::G * (Gm::PADDED + kSignTableLayers * Gm::TB) : 1;
   __device__ static float* data(float* smem, int gi) { return smem + gi * Gm::PADDED; }
   __device__ static uint32_t* table(float* smem, int gi) {
-    return reinterpret_cast<uint32_t*>(smem + Gm::G * Gm::PADDED) + gi * kSignTableLayers * Gm::TB;
+    return reinterpret_cast<uint32_t*>(smem) + table_word(gi);
   }
+  // word index of group gi's table from the start of smem
+  __device__ static int table_word(int gi) { return Gm::G * Gm::PADDED + gi * kSignTableLayers * Gm::TB; }
 };
 
 // Register exchange from group layout (lo_a, nb_a) to (lo_b, nb_b) through LDS.
@@ -171,20 +207,49 @@ __device__ __forceinline__ void exchange(float (&v)[32], float* lds, int t, int 
   for (int r = 0; r < 32; ++r) v[r] = lds[group_lds<LB, 5>(rb, r, lo_b, nb_b)];
 }
 
+// x with its sign bit XOR-ed with bit 31 of m (one v_bitop3).
+__device__ __forceinline__ float flip_by_msb(float x, uint32_t m) {
+  return __uint_as_float(__float_as_uint(x) ^ (m & 0x80000000u));
+}
+
 // Sign layer in layout (lo, nb): v[r] negated where the bit of its position is
-// clear (word p >> 5 of the layer's table, bit p & 31), as an XOR of the float's
-// sign bit.  Position = per-thread base OR a per-register constant (disjoint
-// bits), so word index and bit split the same way.  The 2^(-LB/2) of every layer
-// is applied once, at the end (transform_scale).
+// set in the layer's flip table (word p >> 5, bit p & 31; the table holds the
+// sign words inverted), as an XOR of the float's sign bit.  Position = per-thread
+// base OR a per-register constant (disjoint bits), so word index and bit split
+// the same way.  When the group starts at bit 5 or above, every register's bit
+// is the thread's base & 31, and the words of two registers are shifted
+// together by one 64-bit shift (each dword's bit 31 is its own word's bit: the
+// low word's bits shifted into the high dword stay below bit 31).  The
+// 2^(-LB/2) of every layer is applied once, at the end (transform_scale).
 template <int LB>
-__device__ __forceinline__ void sign_flip(float (&v)[32], const uint32_t* words, int t, int lo, int nb) {
+__device__ __forceinline__ void sign_flip(float (&v)[32], const uint32_t* smem_words, int table, int t, int lo,
+                                          int nb) {
   const int base = group_pos<LB, 5>(t, 0, lo, nb);
+  // The table sits above the exchange buffer (beyond the 64 KiB the LDS
+  // instructions' offset field reaches): its index is opaque to the compiler,
+  // so it is added once and the per-register word offsets fold into the reads.
+  int first = table + (base >> 5);
+  asm("" : "+v"(first));
+  const uint32_t* flips = smem_words + first - (base >> 5);
+  if (lo >= 5) {
+    const uint32_t s = 31u - (uint32_t)(base & 31);
 #pragma unroll
-  for (int r = 0; r < 32; ++r) {
-    const int c = group_pos<LB, 5>(0, r, lo, nb);
-    const uint32_t w = ~words[(base >> 5) + (c >> 5)];
-    const int bit = (base & 31) | (c & 31);
-    v[r] = __uint_as_float(__float_as_uint(v[r]) ^ ((w << (31 - bit)) & 0x80000000u));
+    for (int r = 0; r < 32; r += 2) {
+      const int c0 = group_pos<LB, 5>(0, r, lo, nb), c1 = group_pos<LB, 5>(0, r + 1, lo, nb);
+      const uint64_t pair = (uint64_t)flips[(base >> 5) + (c0 >> 5)] |
+                            ((uint64_t)flips[(base >> 5) + (c1 >> 5)] << 32);
+      uint64_t m;
+      asm("v_lshlrev_b64 %0, %1, %2" : "=v"(m) : "v"(s), "v"(pair));
+      v[r] = flip_by_msb(v[r], (uint32_t)m);
+      v[r + 1] = flip_by_msb(v[r + 1], (uint32_t)(m >> 32));
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      const int c = group_pos<LB, 5>(0, r, lo, nb);
+      const int bit = (base & 31) | (c & 31);
+      v[r] = flip_by_msb(v[r], flips[(base >> 5) + (c >> 5)] << (31 - bit));
+    }
   }
 }
 
@@ -219,9 +284,11 @@ __device__ __forceinline__ void layer_fht(float (&v)[32], float* lds, int t, boo
   }
 }
 
+// Flip table: the block's sign words of layers 0..layers, inverted (a set bit
+// negates its position), one word per thread and layer.
 template <int LB>
 __device__ __forceinline__ void fill_sign_table(uint32_t* tab, uint32_t bkey, int t, int layers) {
-  for (int l = 0; l <= layers; ++l) tab[l * Geo<LB>::TB + t] = sign_word(bkey, layer_key(l), (uint32_t)t);
+  for (int l = 0; l <= layers; ++l) tab[l * Geo<LB>::TB + t] = ~sign_word(bkey, layer_key(l), (uint32_t)t);
 }
 
 // Forward of block slot `slot` (block first_block + slot of one generator) by
@@ -247,17 +314,24 @@ __device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Sto
     // positions >= n read 0 (buffer range)
     const auto lat_r = tile_rsrc(latent, (uint64_t)n * sizeof(T));
     float v[32];
+    if (n >= Gm::B) {  // every position in range: register offsets in the scalar offset
 #pragma unroll
-    for (int r = 0; r < 32; ++r) v[r] = buf_load<T>(lat_r, r * Gm::TB + t);
+      for (int r = 0; r < 32; ++r) v[r] = buf_load_at<T>(lat_r, t, r * Gm::TB);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 32; ++r) v[r] = buf_load<T>(lat_r, r * Gm::TB + t);
+    }
     __syncthreads();  // the sign table is complete
-    sign_flip<LB>(v, tab, t, S::lo(0), S::nb(0));
+    const uint32_t* words = reinterpret_cast<const uint32_t*>(smem);
+    const int tw = BlockLds<LB>::table_word(gi);
+    sign_flip<LB>(v, words, tw, t, S::lo(0), S::nb(0));
     for (int layer = 0; layer < layers; ++layer) {
       const bool odd = layer & 1;
       layer_fht<LB>(v, lds, t, odd);
       if (odd)
-        sign_flip<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(0), S::nb(0));
+        sign_flip<LB>(v, words, tw + (layer + 1) * Gm::TB, t, S::lo(0), S::nb(0));
       else
-        sign_flip<LB>(v, tab + (layer + 1) * Gm::TB, t, S::lo(S::N - 1), S::nb(S::N - 1));
+        sign_flip<LB>(v, words, tw + (layer + 1) * Gm::TB, t, S::lo(S::N - 1), S::nb(S::N - 1));
     }
     const float scale = transform_scale<LB>(layers);
     // store from the layout the last layer ended in
@@ -269,10 +343,16 @@ __device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Sto
       const int pb = group_pos<LB, 5>(t, 0, glo, gnb);
       if constexpr (Gm::TB >= 64) {
         // one block per wave: a uniform buffer resource over the block's range,
-        // positions outside [lo, hi) dropped by its range check
+        // positions outside [lo, hi) dropped by its range check; a whole block
+        // (the wave-uniform common case) stores without per-element checks
         const auto out_r = out.range(base + lo - start, hi - lo);
+        if (lo == 0 && hi == Gm::B) {
 #pragma unroll
-        for (int r = 0; r < 32; ++r) out(out_r, pb + group_pos<LB, 5>(0, r, glo, gnb) - (int)lo, v[r] * scale);
+          for (int r = 0; r < 32; ++r) out.whole(out_r, pb, group_pos<LB, 5>(0, r, glo, gnb), v[r] * scale);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 32; ++r) out(out_r, pb + group_pos<LB, 5>(0, r, glo, gnb) - (int)lo, v[r] * scale);
+        }
       } else {
 #pragma unroll
         for (int r = 0; r < 32; ++r) {
@@ -320,8 +400,13 @@ __device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ pa
     float v[32];
     if constexpr (Gm::TB >= 64) {
       const auto g_r = grad.range(base + lo - start, active ? hi - lo : 0);
+      if (active && lo == 0 && hi == Gm::B) {  // a whole block: no per-element checks
 #pragma unroll
-      for (int r = 0; r < 32; ++r) v[r] = grad(g_r, r * Gm::TB + t - (int)lo);
+        for (int r = 0; r < 32; ++r) v[r] = grad.whole(g_r, t, r * Gm::TB);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) v[r] = grad(g_r, r * Gm::TB + t - (int)lo);
+      }
     } else {
       // several blocks per wave: element loads from a valid index (the slice's
       // first element stands in for positions outside it), then a select
@@ -334,15 +419,17 @@ __device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ pa
       }
     }
     __syncthreads();  // the sign table is complete
-    sign_flip<LB>(v, tab + layers * Gm::TB, t, S::lo(0), S::nb(0));
+    const uint32_t* words = reinterpret_cast<const uint32_t*>(smem);
+    const int tw = BlockLds<LB>::table_word(gi);
+    sign_flip<LB>(v, words, tw + layers * Gm::TB, t, S::lo(0), S::nb(0));
     for (int i = 0; i < layers; ++i) {
       const bool odd = i & 1;
       layer_fht<LB>(v, lds, t, odd);
-      const uint32_t* words = tab + (layers - 1 - i) * Gm::TB;
+      const int lw = tw + (layers - 1 - i) * Gm::TB;
       if (odd)
-        sign_flip<LB>(v, words, t, S::lo(0), S::nb(0));
+        sign_flip<LB>(v, words, lw, t, S::lo(0), S::nb(0));
       else
-        sign_flip<LB>(v, words, t, S::lo(S::N - 1), S::nb(S::N - 1));
+        sign_flip<LB>(v, words, lw, t, S::lo(S::N - 1), S::nb(S::N - 1));
     }
     const float scale = transform_scale<LB>(layers);
     auto write = [&](int glo, int gnb) {
@@ -354,11 +441,11 @@ __device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ pa
                                 : tile_rsrc(partial + slot * stride, (uint64_t)n * 4);
 #pragma unroll
         for (int r = 0; r < 32; ++r) {
-          const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
+          const int c = group_pos<LB, 5>(0, r, glo, gnb);  // disjoint from pb's bits
           if (direct)
-            buf_store<T>(v[r] * scale, d_r, p);
+            buf_store_nn<T>(v[r] * scale, d_r, pb, c);
           else
-            buf_store<float>(v[r] * scale, d_r, p);
+            buf_store_nn<float>(v[r] * scale, d_r, pb, c);
         }
       } else {
 #pragma unroll

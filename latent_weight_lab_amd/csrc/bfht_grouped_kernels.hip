@@ -23,6 +23,9 @@ struct WeightStore {
     return tile_rsrc(out + first, (uint64_t)count * sizeof(W));
   }
   __device__ void operator()(__amdgpu_buffer_rsrc_t r, int i, float v) const { buf_store<W>(value(v), r, i); }
+  __device__ void whole(__amdgpu_buffer_rsrc_t r, int base, int c, float v) const {
+    buf_store_at<W>(value(v), r, base, c);
+  }
   __device__ void at(int64_t i, float v) const { out[i] = from_f32<W>(value(v)); }
   __device__ float value(float v) const { return round_to<T>(round_to<T>(v) * scale); }
 };
@@ -35,6 +38,9 @@ struct WeightGradLoad {
     return tile_rsrc(g + first, (uint64_t)count * sizeof(W));
   }
   __device__ float operator()(__amdgpu_buffer_rsrc_t r, int i) const { return round_to<T>(buf_load<W>(r, i)); }
+  __device__ float whole(__amdgpu_buffer_rsrc_t r, int base, int c) const {
+    return round_to<T>(buf_load_at<W>(r, base, c));
+  }
   __device__ float at(int64_t i) const { return round_to<T>(to_f32(g[i])); }
 };
 

@@ -35,6 +35,7 @@ struct SliceStore {
     return tile_rsrc(out + first, (uint64_t)count * sizeof(T));
   }
   __device__ void operator()(__amdgpu_buffer_rsrc_t r, int i, float v) const { buf_store<T>(v, r, i); }
+  __device__ void whole(__amdgpu_buffer_rsrc_t r, int base, int c, float v) const { buf_store_at<T>(v, r, base, c); }
   __device__ void at(int64_t i, float v) const { out[i] = from_f32<T>(v); }
 };
 template <class T>
@@ -44,6 +45,7 @@ struct SliceLoad {
     return tile_rsrc(g + first, (uint64_t)count * sizeof(T));
   }
   __device__ float operator()(__amdgpu_buffer_rsrc_t r, int i) const { return buf_load<T>(r, i); }
+  __device__ float whole(__amdgpu_buffer_rsrc_t r, int base, int c) const { return buf_load_at<T>(r, base, c); }
   __device__ float at(int64_t i) const { return to_f32(g[i]); }
 };
 

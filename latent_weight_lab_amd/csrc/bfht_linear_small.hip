@@ -39,6 +39,7 @@ struct LdsWeightStore {
   __device__ void operator()(LdsRange r, int i, float v) const {
     if ((unsigned)i < (unsigned)r.count) w[r.first + i] = v * scale;
   }
+  __device__ void whole(LdsRange r, int b, int c, float v) const { w[r.first + b + c] = v * scale; }
   __device__ void at(int64_t i, float v) const { w[i - base] = v * scale; }
 };
 

@@ -79,6 +79,7 @@ struct TableStore {
   __device__ void operator()(Range rg, int i, float v) const {
     if ((unsigned)i < (unsigned)rg.count) put(rg.first + i, v);
   }
+  __device__ void whole(Range rg, int b, int c, float v) const { put(rg.first + b + c, v); }
   __device__ void at(int64_t i, float v) const { put((int)(i - base), v); }
 };
 
