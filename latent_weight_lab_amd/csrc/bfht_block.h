@@ -194,14 +194,39 @@ struct BlockLds {
   __device__ static int table_word(int gi) { return Gm::G * Gm::PADDED + gi * kSignTableLayers * Gm::TB; }
 };
 
-// Register exchange from group layout (lo_a, nb_a) to (lo_b, nb_b) through LDS.
+// Whether the exchange between groups 1 (bits 0-4) and 2 keeps every value in
+// its wave.  group_pos is a bit permutation of (thread, register), so it does
+// when every wave-index bit of the thread (bit 6 and up) lands on the same
+// position bit in both layouts.  True at 2^15 (thread bits 6-9 are position
+// bits 11-14 in both), false below.
 template <int LB>
-__device__ __forceinline__ void exchange(float (&v)[32], float* lds, int t, int lo_a, int nb_a, int lo_b, int nb_b) {
+constexpr bool intra_wave_pair() {
+  using S = BlockSeq<LB>;
+  if (S::N != 3 || Geo<LB>::TB < 64) return false;
+  for (int k = 6; (1 << k) < Geo<LB>::TB; ++k)
+    if (group_pos<LB, 5>(1 << k, 0, S::lo(1), S::nb(1)) != group_pos<LB, 5>(1 << k, 0, S::lo(2), S::nb(2)))
+      return false;
+  return true;
+}
+static_assert(intra_wave_pair<15>() && !intra_wave_pair<14>() && !intra_wave_pair<10>(),
+              "intra-wave exchange pairs");
+
+// Register exchange from group layout (lo_a, nb_a) to (lo_b, nb_b) through LDS.
+// Position p always sits in slot lds_index(p), so a thread writes exactly the
+// slots it read in the previous exchange, which no other thread reads in
+// between: the writes need no barrier before them.  The reads need every
+// thread's writes done (a barrier), except when the exchange keeps each value
+// in its wave (`intra_wave`): a wave's LDS accesses are performed in order.
+template <int LB>
+__device__ __forceinline__ void exchange(float (&v)[32], float* lds, int t, int lo_a, int nb_a, int lo_b, int nb_b,
+                                         bool intra_wave = false) {
   const int wb = group_base<LB, 5>(t, lo_a, nb_a);
-  __syncthreads();  // earlier reads of the buffer are done
 #pragma unroll
   for (int r = 0; r < 32; ++r) lds[group_lds<LB, 5>(wb, r, lo_a, nb_a)] = v[r];
-  __syncthreads();
+  if (intra_wave)
+    asm volatile("" ::: "memory");  // keep the reads after the writes
+  else
+    __syncthreads();
   const int rb = group_base<LB, 5>(t, lo_b, nb_b);
 #pragma unroll
   for (int r = 0; r < 32; ++r) v[r] = lds[group_lds<LB, 5>(rb, r, lo_b, nb_b)];
@@ -267,18 +292,19 @@ __device__ __forceinline__ float transform_scale(int layers) {
 template <int LB>
 __device__ __forceinline__ void layer_fht(float (&v)[32], float* lds, int t, bool reversed) {
   using S = BlockSeq<LB>;
+  constexpr bool kIntra12 = intra_wave_pair<LB>();
   if (!reversed) {
     butterflies<32>(v, S::nb(0));
 #pragma unroll
     for (int g = 1; g < S::N; ++g) {
-      exchange<LB>(v, lds, t, S::lo(g - 1), S::nb(g - 1), S::lo(g), S::nb(g));
+      exchange<LB>(v, lds, t, S::lo(g - 1), S::nb(g - 1), S::lo(g), S::nb(g), kIntra12 && g == 2);
       butterflies<32>(v, S::nb(g));
     }
   } else {
     butterflies<32>(v, S::nb(S::N - 1));
 #pragma unroll
     for (int g = S::N - 2; g >= 0; --g) {
-      exchange<LB>(v, lds, t, S::lo(g + 1), S::nb(g + 1), S::lo(g), S::nb(g));
+      exchange<LB>(v, lds, t, S::lo(g + 1), S::nb(g + 1), S::lo(g), S::nb(g), kIntra12 && g == 1);
       butterflies<32>(v, S::nb(g));
     }
   }

@@ -93,7 +93,7 @@ __device__ __forceinline__ int group_job(const Table& g, int wg) {
 // of 2^(LE-nb) columns placed above the thread index, so that for a fixed
 // register the lanes of a wave touch consecutive columns.
 template <int LB, int LE>
-__device__ __forceinline__ int group_pos(int t, int r, int lo, int nb) {
+__host__ __device__ constexpr int group_pos(int t, int r, int lo, int nb) {
   const int rlo = r & ((1 << nb) - 1);
   const int c = ((r >> nb) << (LB - LE)) | t;
   return ((c >> lo) << (lo + nb)) | (rlo << lo) | (c & ((1 << lo) - 1));
