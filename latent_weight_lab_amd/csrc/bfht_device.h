@@ -130,51 +130,15 @@ __device__ __forceinline__ int group_base(int t, int lo, int nb) {
   return lds_index(group_pos<LB, LE>(t, 0, lo, nb));
 }
 
-// Full unnormalized Walsh-Hadamard transform of an LB-bit block held as
-// v[E] per thread in the contiguous layout (thread t holds positions t*E + r),
-// using `lds` (lds_index-padded, one block) for the group exchanges.  Leaves v
-// in the same contiguous layout.  All threads of the workgroup must call it
-// (it contains barriers); `t` is the thread's index within its block.
-template <int LB, int LE>
-__device__ __forceinline__ void fht_unnormalized(float (&v)[1 << LE], float* lds, int t) {
-  constexpr int E = 1 << LE;
-  constexpr int NG = (LB + 4) / 5;
-  butterflies<E>(v, LE < 5 ? LE : 5);
-  if constexpr (NG > 1) {
-#pragma unroll
-    for (int g = 1; g < NG; ++g) {
-      const int plo = (g - 1) * 5;  // every group but the last has 5 bits
-      const int wb = group_base<LB, LE>(t, plo, 5);
-      __syncthreads();
-#pragma unroll
-      for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, plo, 5)] = v[r];
-      __syncthreads();
-      const int lo = g * 5, nb = (g == NG - 1) ? LB - lo : 5;
-      const int rb = group_base<LB, LE>(t, lo, nb);
-#pragma unroll
-      for (int r = 0; r < E; ++r) v[r] = lds[group_lds<LB, LE>(rb, r, lo, nb)];
-      butterflies<E>(v, nb);
-    }
-    {
-      const int lo = (NG - 1) * 5, nb = LB - lo;
-      const int wb = group_base<LB, LE>(t, lo, nb);
-      __syncthreads();
-#pragma unroll
-      for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, lo, nb)] = v[r];
-      __syncthreads();
-      const int cb = lds_index(t * E);  // contiguous layout: t * E + r, r < E <= 32
-#pragma unroll
-      for (int r = 0; r < E; ++r) v[r] = lds[cb + r];
-    }
-  }
-}
-
 // Full unnormalized transform of an LB-bit block held in the coalesced layout
 // (thread t, register r holds position r * 2^(LB-LE) + t, so a warp's lanes
 // touch consecutive positions for every register), left in the same layout.
 // The registers already span the top LE bits, so the transform starts there and
 // needs one LDS exchange per remaining group of up to 5 bits plus one back to
-// the coalesced layout.  All threads of the workgroup must call it.
+// the coalesced layout.  All threads of the workgroup must call it.  Position p
+// keeps slot lds_index(p) in every layout, so a thread's writes go to slots it
+// read itself in the previous exchange (or in the previous call's last one):
+// only the reads wait at a barrier.
 template <int LB, int LE>
 __device__ __forceinline__ void fht_coalesced(float (&v)[1 << LE], float* lds, int t) {
   constexpr int E = 1 << LE;
@@ -187,7 +151,6 @@ __device__ __forceinline__ void fht_coalesced(float (&v)[1 << LE], float* lds, i
     for (int g = 0; g < NR; ++g) {
       const int lo = 5 * g, nb = (TOP - lo < 5) ? TOP - lo : 5;
       const int wb = group_base<LB, LE>(t, lo_cur, nb_cur);
-      __syncthreads();
 #pragma unroll
       for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, lo_cur, nb_cur)] = v[r];
       __syncthreads();
@@ -199,7 +162,6 @@ __device__ __forceinline__ void fht_coalesced(float (&v)[1 << LE], float* lds, i
       nb_cur = nb;
     }
     const int wb = group_base<LB, LE>(t, lo_cur, nb_cur);
-    __syncthreads();
 #pragma unroll
     for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, lo_cur, nb_cur)] = v[r];
     __syncthreads();
