@@ -99,11 +99,11 @@ __host__ __device__ constexpr int group_pos(int t, int r, int lo, int nb) {
   return ((c >> lo) << (lo + nb)) | (rlo << lo) | (c & ((1 << lo) - 1));
 }
 
-// Unnormalized radix-2 butterflies over register-index bits [0, nb).
+// Unnormalized radix-2 butterflies over register-index bits [0, nb), nb <= 6.
 template <int E>
 __device__ __forceinline__ void butterflies(float (&v)[E], int nb) {
 #pragma unroll
-  for (int j = 0; j < 5; ++j) {
+  for (int j = 0; j < 6; ++j) {
     if (j < nb) {
 #pragma unroll
       for (int r = 0; r < E; ++r) {
@@ -139,10 +139,19 @@ __device__ __forceinline__ int group_base(int t, int lo, int nb) {
 // keeps slot lds_index(p) in every layout, so a thread's writes go to slots it
 // read itself in the previous exchange (or in the previous call's last one):
 // only the reads wait at a barrier.
-template <int LB, int LE>
+// When the block's 2^(LB-LE) threads sit in one wave (kOneWave), the reads
+// need no barrier either: a wave's LDS accesses are performed in order.
+template <int LB, int LE, bool kOneWave = false>
 __device__ __forceinline__ void fht_coalesced(float (&v)[1 << LE], float* lds, int t) {
   constexpr int E = 1 << LE;
   constexpr int TOP = LB - LE;  // position bits [TOP, LB) are the register bits
+  static_assert(!kOneWave || (1 << TOP) <= 64, "one wave holds the block");
+  auto sync = [] {
+    if constexpr (kOneWave)
+      asm volatile("" ::: "memory");
+    else
+      __syncthreads();
+  };
   butterflies<E>(v, LE);
   if constexpr (TOP > 0) {
     constexpr int NR = (TOP + 4) / 5;
@@ -153,7 +162,7 @@ __device__ __forceinline__ void fht_coalesced(float (&v)[1 << LE], float* lds, i
       const int wb = group_base<LB, LE>(t, lo_cur, nb_cur);
 #pragma unroll
       for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, lo_cur, nb_cur)] = v[r];
-      __syncthreads();
+      sync();
       const int rb = group_base<LB, LE>(t, lo, nb);
 #pragma unroll
       for (int r = 0; r < E; ++r) v[r] = lds[group_lds<LB, LE>(rb, r, lo, nb)];
@@ -164,7 +173,7 @@ __device__ __forceinline__ void fht_coalesced(float (&v)[1 << LE], float* lds, i
     const int wb = group_base<LB, LE>(t, lo_cur, nb_cur);
 #pragma unroll
     for (int r = 0; r < E; ++r) lds[group_lds<LB, LE>(wb, r, lo_cur, nb_cur)] = v[r];
-    __syncthreads();
+    sync();
     const int rb = group_base<LB, LE>(t, TOP, LE);
 #pragma unroll
     for (int r = 0; r < E; ++r) v[r] = lds[group_lds<LB, LE>(rb, r, TOP, LE)];

@@ -28,7 +28,10 @@ def signs_for(P, seed):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows,features", [(4096, 768), (300, 3072), (7, 1), (33, 5), (64, 32), (65, 33),
-                                           (10, 1000), (9, 4096), (3, 32768), (1, 20000)])
+                                           (10, 1000), (9, 4096), (3, 32768), (1, 20000),
+                                           # one-wave rows (P = 1024, 4096): odd row counts, ragged
+                                           # rows and rows of no whole 16-byte chunks
+                                           (7, 1000), (3, 517), (5, 2051), (129, 4000)])
 def test_mix_matches_oracle(rows, features, dtype):
     P = ops.next_power_of_two(features)
     s = signs_for(P, features)
@@ -41,13 +44,14 @@ def test_mix_matches_oracle(rows, features, dtype):
 
 
 def test_mix_in_place_and_empty():
-    s = signs_for(1024, 1).cuda()
-    x = torch.randn(100, 768, device="cuda")
-    want = ops.fht_mix(x, s)
-    ops.fht_mix(x, s, out=x)
-    assert torch.equal(x, want)
+    for rows, features, P in ((100, 768, 1024), (37, 3072, 4096), (11, 1500, 2048)):
+        s = signs_for(P, 1).cuda()
+        x = torch.randn(rows, features, device="cuda")
+        want = ops.fht_mix(x, s)
+        ops.fht_mix(x, s, out=x)
+        assert torch.equal(x, want)
     e = torch.empty(0, 768, device="cuda")
-    assert ops.fht_mix(e, s).shape == (0, 768)
+    assert ops.fht_mix(e, signs_for(1024, 1).cuda()).shape == (0, 768)
 
 
 def test_mix_involution_at_power_of_two():
