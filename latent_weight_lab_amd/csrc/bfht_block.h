@@ -292,19 +292,20 @@ __device__ __forceinline__ float transform_scale(int layers) {
 template <int LB>
 __device__ __forceinline__ void layer_fht(float (&v)[32], float* lds, int t, bool reversed) {
   using S = BlockSeq<LB>;
+  constexpr bool kOneWave = Geo<LB>::TB <= 64;  // a block in one wave: its exchanges stay there
   constexpr bool kIntra12 = intra_wave_pair<LB>();
   if (!reversed) {
     butterflies<32>(v, S::nb(0));
 #pragma unroll
     for (int g = 1; g < S::N; ++g) {
-      exchange<LB>(v, lds, t, S::lo(g - 1), S::nb(g - 1), S::lo(g), S::nb(g), kIntra12 && g == 2);
+      exchange<LB>(v, lds, t, S::lo(g - 1), S::nb(g - 1), S::lo(g), S::nb(g), kOneWave || (kIntra12 && g == 2));
       butterflies<32>(v, S::nb(g));
     }
   } else {
     butterflies<32>(v, S::nb(S::N - 1));
 #pragma unroll
     for (int g = S::N - 2; g >= 0; --g) {
-      exchange<LB>(v, lds, t, S::lo(g + 1), S::nb(g + 1), S::lo(g), S::nb(g), kIntra12 && g == 1);
+      exchange<LB>(v, lds, t, S::lo(g + 1), S::nb(g + 1), S::lo(g), S::nb(g), kOneWave || (kIntra12 && g == 1));
       butterflies<32>(v, S::nb(g));
     }
   }
@@ -392,7 +393,7 @@ __device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Sto
     } else if constexpr (S::kLastStores) {
       store(S::lo(S::N - 1), S::nb(S::N - 1));
     } else {
-      exchange<LB>(v, lds, t, S::lo(S::N - 1), S::nb(S::N - 1), S::lo(0), S::nb(0));
+      exchange<LB>(v, lds, t, S::lo(S::N - 1), S::nb(S::N - 1), S::lo(0), S::nb(0), Gm::TB <= 64);
       store(S::lo(0), S::nb(0));
     }
   }
@@ -491,7 +492,7 @@ __device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ pa
     } else if constexpr (S::kLastStores) {
       write(S::lo(S::N - 1), S::nb(S::N - 1));
     } else {
-      exchange<LB>(v, lds, t, S::lo(S::N - 1), S::nb(S::N - 1), S::lo(0), S::nb(0));
+      exchange<LB>(v, lds, t, S::lo(S::N - 1), S::nb(S::N - 1), S::lo(0), S::nb(0), Gm::TB <= 64);
       write(S::lo(0), S::nb(0));
     }
   }
