@@ -156,6 +156,27 @@ __device__ __forceinline__ void block_bwd_small(Load grad, float* __restrict__ p
   }
 }
 
+// Layout of bit group [lo, lo + nb) (nb <= 5) in the whole-block kernels:
+// register r of thread t holds position bpos(t, r, lo, nb).  The 5 register
+// bits sit at position bits lo .. lo + 4 — the group's nb bits first, then
+// 5 - nb bits that the group leaves untransformed — and the thread bits fill
+// the other position bits from 0 up.  For a group at bit 5 or above, lanes 0-31
+// then hold 32 consecutive positions, and every layout with lo >= 5 or lo = 0
+// puts thread bits 6 and up on the same position bits, so an exchange between
+// such layouts stays inside each wave.
+template <int LB>
+__host__ __device__ constexpr int bpos(int t, int r, int lo, int nb) {
+  return ((t >> lo) << (lo + 5)) | (r << lo) | (t & ((1 << lo) - 1));
+}
+template <int LB>
+__device__ __forceinline__ int bslot_base(int t, int lo, int nb) {  // padded LDS slot of (t, 0)
+  return lds_index(bpos<LB>(t, 0, lo, nb));
+}
+template <int LB>
+__device__ __forceinline__ int bslot(int base, int r, int lo, int nb) {  // slot of (t, r): disjoint bit fields
+  return base + lds_index(bpos<LB>(0, r, lo, nb));
+}
+
 // Blocks of 2^6 .. 2^15: 32 values per thread.  The transform is a sequence of
 // bit groups — the top group (position bits LB-5 .. LB-1, which the registers
 // of the coalesced layout span: register r of thread t holds position
@@ -195,21 +216,25 @@ struct BlockLds {
 };
 
 // Whether the exchange between groups 1 (bits 0-4) and 2 keeps every value in
-// its wave.  group_pos is a bit permutation of (thread, register), so it does
+// its wave.  bpos is a bit permutation of (thread, register), so it does
 // when every wave-index bit of the thread (bit 6 and up) lands on the same
-// position bit in both layouts.  True at 2^15 (thread bits 6-9 are position
-// bits 11-14 in both), false below.
+// position bit in both layouts: thread bit k >= 5 is position bit k + 5 in
+// both, so it holds from 2^12 (two waves per block) to 2^15; below 2^12 a
+// block sits in one wave anyway.
 template <int LB>
 constexpr bool intra_wave_pair() {
   using S = BlockSeq<LB>;
   if (S::N != 3 || Geo<LB>::TB < 64) return false;
   for (int k = 6; (1 << k) < Geo<LB>::TB; ++k)
-    if (group_pos<LB, 5>(1 << k, 0, S::lo(1), S::nb(1)) != group_pos<LB, 5>(1 << k, 0, S::lo(2), S::nb(2)))
+    if (bpos<LB>(1 << k, 0, S::lo(1), S::nb(1)) != bpos<LB>(1 << k, 0, S::lo(2), S::nb(2)))
       return false;
   return true;
 }
-static_assert(intra_wave_pair<15>() && !intra_wave_pair<14>() && !intra_wave_pair<10>(),
+static_assert(intra_wave_pair<15>() && intra_wave_pair<14>() && intra_wave_pair<13>() && intra_wave_pair<12>() &&
+                  !intra_wave_pair<10>(),
               "intra-wave exchange pairs");
+static_assert(bpos<15>(1000, 7, 10, 5) == 7 * 1024 + 1000 && bpos<13>(5, 3, 8, 5) == 3 * 256 + 5,
+              "the top group's layout is the coalesced one: register r of thread t at r * TB + t");
 
 // Register exchange from group layout (lo_a, nb_a) to (lo_b, nb_b) through LDS.
 // Position p always sits in slot lds_index(p), so a thread writes exactly the
@@ -220,16 +245,16 @@ static_assert(intra_wave_pair<15>() && !intra_wave_pair<14>() && !intra_wave_pai
 template <int LB>
 __device__ __forceinline__ void exchange(float (&v)[32], float* lds, int t, int lo_a, int nb_a, int lo_b, int nb_b,
                                          bool intra_wave = false) {
-  const int wb = group_base<LB, 5>(t, lo_a, nb_a);
+  const int wb = bslot_base<LB>(t, lo_a, nb_a);
 #pragma unroll
-  for (int r = 0; r < 32; ++r) lds[group_lds<LB, 5>(wb, r, lo_a, nb_a)] = v[r];
+  for (int r = 0; r < 32; ++r) lds[bslot<LB>(wb, r, lo_a, nb_a)] = v[r];
   if (intra_wave)
     asm volatile("" ::: "memory");  // keep the reads after the writes
   else
     __syncthreads();
-  const int rb = group_base<LB, 5>(t, lo_b, nb_b);
+  const int rb = bslot_base<LB>(t, lo_b, nb_b);
 #pragma unroll
-  for (int r = 0; r < 32; ++r) v[r] = lds[group_lds<LB, 5>(rb, r, lo_b, nb_b)];
+  for (int r = 0; r < 32; ++r) v[r] = lds[bslot<LB>(rb, r, lo_b, nb_b)];
 }
 
 // x with its sign bit XOR-ed with bit 31 of m (one v_bitop3).
@@ -249,7 +274,7 @@ __device__ __forceinline__ float flip_by_msb(float x, uint32_t m) {
 template <int LB>
 __device__ __forceinline__ void sign_flip(float (&v)[32], const uint32_t* smem_words, int table, int t, int lo,
                                           int nb) {
-  const int base = group_pos<LB, 5>(t, 0, lo, nb);
+  const int base = bpos<LB>(t, 0, lo, nb);
   // The table sits above the exchange buffer (beyond the 64 KiB the LDS
   // instructions' offset field reaches): its index is opaque to the compiler,
   // so it is added once and the per-register word offsets fold into the reads.
@@ -260,7 +285,7 @@ __device__ __forceinline__ void sign_flip(float (&v)[32], const uint32_t* smem_w
     const uint32_t s = 31u - (uint32_t)(base & 31);
 #pragma unroll
     for (int r = 0; r < 32; r += 2) {
-      const int c0 = group_pos<LB, 5>(0, r, lo, nb), c1 = group_pos<LB, 5>(0, r + 1, lo, nb);
+      const int c0 = bpos<LB>(0, r, lo, nb), c1 = bpos<LB>(0, r + 1, lo, nb);
       const uint64_t pair = (uint64_t)flips[(base >> 5) + (c0 >> 5)] |
                             ((uint64_t)flips[(base >> 5) + (c1 >> 5)] << 32);
       uint64_t m;
@@ -271,7 +296,7 @@ __device__ __forceinline__ void sign_flip(float (&v)[32], const uint32_t* smem_w
   } else {
 #pragma unroll
     for (int r = 0; r < 32; ++r) {
-      const int c = group_pos<LB, 5>(0, r, lo, nb);
+      const int c = bpos<LB>(0, r, lo, nb);
       const int bit = (base & 31) | (c & 31);
       v[r] = flip_by_msb(v[r], flips[(base >> 5) + (c >> 5)] << (31 - bit));
     }
@@ -367,7 +392,7 @@ __device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Sto
     const int64_t hi = stop - base < Gm::B ? stop - base : Gm::B;
     auto store = [&](int glo, int gnb) {
       if (!active) return;
-      const int pb = group_pos<LB, 5>(t, 0, glo, gnb);
+      const int pb = bpos<LB>(t, 0, glo, gnb);
       if constexpr (Gm::TB >= 64) {
         // one block per wave: a uniform buffer resource over the block's range,
         // positions outside [lo, hi) dropped by its range check; a whole block
@@ -375,15 +400,15 @@ __device__ __forceinline__ void block_fwd_slot(const T* __restrict__ latent, Sto
         const auto out_r = out.range(base + lo - start, hi - lo);
         if (lo == 0 && hi == Gm::B) {
 #pragma unroll
-          for (int r = 0; r < 32; ++r) out.whole(out_r, pb, group_pos<LB, 5>(0, r, glo, gnb), v[r] * scale);
+          for (int r = 0; r < 32; ++r) out.whole(out_r, pb, bpos<LB>(0, r, glo, gnb), v[r] * scale);
         } else {
 #pragma unroll
-          for (int r = 0; r < 32; ++r) out(out_r, pb + group_pos<LB, 5>(0, r, glo, gnb) - (int)lo, v[r] * scale);
+          for (int r = 0; r < 32; ++r) out(out_r, pb + bpos<LB>(0, r, glo, gnb) - (int)lo, v[r] * scale);
         }
       } else {
 #pragma unroll
         for (int r = 0; r < 32; ++r) {
-          const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
+          const int p = pb | bpos<LB>(0, r, glo, gnb);
           if (p >= lo && p < hi) out.at(base + p - start, v[r] * scale);
         }
       }
@@ -461,14 +486,14 @@ __device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ pa
     const float scale = transform_scale<LB>(layers);
     auto write = [&](int glo, int gnb) {
       if (!active) return;
-      const int pb = group_pos<LB, 5>(t, 0, glo, gnb);
+      const int pb = bpos<LB>(t, 0, glo, gnb);
       if constexpr (Gm::TB >= 64) {
         // one block per wave: uniform resources, positions >= n dropped
         const auto d_r = direct ? tile_rsrc(grad_latent, (uint64_t)n * sizeof(T))
                                 : tile_rsrc(partial + slot * stride, (uint64_t)n * 4);
 #pragma unroll
         for (int r = 0; r < 32; ++r) {
-          const int c = group_pos<LB, 5>(0, r, glo, gnb);  // disjoint from pb's bits
+          const int c = bpos<LB>(0, r, glo, gnb);  // disjoint from pb's bits
           if (direct)
             buf_store_nn<T>(v[r] * scale, d_r, pb, c);
           else
@@ -477,7 +502,7 @@ __device__ __forceinline__ void block_bwd_slot(Load grad, float* __restrict__ pa
       } else {
 #pragma unroll
         for (int r = 0; r < 32; ++r) {
-          const int p = pb | group_pos<LB, 5>(0, r, glo, gnb);
+          const int p = pb | bpos<LB>(0, r, glo, gnb);
           if (p < n) {
             if (direct)
               grad_latent[p] = from_f32<T>(v[r] * scale);
