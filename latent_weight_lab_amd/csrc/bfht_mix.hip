@@ -7,15 +7,16 @@
 // symmetric, so the same kernel computes the backward on the gradient.
 //
 // P = 4096 (GPT-2's 3072 features padded): bfht_mix_square, one wave per row,
-// one LDS exchange.  Other sizes: one row per thread group of the whole-block
-// VALU geometry (Geo<LB>), the workgroups looping over row groups; where a row
-// fits one wave (P <= 2048) its exchanges need no barrier.  A row stays in the coalesced layout
-// (register r of thread t holds position r * TB + t), so it is loaded, signed
-// (a per-thread sign mask read once per workgroup) and stored without staging,
-// and the transform starts on the register bits and needs one LDS exchange per
-// remaining 5-bit group plus one back.  Each thread reads its values before it
-// writes any, and every position is read and written by the same thread, so
-// the output may alias the input.
+// one LDS exchange (below).  Other sizes: bfht_mix_rows, one row per thread
+// group of the whole-block VALU geometry (Geo<LB>), the workgroups looping over
+// row groups.  A row stays in the coalesced layout (register r of thread t
+// holds position r * TB + t), so it is loaded, signed (a per-thread sign mask
+// read once per workgroup) and stored without staging, and the transform starts
+// on the register bits and needs one LDS exchange per remaining 5-bit group
+// plus one back; where a row fits one wave (P <= 2048) no exchange waits at a
+// barrier.  The output may alias the input: bfht_mix_rows writes each position
+// from the thread that read it, bfht_mix_square from the row's own wave after
+// all of the row's reads.
 #include "bfht_block.h"
 
 namespace lwl {
