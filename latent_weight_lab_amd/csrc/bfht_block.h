@@ -185,9 +185,9 @@ __device__ __forceinline__ int bslot(int base, int r, int lo, int nb) {  // slot
 // layers in reverse, so a layer boundary needs no exchange: the sign layer
 // between them is applied in whatever layout the data is in, from a table of
 // the block's inverted sign words in LDS (hashed once per block, one word per
-// thread and layer).  The block is read and written in the coalesced layout (or, after an
-// odd number of layers, in the last group's layout when that keeps 32
-// consecutive positions per half wave).
+// thread and layer).  The block is read and written in the coalesced layout
+// (or, after an odd number of layers, in the last group's layout when that
+// keeps 32 consecutive positions per half wave).  Layouts: bpos above.
 template <int LB>
 struct BlockSeq {
   static constexpr int TOP = LB - 5;
