@@ -54,6 +54,27 @@ def test_mix_in_place_and_empty():
     assert ops.fht_mix(e, signs_for(1024, 1).cuda()).shape == (0, 768)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,features", [(9, 3072), (6, 768)])
+def test_mix_unaligned_buffers(rows, features, dtype):
+    """x and out one element off the 16-byte grid: the element-store paths, equal to the
+    aligned call bit for bit."""
+    P = ops.next_power_of_two(features)
+    s = signs_for(P, 4).cuda()
+    x = torch.randn(rows, features, generator=torch.Generator().manual_seed(7)).to(dtype).cuda()
+    want = ops.fht_mix(x, s)
+    xb = torch.zeros(rows * features + 1, dtype=dtype, device="cuda")
+    xb[1:] = x.reshape(-1)
+    ob = torch.zeros(rows * features + 2, dtype=dtype, device="cuda")
+    xv = xb[1:].view(rows, features)
+    ov = ob[1:-1].view(rows, features)
+    assert xv.data_ptr() % 16 != 0 and ov.data_ptr() % 16 != 0
+    ops.fht_mix(xv, s, out=ov)
+    torch.cuda.synchronize()
+    assert torch.equal(ov, want)
+    assert ob[0].item() == 0 and ob[-1].item() == 0  # nothing written outside out
+
+
 def test_mix_involution_at_power_of_two():
     s = signs_for(4096, 2).cuda()
     x = torch.randn(50, 4096, device="cuda")
