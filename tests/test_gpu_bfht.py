@@ -211,6 +211,36 @@ def test_bf16_slice_backward_equals_masked_full_backward_bitwise():
     assert rel_l2(to_np(got), gwant) < TOL[torch.bfloat16]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("log_block", [10, 13, 15])
+def test_valu_block_paths_agree_bitwise(log_block, dtype):
+    """The VALU whole-block kernels take check-free loads and stores for whole blocks and
+    range-checked ones for partial blocks and short latents; all of them give the same bits:
+    a latent 5 short of the block equals its zero-padded copy (forward and the gradient's
+    first n values), slices equal the same range of the full output, and a slice's backward
+    equals the full backward of the gradient masked to the slice."""
+    B = 1 << log_block
+    size = 5 * B + 1000  # ragged last block
+    n = B - 5
+    lat = latent_for(n, 31, dtype).cuda()
+    padded = torch.cat([lat, torch.zeros(5, dtype=dtype, device="cuda")])
+    full = ops.forward(lat, size, 3, 11, 0, size)
+    assert torch.equal(full, ops.forward(padded, size, 3, 11, 0, size))
+    want = c_oracle.forward(to_np(lat), size, 3, 11, 0, size)
+    assert rel_l2(to_np(full), want) < TOL[dtype]
+    for start, stop in [(7, 2 * B + 3), (B, 3 * B), (B - 1, B + 1), (3 * B + 17, size), (0, B)]:
+        assert torch.equal(ops.forward(lat, size, 3, 11, start, stop), full[start:stop]), (start, stop)
+    g = torch.randn(size, generator=torch.Generator().manual_seed(12)).to(dtype).cuda()
+    gl = ops.backward(g, n, dtype, size, 3, 11, 0, size)
+    assert torch.equal(gl, ops.backward(g, B, dtype, size, 3, 11, 0, size)[:n])
+    for start, stop in [(7, 2 * B + 3), (B, 3 * B), (3 * B + 17, size)]:
+        masked = torch.zeros_like(g)
+        masked[start:stop] = g[start:stop]
+        want = ops.backward(masked, n, dtype, size, 3, 11, 0, size)
+        got = ops.backward(g[start:stop].clone(), n, dtype, size, 3, 11, start, stop)
+        assert torch.equal(got, want), (start, stop)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_config2_slice_and_determinism(dtype):
     """Config 2's slice [12,345, 1,012,345) (31 blocks, both ends inside a block) at config 2's
