@@ -317,7 +317,10 @@ int lwl_bfht_flush_weight_grads(const lwl_bfht_weight_job* jobs, int64_t count, 
  * P = next power of two >= features (<= 32768), pad appends zeros, S =
  * diag(signs) with signs[P] = ±1.0f (the module's buffer, on the device), H the
  * Sylvester Walsh-Hadamard transform divided by sqrt(P).  float32 arithmetic,
- * one rounding to `dtype` at the end.  S H S is symmetric, so the backward is
+ * one rounding to `dtype` at the end; float16 / bfloat16 rows of P = 1024 or
+ * 4096 run on the matrix cores instead (operands in `dtype`, float32
+ * accumulation: the intermediate of the two radix-32 stages is rounded once to
+ * `dtype`, then the output once more).  S H S is symmetric, so the backward is
  * the same call on the output gradient.  out may equal x (in place).
  */
 int lwl_fht_mix(const void* x, int dtype, int64_t rows, int64_t features, const float* signs, void* out,

@@ -242,5 +242,9 @@ hipError_t launch_grouped(const WeightJob* jobs, int64_t count, void* work, hipS
 // out = (S H S pad(x))[:features] per row, H of order 2^log_size, S = diag(signs).
 hipError_t launch_fht_mix(int dtype, const void* x, void* out, const float* signs, int64_t rows, int64_t features,
                           int log_size, hipStream_t s);
+// float16 / bfloat16 rows of 2^10 or 2^12 run on the matrix cores (bfht_mix_mfma.hip).
+bool fht_mix_on_matrix_cores(int dtype, int log_size);
+hipError_t launch_fht_mix_mfma(int dtype, const void* x, void* out, const float* signs, int64_t rows,
+                               int64_t features, int log_size, hipStream_t s);
 
 }  // namespace lwl

@@ -254,6 +254,8 @@ hipError_t launch_fht_mix(int dtype, const void* x, void* out, const float* sign
                           int log_size, hipStream_t s) {
   if (rows == 0) return hipSuccess;
   if (log_size < 0 || log_size > kTileLog) return hipErrorInvalidValue;
+  if (fht_mix_on_matrix_cores(dtype, log_size))
+    return launch_fht_mix_mfma(dtype, x, out, signs, rows, features, log_size, s);
   const auto seq = std::make_integer_sequence<int, kTileLog + 1>{};
   switch (dtype) {
     case kF32: return dispatch_mix<float>(log_size, x, out, signs, rows, features, s, seq);

@@ -5,8 +5,11 @@ Sylvester FHT, multiply by the buffer again, keep the original width.
 
 The reference runs ``normalized_fht_last_dim`` (``model.py:180-197``) as a torch
 loop of log2(P) reshape / clone stages in the activation dtype; here one HIP
-launch does the whole row transform in float32 (``lwl_fht_mix``).  The map is
-symmetric, so its backward is the same launch on the gradient.
+launch does the whole row transform (``lwl_fht_mix``): in float32 with one
+rounding, or for bfloat16 / float16 rows of 1024 and 4096 values (GPT-2's 768
+and 3072 features) on the matrix cores, with one intermediate rounding to the
+activation dtype between its two radix-32 stages.  The map is symmetric, so its
+backward is the same launch on the gradient.
 """
 from __future__ import annotations
 

@@ -54,6 +54,26 @@ def test_mix_in_place_and_empty():
     assert ops.fht_mix(e, signs_for(1024, 1).cuda()).shape == (0, 768)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,features", [(101, 768), (3, 1000), (37, 3072), (5, 4096),
+                                           # more row groups than the launch's waves: each wave loops
+                                           (9001, 768), (5000, 3072)])
+def test_mix_matrix_core_rows(rows, features, dtype):
+    """The matrix-core kernel (bf16 / fp16 rows of P = 1024 and 4096; four rows per wave at
+    1024, a row count that is no multiple of four leaves the last wave's rows partly empty):
+    against the oracle, and in place equal to out of place bit for bit."""
+    P = ops.next_power_of_two(features)
+    s = signs_for(P, rows + features)
+    x = torch.randn(rows, features, generator=torch.Generator().manual_seed(rows)).to(dtype).cuda()
+    got = ops.fht_mix(x, s.cuda())
+    y = x.clone()
+    ops.fht_mix(y, s.cuda(), out=y)
+    torch.cuda.synchronize()
+    assert torch.equal(y, got)
+    want = O.fixed_fht_mix(x.double().cpu().numpy(), s.double().numpy())
+    assert O.rel_l2(got.double().cpu().numpy(), want) < TOL[dtype]
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,features", [(9, 3072), (6, 768)])
 def test_mix_unaligned_buffers(rows, features, dtype):
