@@ -63,6 +63,10 @@ __device__ __forceinline__ void store_range_shifted(const u32x4* stage, __bf16* 
   }
 }
 
+// Output ranges staged and stored one after another by the forward kernel
+// when the chain ends in S1 (odd L): 1, 2 or 4.
+constexpr int kOutPhases = 2;
+
 template <int L, bool kWhole>
 __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __restrict__ latent,
                                                             __bf16* __restrict__ out, int n,
@@ -79,14 +83,40 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
   // The signed bf16 block goes through the free exchange buffer in position
   // order, then to memory with consecutive threads on consecutive chunks.
   u32x4* stage = reinterpret_cast<u32x4*>(lds + (L & 1) * kXBufBytes);
-  stage_output<L>(acc, nw, x, stage);
-  __syncthreads();
   // block-local output range [lo, hi); out element of block position p is (base - start) + p
   const int64_t base = block * kB;
   const int lo = kWhole ? 0 : (int)(start - base > 0 ? start - base : 0);
   const int hi = kWhole ? kB : (int)(stop - base < kB ? stop - base : kB);
   __bf16* oblk = out + (base - start);
   const bool full = kWhole || (lo == 0 && hi == kB && (((uintptr_t)oblk & 15) == 0));
+  if constexpr (L % 2 == 1 && kOutPhases > 1) {
+    if (full) {
+      // In S1 a lane's chunk k lies in position range (k >> 1) of four (bits
+      // 13-14), so the block is staged and stored range by range: a range's
+      // stores go out while the next range's chunks are written to LDS.
+      const auto out_r = rsrc(oblk, (uint32_t)(kB * 2));
+      u32x4 v[8];
+      out_chunks<L>(acc, nw, x, v);
+      constexpr int kPerPhase = kChunks / kOutPhases;
+#pragma unroll
+      for (int ph = 0; ph < kOutPhases; ++ph) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (k * kOutPhases / 8 == ph) stage[stage_slot(out_chunk_pos<L>(x, k) >> 3)] = v[k];
+        __syncthreads();
+        u32x4 w[kPerPhase / kThreads];
+#pragma unroll
+        for (int i = 0; i < kPerPhase / kThreads; ++i) w[i] = stage[stage_slot(ph * kPerPhase + i * kThreads + (int)threadIdx.x)];
+#pragma unroll
+        for (int i = 0; i < kPerPhase / kThreads; ++i)
+          __builtin_amdgcn_raw_buffer_store_b128(w[i], out_r, (ph * kPerPhase + i * kThreads + (int)threadIdx.x) * 16, 0,
+                                                 kStreamStore);
+      }
+      return;
+    }
+  }
+  stage_output<L>(acc, nw, x, stage);
+  __syncthreads();
   if (!kWhole && !full && (((uintptr_t)oblk & 1) == 0)) {
     // part of a block, or an output off the 16-byte grid: 16-byte stores on the
     // grid, element stores at the range's ends (uniform branch)

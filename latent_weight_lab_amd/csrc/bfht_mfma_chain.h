@@ -685,61 +685,69 @@ __device__ __forceinline__ void write_partial_row(const f32x16 (&acc)[kTiles], c
     return __uint_as_float(__float_as_uint(v) ^ ((w << (31 - b)) & 0x80000000u));
   };
   f32x4* stage = reinterpret_cast<f32x4*>(lds);  // all 128 KiB
+  // bf16 rows of odd L go out in two halves: register r holds position bit 14
+  // = r >> 3, so the first half's stores leave while the second half is staged.
+  constexpr int kPhases = (L % 2 == 1 && sizeof(P) == 2) ? 2 : 1;
   __syncthreads();  // every wave has read its last exchange
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    f32x4 v;
-    int p;
-    if constexpr (L % 2 == 1) {
-      // S1: chunk = the 4 tiles at register r (p0, p1 = tile bits)
-      p = (((r >> 1) & 1) << 2) + ((r & 1) << 3) + (x.p4 << 4) + (x.lane32 << 5) + ((x.wave >> 1) << 10) +
-          (x.l5 << 12) + ((r >> 2) << 13);
-      const uint32_t w = nw[r >> 2];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = scale * flip(acc[t][r], w, (p & 31) + t);
-    } else {
-      // S0: chunk = registers r0 .. r0+3 of tile t (p0, p1 = register bits)
-      const int t = r & 3, r0 = (r >> 2) << 2;
-      p = (t << 2) + (((r0 >> 2) & 1) << 4) + (x.lane32 << 5) + (x.l5 << 10) + ((r0 >> 3) << 11) +
-          (x.wave << 12);
-      const uint32_t w = nw[r0 >> 3];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = scale * flip(acc[t][r0 + e], w, (p & 31) + e);
-    }
-    const int c = p >> 2;
-    stage[c ^ ((c >> 3) & 7)] = v;
-  }
-  __syncthreads();
   const auto p_r = rsrc(prow, (uint32_t)n * (uint32_t)sizeof(P));
-  if constexpr (sizeof(P) == 4) {
 #pragma unroll
-    for (int i = 0; i < (kB / 4) / kThreads; ++i) {
-      const int c = i * kThreads + (int)threadIdx.x;
-      const f32x4 v = stage[c ^ ((c >> 3) & 7)];
-      const int p = c * 4;
-      if (kExact || p + 4 <= n) {
-        __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, kStreamStore);  // dropped past n
-      } else if (p < n) {
+  for (int ph = 0; ph < kPhases; ++ph) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (p + e < n) prow[p + e] = v[e];
+    for (int r = 0; r < 16; ++r) {
+      if (kPhases > 1 && (r >> 3) != ph) continue;
+      f32x4 v;
+      int p;
+      if constexpr (L % 2 == 1) {
+        // S1: chunk = the 4 tiles at register r (p0, p1 = tile bits)
+        p = (((r >> 1) & 1) << 2) + ((r & 1) << 3) + (x.p4 << 4) + (x.lane32 << 5) + ((x.wave >> 1) << 10) +
+            (x.l5 << 12) + ((r >> 2) << 13);
+        const uint32_t w = nw[r >> 2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = scale * flip(acc[t][r], w, (p & 31) + t);
+      } else {
+        // S0: chunk = registers r0 .. r0+3 of tile t (p0, p1 = register bits)
+        const int t = r & 3, r0 = (r >> 2) << 2;
+        p = (t << 2) + (((r0 >> 2) & 1) << 4) + (x.lane32 << 5) + (x.l5 << 10) + ((r0 >> 3) << 11) +
+            (x.wave << 12);
+        const uint32_t w = nw[r0 >> 3];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = scale * flip(acc[t][r0 + e], w, (p & 31) + e);
       }
+      const int c = p >> 2;
+      stage[c ^ ((c >> 3) & 7)] = v;
     }
-  } else {  // bf16 row: two staged chunks (8 positions) per 16-byte store
+    __syncthreads();
+    if constexpr (sizeof(P) == 4) {
 #pragma unroll
-    for (int i = 0; i < (kB / 8) / kThreads; ++i) {
-      const int c2 = i * kThreads + (int)threadIdx.x;
-      const f32x4 a = stage[(2 * c2) ^ (((2 * c2) >> 3) & 7)];
-      const f32x4 b = stage[(2 * c2 + 1) ^ (((2 * c2 + 1) >> 3) & 7)];
-      const u32x4 v = {pk(a[0], a[1]), pk(a[2], a[3]), pk(b[0], b[1]), pk(b[2], b[3])};
-      const int p = c2 * 8;
-      if (kExact || p + 8 <= n) {
-        __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 2, 0, kStreamStore);  // dropped past n
-      } else if (p < n) {
-        uint16_t* row16 = reinterpret_cast<uint16_t*>(prow);
+      for (int i = 0; i < (kB / 4) / kThreads; ++i) {
+        const int c = i * kThreads + (int)threadIdx.x;
+        const f32x4 v = stage[c ^ ((c >> 3) & 7)];
+        const int p = c * 4;
+        if (kExact || p + 4 <= n) {
+          __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 4, 0, kStreamStore);  // dropped past n
+        } else if (p < n) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (p + e < n) row16[p + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+          for (int e = 0; e < 4; ++e)
+            if (p + e < n) prow[p + e] = v[e];
+        }
+      }
+    } else {  // bf16 row: two staged chunks (8 positions) per 16-byte store
+      constexpr int kPer = (kB / 8) / kPhases;
+#pragma unroll
+      for (int i = 0; i < kPer / kThreads; ++i) {
+        const int c2 = ph * kPer + i * kThreads + (int)threadIdx.x;
+        const f32x4 a = stage[(2 * c2) ^ (((2 * c2) >> 3) & 7)];
+        const f32x4 b = stage[(2 * c2 + 1) ^ (((2 * c2 + 1) >> 3) & 7)];
+        const u32x4 v = {pk(a[0], a[1]), pk(a[2], a[3]), pk(b[0], b[1]), pk(b[2], b[3])};
+        const int p = c2 * 8;
+        if (kExact || p + 8 <= n) {
+          __builtin_amdgcn_raw_buffer_store_b128(v, p_r, p * 2, 0, kStreamStore);  // dropped past n
+        } else if (p < n) {
+          uint16_t* row16 = reinterpret_cast<uint16_t*>(prow);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (p + e < n) row16[p + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+        }
       }
     }
   }
