@@ -763,8 +763,8 @@ __device__ __forceinline__ void load_latent(const Ctx& x, const __bf16* latent, 
   load_source(
       x,
       [&](int p) -> u32x4 {
-        // sc0: every CU reads each latent line once, from its XCD's L2 (8.86
-        // against 8.92-8.98 us at config 2 with the default policy; sc1 or nt,
+        // sc0: every CU reads each latent line once, from its XCD's L2 (config 2:
+        // within run-to-run spread of the default policy, 8.86-9.02 us; sc1 or nt,
         // which miss the L2, take ~9.9 us)
         u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(lat_r, p * 2, 0, 1);  // 0 past n
         if (tail && p < n && p + 8 > n) {  // straddles the end of the latent: exact element loads
