@@ -141,11 +141,34 @@ def time_graph(torch, fn, steps: int, warmup: int) -> float:
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
+    # The GPU spins (a bounded clock loop) while the host submits the graph, so that the start
+    # event is reached with the K launches already queued: the events then time the K steps'
+    # device work, not the host's submission latency (a fixed ~20 us that a 20-step graph would
+    # otherwise add to every step as ~1 us).
+    gpu_spin(torch, 300e-6)
     start.record()
     g.replay()
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / 1e3 / steps
+
+
+_SPIN_CYCLES_PER_S = None
+
+
+def gpu_spin(torch, seconds: float) -> None:
+    """Enqueue a kernel that spins on the device clock for about `seconds` (torch.cuda._sleep,
+    calibrated once against events)."""
+    global _SPIN_CYCLES_PER_S
+    if _SPIN_CYCLES_PER_S is None:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        a.record()
+        torch.cuda._sleep(1_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        _SPIN_CYCLES_PER_S = 1_000_000 / max(a.elapsed_time(b) / 1e3, 1e-6)
+    torch.cuda._sleep(int(seconds * _SPIN_CYCLES_PER_S))
 
 
 def time_eager(torch, fn, steps: int, warmup: int) -> float:
@@ -429,7 +452,122 @@ def extra_configs(abi, steps, warmup, only):
     # latents of 32768 bf16, seeds 100+i), forward only, fused vs dense on materialized weights
     if want("c5_stack"):
         res["c5_stack"] = stack_bench(abi, torch)
+
+    # the reference's own published shapes (context beside docs/block_fht_notes.md:34-39,81-85,
+    # RTX 4080 prototype numbers; not targets): its block-size sweep and its stacked decode
+    for name, fn in (("ref_sweep", ref_sweep_bench), ("ref_stack", ref_stack_bench)):
+        if want(name):
+            try:
+                res[name] = fn(torch)
+            except Exception as exc:  # noqa: BLE001
+                res[name] = {"error": f"{type(exc).__name__}: {exc}"}
     return res
+
+
+def ref_sweep_bench(torch, iters: int = 10):
+    """benchmarks/bench_block_fht.py:26-49 on this GPU: for block 2^5 .. 2^23, BlockFHT of a
+    float32 latent of one block, size = block, layers 1, seed = the power; forward, and forward +
+    backward of mean(y^2), each timed the reference's way (wall clock, a device sync per
+    iteration, 10 iterations after one warm-up slice backward; here also one untimed iteration of
+    each loop first, so that no one-time first-call cost lands in its mean).  Also the device time
+    of the forward in graph replay (no host or sync latency)."""
+    from latent_weight_lab_amd import BlockFHT
+
+    rows = {}
+    for power in range(5, 24):
+        block = 1 << power
+        torch.manual_seed(power)
+        m = BlockFHT(block, size=block, layers=1, seed=power).cuda()
+        m.latent.data = m.latent.data.float()
+        m.slice(0, min(block, 1024)).sum().backward()
+        m.latent.grad = None
+        torch.cuda.synchronize()
+
+        def fwd():
+            m()
+
+        def fwd_bwd():
+            m.latent.grad = None
+            m().square().mean().backward()
+
+        def wall_ms(fn):
+            fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                fn()
+                torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / iters
+
+        fwd_ms, fb_ms = wall_ms(fwd), wall_ms(fwd_bwd)
+        with torch.no_grad():
+            dev_ms = time_graph(torch, lambda: m(), 20, 3) * 1e3
+        rows[f"2^{power}"] = {"forward_ms": round(fwd_ms, 4), "forward_backward_ms": round(fb_ms, 4),
+                              "forward_device_ms": round(dev_ms, 5)}
+        del m
+    return {"method": "reference bench_block_fht.py (wall clock, sync per iteration, 10 iterations), fp32, "
+                      "layers 1, size = block", "rows": rows}
+
+
+def ref_stack_bench(torch, iters: int = 20):
+    """benchmarks/bench_fused_linear_stack.py:15-84 on this GPU: tokens 1, 1024 -> 4096, one float32
+    latent of 16384 shared by every matrix, layers 2, seeds 1000 + i; 1 / 4 / 16 / 64 matrices
+    through the fused linear ("fused_shared_latent") against F.linear on resident materialized
+    weights ("resident_dense"), each iteration ending in the reference's reduction of the
+    outputs, timed its way (wall clock over 20 iterations after 3 warm-ups, peak MiB from
+    max_memory_allocated after a reset).  The reference runs each mode in a process of its own;
+    here the fused mode runs before the weights exist and both peaks leave out what the earlier
+    bench rows still hold."""
+    import torch.nn.functional as F
+
+    from latent_weight_lab_amd import block_fht_linear_forward, block_fht_slice
+
+    tokens, fin, fout, ld, layers = 1, 1024, 4096, 16384, 2
+    torch.cuda.synchronize()
+    outside = torch.cuda.memory_allocated()  # what earlier rows still hold
+    torch.manual_seed(123)
+    x = torch.randn(tokens, fin, device="cuda")
+    latent = torch.randn(ld, device="cuda")
+
+    def bench(weights, matrices, n):
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            outs = []
+            for i in range(len(weights) if weights is not None else matrices):
+                if weights is None:
+                    outs.append(block_fht_linear_forward(x, latent, fout, layers, 1000 + i))
+                else:
+                    outs.append(F.linear(x, weights[i]))
+            y = torch.stack([o.float().mean() for o in outs]).sum()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / n
+        peak = (torch.cuda.max_memory_allocated() - outside) / 2**20
+        float(y)
+        return ms, peak
+
+    rows = {}
+    with torch.no_grad():
+        for matrices in (1, 4, 16, 64):
+            size = fin * fout
+            for _ in range(3):
+                bench(None, matrices, 1)
+            f_ms, f_peak = bench(None, matrices, iters)
+            weights = [block_fht_slice(latent, size, layers, 1000 + i, 0, size).view(fout, fin).clone()
+                       for i in range(matrices)]
+            torch.cuda.synchronize()
+            for _ in range(3):
+                bench(weights, matrices, 1)
+            d_ms, d_peak = bench(weights, matrices, iters)
+            rows[f"matrices_{matrices}"] = {"fused_ms": round(f_ms, 4), "fused_peak_MiB": round(f_peak, 1),
+                                            "resident_dense_ms": round(d_ms, 4),
+                                            "resident_dense_peak_MiB": round(d_peak, 1),
+                                            "fused_over_dense": f_ms / d_ms}
+            del weights
+            torch.cuda.empty_cache()
+    return {"method": "reference bench_fused_linear_stack.py (wall clock, 20 iterations), fp32, tokens 1, "
+                      "1024 -> 4096, shared latent 16384, layers 2", "rows": rows}
 
 
 GPT2_SHAPES = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]

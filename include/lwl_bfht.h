@@ -114,7 +114,12 @@ int lwl_bfht_backward(const void* grad_out, int dtype, int64_t latent_size, int6
  * 2^15) of up to 256 blocks of 2^15 (config 2 in float32), not the multi-pass
  * blocks' work buffer beyond 32 MiB.  Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (other streams, other threads) race.
- * Allocates nothing; results are bit-identical to lwl_bfht_backward.
+ * Allocates nothing; results are bit-identical to lwl_bfht_backward.  The
+ * first accepted call on each device resolves the array's device address
+ * (hipGetSymbolAddress, which may load the library's code object onto the
+ * device): make that call outside stream capture (any accepted call does,
+ * e.g. one of an empty slice); later calls, captured or not, read the cached
+ * address.
  */
 #define LWL_BFHT_NOALLOC_SCRATCH_BYTES (32 << 20)
 int lwl_bfht_backward_noalloc(const void* grad_out, int dtype, int64_t latent_size, int64_t output_size,
@@ -166,11 +171,14 @@ int lwl_bfht_check_linear_forward(int dtype, int64_t tokens, int64_t in_features
  * the modulation term, the residual base and the bias, each a separate torch op
  * after ext.linear_forward) with the store of the fused kernels:
  *
- *   out[t, o] = base[t, o] + weight_scale * sum_i input[t, i] * W[o, i]
- *             + row_sum_scale * (*row_sum_coef) * sum_i input[t, i] + bias[o]
+ *   out[t, o] = ((weight_scale * sum_i input[t, i] * W[o, i]
+ *                 + row_sum_scale * (*row_sum_coef) * sum_i input[t, i])
+ *                + base[t, o]) + bias[o]
  *
- * summed in float32 in that order and rounded once to `dtype` (the reference
- * rounds after each op, so results agree to the I/O type's rounding).  Terms
+ * summed in float32 in that order (the product, then the row-sum term, then the
+ * base, then the bias: the order of the reference's ops, block_fht.py:493-500;
+ * no fused multiply-adds) and rounded once to `dtype` (the reference rounds
+ * after each op, so results agree to the I/O type's rounding).  Terms
  * whose pointer is NULL are left out; bias [out_features] and base
  * [tokens, out_features] (the residual base's input @ base_weight^T) are in
  * `dtype`; row_sum_coef is one float32 on the device (the module's
@@ -204,8 +212,10 @@ int lwl_bfht_linear_forward_ex(const void* input, const void* latent, int dtype,
  * GPT-2 matrix has 18..72 generated blocks, so one matrix per launch leaves
  * most of the chip idle; jobs the bf16 matrix-core kernel takes with fewer
  * than 256 tokens run together, one launch per layer count for up to 48 jobs;
- * other jobs run as their single calls.  All jobs share `dtype`; outputs must
- * not overlap; inputs and latents may be shared.  A job's `epilogue` (NULL:
+ * other jobs run as their single calls, so jobs do not run in job order.  All
+ * jobs share `dtype`; outputs must not overlap, and no job's output may overlap
+ * another job's input, latent, base or bias (the check rejects both); inputs
+ * and latents may be shared.  A job's `epilogue` (NULL:
  * none) is that of lwl_bfht_linear_forward_ex; jobs whose epilogue has only a
  * bias still run grouped, jobs with a base or a row-sum term as single calls.
  * Workspace (query with the same jobs): the grouped jobs' own workspaces side
@@ -226,7 +236,8 @@ typedef struct lwl_bfht_linear_job {
   const lwl_bfht_linear_epilogue* epilogue; /* or NULL */
 } lwl_bfht_linear_job;
 
-/* Host-only check of `count` jobs (each as lwl_bfht_check_linear_forward, plus disjoint outputs). */
+/* Host-only check of `count` jobs (each as lwl_bfht_check_linear_forward, plus disjoint outputs
+ * and no output overlapping another job's operands). */
 int lwl_bfht_check_linear_jobs(int dtype, const lwl_bfht_linear_job* jobs, int64_t count);
 size_t lwl_bfht_linear_forward_grouped_workspace_size(int dtype, const lwl_bfht_linear_job* jobs, int64_t count);
 int lwl_bfht_linear_forward_grouped(int dtype, const lwl_bfht_linear_job* jobs, int64_t count, void* workspace,

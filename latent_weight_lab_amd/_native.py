@@ -51,8 +51,8 @@ class WeightJob(ctypes.Structure):
 
 
 class LinearEpilogue(ctypes.Structure):
-    """``lwl_bfht_linear_epilogue``: out = base + weight_scale * x @ W^T
-    + row_sum_scale * (*row_sum_coef) * x.sum(-1) + bias, one rounding."""
+    """``lwl_bfht_linear_epilogue``: out = ((weight_scale * x @ W^T + row_sum_scale *
+    (*row_sum_coef) * x.sum(-1)) + base) + bias in float32 in that order, one rounding."""
     _fields_ = [
         ("bias", ctypes.c_void_p),
         ("base", ctypes.c_void_p),

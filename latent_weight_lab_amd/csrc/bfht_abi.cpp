@@ -289,15 +289,34 @@ int check_linear_jobs(int dtype, const lwl_bfht_linear_job* jobs, int64_t count,
     v[(size_t)i].out = j.out;
     v[(size_t)i].epi = epilogue_of(j.epilogue);
   }
-  if (need_ptrs)
-    for (int64_t a = 0; a < count; ++a)
-      for (int64_t b = a + 1; b < count; ++b) {
-        const uintptr_t x0 = (uintptr_t)jobs[a].out, y0 = (uintptr_t)jobs[b].out;
-        const uintptr_t x1 = x0 + (uintptr_t)(jobs[a].tokens * jobs[a].out_features * esize);
-        const uintptr_t y1 = y0 + (uintptr_t)(jobs[b].tokens * jobs[b].out_features * esize);
-        if (x1 > x0 && y1 > y0 && x0 < y1 && y0 < x1)
+  if (need_ptrs) {
+    // [p, p + bytes) ranges; empty ranges and null pointers overlap nothing
+    auto overlap = [](const void* p, int64_t bytes, const void* q, int64_t qbytes) {
+      const uintptr_t x0 = (uintptr_t)p, y0 = (uintptr_t)q;
+      return p && q && bytes > 0 && qbytes > 0 && x0 < y0 + (uintptr_t)qbytes && y0 < x0 + (uintptr_t)bytes;
+    };
+    for (int64_t a = 0; a < count; ++a) {
+      const int64_t out_bytes = jobs[a].tokens * jobs[a].out_features * esize;
+      for (int64_t b = 0; b < count; ++b) {
+        const lwl_bfht_linear_job& jb = jobs[b];
+        if (b > a && overlap(jobs[a].out, out_bytes, jb.out, jb.tokens * jb.out_features * esize))
           return fail(LWL_ERR_INVALID, "jobs %lld and %lld write overlapping outputs", (long long)a, (long long)b);
+        // jobs do not run in job order (grouped ones share launches), so no job may
+        // read what another job writes (a job's own operands follow its single call)
+        if (b == a) continue;
+        const lwl_bfht_linear_epilogue* e = jb.tokens > 0 ? jb.epilogue : nullptr;
+        const char* what = overlap(jobs[a].out, out_bytes, jb.input, jb.tokens * jb.in_features * esize) ? "input"
+                         : overlap(jobs[a].out, out_bytes, jb.latent, jb.tokens > 0 ? jb.latent_size * esize : 0)
+                             ? "latent"
+                         : (e && overlap(jobs[a].out, out_bytes, e->base, jb.tokens * jb.out_features * esize))
+                             ? "base"
+                         : (e && overlap(jobs[a].out, out_bytes, e->bias, jb.out_features * esize)) ? "bias"
+                                                                                                    : nullptr;
+        if (what)
+          return fail(LWL_ERR_INVALID, "job %lld's output overlaps job %lld's %s", (long long)a, (long long)b, what);
       }
+    }
+  }
   if (out) *out = std::move(v);
   return LWL_OK;
 }
@@ -433,12 +452,13 @@ int lwl_bfht_backward_noalloc(const void* grad_out, int dtype, int64_t latent_si
                 "lwl_bfht_backward_noalloc: this call needs %zu bytes of scratch, more than the %zu of its "
                 "device array; call lwl_bfht_backward with a workspace",
                 need, (size_t)LWL_BFHT_NOALLOC_SCRATCH_BYTES);
-  void* work = nullptr;
-  if (need > 0) {
-    hipError_t e = hipSuccess;
-    work = lwl::noalloc_scratch((hipStream_t)stream, &e);
-    if (!work) return hip_status(e, "lwl_bfht_backward_noalloc: scratch address");
-  }
+  // every accepted call resolves the device's array address (the first one per
+  // device asks hipGetSymbolAddress; later ones read the cached address), even
+  // one that needs no scratch, so a caller can settle it before a graph capture
+  hipError_t e = hipSuccess;
+  void* scratch = lwl::noalloc_scratch((hipStream_t)stream, &e);
+  if (!scratch) return hip_status(e, "lwl_bfht_backward_noalloc: scratch address");
+  void* work = need > 0 ? scratch : nullptr;
   a.src = grad_out;
   a.dst = grad_latent;
   a.work = work;

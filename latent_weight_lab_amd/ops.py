@@ -106,9 +106,10 @@ def linear_forward(x2d: torch.Tensor, latent: torch.Tensor, out_features: int, l
     """Fused ``x @ (weight_scale * W)^T`` with W generated on chip (reference
     ext.linear_forward, ``csrc/block_fht_ext_cuda.cu:624-681``).  With any of ``bias``
     ``[out]``, ``base`` ``[tokens, out]`` (both of x's dtype) or ``row_sum_coef`` (a device
-    scalar) the kernels' stores add ``base + row_sum_scale * row_sum_coef * x.sum(-1) + bias``
-    in float32 before the one rounding (``lwl_bfht_linear_forward_ex``; reference
-    ``forward_fused``'s tail, ``block_fht.py:493-500``)."""
+    scalar) the kernels' stores form ``((weight_scale * x W^T + row_sum_scale * row_sum_coef *
+    x.sum(-1)) + base) + bias`` in float32, in that order, before the one rounding
+    (``lwl_bfht_linear_forward_ex``; the order of the reference ``forward_fused``'s tail,
+    ``block_fht.py:493-500``)."""
     dev = N.require_cuda(x2d, latent)
     x2d = x2d.contiguous()
     latent = latent.contiguous()

@@ -3,6 +3,7 @@ declared symbol, shares torch's HIP runtime, and validates arguments with the
 reference's messages — without launching anything."""
 from __future__ import annotations
 
+import ctypes
 import re
 from pathlib import Path
 
@@ -98,6 +99,20 @@ def test_workspace_sizes():
     assert lib.lwl_bfht_backward_workspace_size(1 << 23, 1 << 26, 0, 1 << 26) == 8 * (1 << 23) * 4
 
 
+def test_noalloc_backward_refuses_oversized_scratch_on_the_host():
+    """lwl_bfht_backward_noalloc refuses a call whose scratch exceeds its 32 MiB device array
+    before any HIP call: config 3 at 2^20 needs a 256 MiB work buffer.  The pointers are fake
+    (never dereferenced); were the guard to let the call through, it would fail here with a
+    HIP error (no device), not touch memory."""
+    lib = N.lib()
+    need = lib.lwl_bfht_backward_workspace_size(1 << 20, 1 << 26, 0, 1 << 26)
+    assert need > 32 << 20
+    rc = lib.lwl_bfht_backward_noalloc(0x10000, 0, 1 << 20, 1 << 26, 3, 99, 0, 1 << 26, 0x20000, None)
+    assert rc == N.LWL_ERR_UNSUPPORTED
+    msg = lib.lwl_last_error().decode()
+    assert "bytes of scratch" in msg and str(need) in msg
+
+
 def test_cpu_tensors_fail_loudly():
     from latent_weight_lab_amd import BlockFHT
 
@@ -122,6 +137,31 @@ def test_module_metadata_and_validation():
         BlockFHT(torch.zeros(2, 2), size=10)
     layer = BlockFHTLinear(768, 3072, latent_dim=32768, layers=3, seed=3)
     assert layer.generator.block_size == 32768 and layer.generator.size == 768 * 3072
+
+
+@pytest.mark.parametrize("fin,fout,seed,rank", [(8, 12, 9, 2), (768, 3072, 5, 4), (5, 7, -40, 3)])
+def test_spectral_buffers_are_persistent_walsh_columns(fin, fout, seed, rank):
+    """BlockFHTLinear's spectral_u / spectral_v (reference block_fht.py:411-412,426-435) travel
+    in the state dict and hold columns seed + 17 .. and seed + 31 .. of the order-n Sylvester
+    matrix over sqrt(n): entry (i, j) = (-1)^popcount(i & (first + j)) / sqrt(n), rows 0 .. n-1
+    (n need not be a power of two: the rows are truncated)."""
+    import math
+
+    import numpy as np
+
+    from latent_weight_lab_amd import BlockFHTLinear
+
+    layer = BlockFHTLinear(fin, fout, latent_dim=8, layers=2, seed=seed, spectral_rank=rank)
+    sd = layer.state_dict()
+    for name, n, first in (("spectral_u", fout, seed + 17), ("spectral_v", fin, seed + 31)):
+        assert name in sd
+        cols = [first + j for j in range(rank)]
+        # negative column indices (seed < -31) follow the two's-complement int64 AND
+        signs = [[1.0 - 2.0 * (bin((i & c) & ((1 << 64) - 1)).count("1") & 1) for c in cols] for i in range(n)]
+        # the reference divides the float32 signs by the Python float sqrt(n) (block_fht.py:435)
+        want = torch.tensor(signs, dtype=torch.float32) / math.sqrt(n)
+        assert torch.equal(sd[name], want), name
+        assert np.allclose(sd[name].double().numpy(), np.array(signs) / np.sqrt(n), rtol=1e-7, atol=0), name
 
 
 def test_sign_word_api_matches_oracle():
@@ -354,6 +394,27 @@ def test_linear_jobs_validation():
     arr = (N.LinearJob * 2)(linear_job(1, 768, 2304, 32768, out=0x100000), linear_job(1, 768, 768, 32768, out=0x100010))
     assert lib.lwl_bfht_check_linear_jobs(2, arr, 2) == N.LWL_ERR_INVALID
     assert "overlapping" in lib.lwl_last_error().decode()
+    # an output over another job's input, latent, base or bias (jobs do not run in job order)
+    for kw, what in ((dict(inp=0x100000), "input"), (dict(lat=0x100100), "latent")):
+        arr = (N.LinearJob * 2)(linear_job(1, 768, 2304, 32768, out=0x100000),
+                                linear_job(1, 768, 768, 32768, out=0x200000, **kw))
+        assert lib.lwl_bfht_check_linear_jobs(2, arr, 2) == N.LWL_ERR_INVALID
+        assert f"job 0's output overlaps job 1's {what}" in lib.lwl_last_error().decode()
+    for field, ptr, what in (("base", 0x200400, "base"), ("bias", 0x2005fe, "bias")):
+        epi = N.LinearEpilogue()
+        setattr(epi, field, ptr)
+        j1 = linear_job(1, 768, 2304, 32768, out=0x100000)
+        j1.epilogue = ctypes.pointer(epi)
+        arr = (N.LinearJob * 2)(j1, linear_job(1, 768, 768, 32768, out=0x200000))
+        assert lib.lwl_bfht_check_linear_jobs(2, arr, 2) == N.LWL_ERR_INVALID
+        assert f"job 1's output overlaps job 0's {what}" in lib.lwl_last_error().decode()
+    # a job's own base may be its output (in place, as its single call allows)
+    epi = N.LinearEpilogue()
+    epi.base = 0x100000
+    j0 = linear_job(1, 768, 2304, 32768, out=0x100000)
+    j0.epilogue = ctypes.pointer(epi)
+    arr = (N.LinearJob * 2)(j0, linear_job(1, 768, 768, 32768, out=0x200000))
+    assert lib.lwl_bfht_check_linear_jobs(2, arr, 2) == N.LWL_OK
     # a job outside every fused kernel names its index
     arr = (N.LinearJob * 2)(linear_job(1, 768, 2304, 32768), linear_job(1, 768, 64, 16384, out=0x200000))
     assert lib.lwl_bfht_check_linear_jobs(2, arr, 2) == N.LWL_ERR_UNSUPPORTED

@@ -27,6 +27,13 @@ def disturb():
     ops.backward(torch.randn(5000, device="cuda", generator=g), 3000, torch.float32, 5000, 2, 4, 0, 5000)
     x = torch.randn(20, 768, device="cuda", generator=g).to(torch.bfloat16)
     ops.linear_forward(x, lat, 768, 3, 5, 1.0)
+    # the no-allocation backward on another shape: replays then run over its reused scratch array
+    gr = torch.randn(108_618, device="cuda", generator=g)
+    gl = torch.empty(1024, device="cuda")
+    lib = N.lib()
+    rc = lib.lwl_bfht_backward_noalloc(gr.data_ptr(), N.dtype_code(torch.float32), 1024, 108_618, 3, 123, 0,
+                                       108_618, gl.data_ptr(), ctypes.c_void_p(N.stream_ptr(gr.device)))
+    assert rc == N.LWL_OK, lib.lwl_last_error().decode()
 
 
 def check_graph(fn):

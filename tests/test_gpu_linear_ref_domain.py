@@ -75,6 +75,9 @@ CASES = [
     (64, 2048, 40, 16384, 3, 7, 1.0),   # 16 rows per 16-bit tile; float32 (8 rows) stays on VALU
     (2048, 128, 512, 1024, 2, 9, 0.5),  # block 2^10, token splits
     (80, 16, 64, 64, 1, 10, 1.0),       # in 16: float32 on the matrix cores, 16-bit on VALU
+    # block 2^5, the matrix-core kernel's smallest: 256 blocks per generator call, 4 calls per tile
+    (64, 32, 48, 32, 2, 3, 1.0),        # 16-bit and float32 on the matrix cores (48 of 1024 table rows)
+    (80, 16, 40, 32, 1, 4, 1.0),        # float32 on the matrix cores, 16-bit on VALU
 ]
 
 
