@@ -402,11 +402,21 @@ __device__ __forceinline__ void reg_butterflies(float (&v)[32]) {
 // wave-uniform one per register: the 32 loads are issued back to back without
 // per-element addresses, and range limits (latent length, slice ends) are
 // buffer bounds.  SRC / DST are compile-time.
+//
+// DST = kDstSum (the backward's last pass): instead of one partial row per
+// block, workgroup (tile, group) walks tile `tile` of the group's blocks
+// group * group_blocks .. in ascending order (the next block's tile loading
+// while the current one transforms) and adds each block's scaled result in
+// registers; at the end it stores the sum of its group: straight to the latent
+// gradient (dst_io, the first n positions) when there is one group, else into
+// the work buffer's row of the group's first block (read by no other
+// workgroup, and by this one before it is written), for the block sum over
+// the groups.
 template <class T, int SRC, int DST, int TL>
 __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
     const T* __restrict__ src_io, float* __restrict__ work, T* __restrict__ dst_io, int LB, int pre, int post,
     int n, int64_t first_block, int64_t ntiles_total, int64_t start, int64_t stop, uint32_t seed32, int sign_layer,
-    float scale) {
+    float scale, int64_t group_blocks, int ngroups) {
   __shared__ float lds[kTilePadded];
   __shared__ uint32_t words[kTileElems / 32];
   static_assert(kTileElems / 32 == kTileThreads, "one sign word per thread");
@@ -480,11 +490,34 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
       for (int r = 0; r < 32; ++r) lds[group_lds<kTileLog, 5>(b, r, lo, nb)] = v[r];
     }
   };
+  // the tiles this workgroup walks: t0, t0 + t_step, ... below t_end
+  int64_t t0 = blockIdx.x, t_step = gridDim.x, t_end = ntiles_total;
+  int sum_tile = 0;
+  int64_t sum_group = 0;
+  float acc[32];
+  if constexpr (DST == kDstSum) {
+    sum_tile = (int)(blockIdx.x & ((1u << tiles_log) - 1));
+    sum_group = (int64_t)(blockIdx.x >> tiles_log);
+    const int64_t nblk = ntiles_total >> tiles_log;
+    const int64_t b0 = sum_group * group_blocks;
+    const int64_t b1 = b0 + group_blocks < nblk ? b0 + group_blocks : nblk;
+    t0 = (b0 << tiles_log) | sum_tile;
+    t_step = (int64_t)1 << tiles_log;
+    t_end = b1 << tiles_log;
+#pragma unroll
+    for (int r = 0; r < 32; ++r) acc[r] = 0.0f;
+  }
+  // The next tile's loads are in flight during the current one's transforms,
+  // except in a summing pass over high tiles that go through LDS (blocks above
+  // 2^20): there the sum's 32 registers leave no room for them beside the
+  // transform's, and each tile is loaded at the start of its own iteration.
+  constexpr bool kPrefetch = !(DST == kDstSum && high && G::kExtra > 0);
   float x[32];
-  int64_t t = blockIdx.x;
-  if (t < ntiles_total) load_tile(geo(t), x);
-  for (; t < ntiles_total; t += gridDim.x) {
+  int64_t t = t0;
+  if (kPrefetch && t < t_end) load_tile(geo(t), x);
+  for (; t < t_end; t += t_step) {
     const Geo g = geo(t);
+    if constexpr (!kPrefetch) load_tile(g, x);
     float v[32];
     __syncthreads();  // the previous tile's reads of lds and of the sign table are done
     const uint32_t my_word = sign_word(block_key(seed32, g.block), layer_key(sign_layer), pos(32u * tid, g.tile) >> 5);
@@ -492,7 +525,7 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
     if constexpr (G::kExtra == 0) {
 #pragma unroll
       for (int r = 0; r < 32; ++r) v[r] = x[r];
-      if (t + gridDim.x < ntiles_total) load_tile(geo(t + gridDim.x), x);  // in flight during the transforms
+      if (t + t_step < t_end) load_tile(geo(t + t_step), x);  // in flight during the transforms
       if (pre) reg_butterflies<G::kRegLo>(v);
       __syncthreads();  // the sign table is complete
       tile_signs<10, 5>(words, v, tid);
@@ -500,7 +533,7 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
     } else {
       if (pre) reg_butterflies<G::kRegLo>(x);
       group_rw(x, 10, 5, false);
-      if (t + gridDim.x < ntiles_total) load_tile(geo(t + gridDim.x), x);  // in flight during the transforms
+      if (kPrefetch && t + t_step < t_end) load_tile(geo(t + t_step), x);  // in flight during the transforms
       // downwards: the groups of the first transform (without one, straight to
       // the last group's layout), then the sign layer
       if (pre) {
@@ -552,14 +585,26 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
 #pragma unroll
     for (int r = 0; r < 32; ++r) {
       const float vs = v[r] * scale;
-      if constexpr (DST == kDstWork) {
+      if constexpr (DST == kDstSum) {
+        acc[r] += vs;
+      } else if constexpr (DST == kDstWork) {
         buf_store<float>(vs, tile_rsrc(work + g.slot * B, (uint64_t)B * 4), g.pt + pr(r));
-      } else if constexpr (DST == kDstOut) {
+      } else {
+        static_assert(DST == kDstOut, "tile pass destinations: work buffer, output slice, block sum");
         T* o0 = dst_io + (g.base + g.lo - start);
         buf_store<T>(vs, tile_rsrc(o0, (uint64_t)(g.hi - g.lo) * sizeof(T)), g.pt + pr(r) - (int)g.lo);
-      } else {  // kDstPartial: the first n positions, left in the work buffer
-        buf_store<float>(vs, tile_rsrc(work + g.slot * B, (uint64_t)n * 4), g.pt + pr(r));
       }
+    }
+  }
+  if constexpr (DST == kDstSum) {
+    const int pt = (int)pos((uint32_t)tid, sum_tile);
+    if (ngroups == 1) {
+#pragma unroll
+      for (int r = 0; r < 32; ++r) buf_store<T>(acc[r], tile_rsrc(dst_io, (uint64_t)n * sizeof(T)), pt + pr(r));
+    } else {
+      float* row = work + sum_group * group_blocks * B;
+#pragma unroll
+      for (int r = 0; r < 32; ++r) buf_store<float>(acc[r], tile_rsrc(row, (uint64_t)n * 4), pt + pr(r));
     }
   }
 }
@@ -604,14 +649,14 @@ static hipError_t dispatch_block(int LB, bool fwd, const BfhtArgs& a, hipStream_
 // Passes that neither read nor write the I/O type run the float instantiation.
 template <class T, int SRC, int DST>
 static hipError_t launch_tile_kind(const BfhtArgs& a, hipStream_t s, int tl, int pre, int post, int layer,
-                                   float scale, unsigned grid) {
+                                   float scale, unsigned grid, int64_t group_blocks = 0, int ngroups = 0) {
   const int64_t ntiles = a.nblocks << (a.log_block - kTileLog);
-  constexpr bool typed = SRC != kSrcWork || DST == kDstOut;
+  constexpr bool typed = SRC != kSrcWork || DST == kDstOut || DST == kDstSum;
   using U = std::conditional_t<typed, T, float>;
 #define LWL_TILE(TL)                                                                                      \
   hipLaunchKernelGGL((bfht_tile_pass<U, SRC, DST, TL>), dim3(grid), dim3(kTileThreads), 0, s,            \
                      (const U*)a.src, (float*)a.work, (U*)a.dst, a.log_block, pre, post, (int)a.n,         \
-                     a.first_block, ntiles, a.start, a.stop, a.seed32, layer, scale)
+                     a.first_block, ntiles, a.start, a.stop, a.seed32, layer, scale, group_blocks, ngroups)
   switch (tl) {
     case 0: LWL_TILE(0); break;
     case 1: if constexpr (SRC == kSrcWork) LWL_TILE(1); break;
@@ -635,8 +680,7 @@ static hipError_t launch_tile_pass(const BfhtArgs& a, hipStream_t s, int src, in
   if (src == kSrcLatent) return launch_tile_kind<T, kSrcLatent, kDstWork>(a, s, 0, pre, post, layer, scale, grid);
   if (src == kSrcGrad) return launch_tile_kind<T, kSrcGrad, kDstWork>(a, s, 0, pre, post, layer, scale, grid);
   if (dst == kDstWork) return launch_tile_kind<T, kSrcWork, kDstWork>(a, s, tl, pre, post, layer, scale, grid);
-  if (dst == kDstOut) return launch_tile_kind<T, kSrcWork, kDstOut>(a, s, tl, pre, post, layer, scale, grid);
-  return launch_tile_kind<T, kSrcWork, kDstPartial>(a, s, tl, pre, post, layer, scale, grid);
+  return launch_tile_kind<T, kSrcWork, kDstOut>(a, s, tl, pre, post, layer, scale, grid);
 }
 
 // Blocks above 2^15: H = H_low (x) H_high over block bits 0-14 and 15..LB-1,
@@ -645,7 +689,11 @@ static hipError_t launch_tile_pass(const BfhtArgs& a, hipStream_t s, int src, in
 // (L + 1 passes, each one read and one write of the float32 work buffer).
 // Pass k >= 1 completes layer k - 1 and applies its 2^(-LB/2).  The backward
 // runs the same schedule on grad with the sign layers in reverse (D_L first,
-// D_0 last) and leaves partial rows of n values for the block sum.
+// D_0 last); its last pass (kDstSum) also sums the blocks: each workgroup adds
+// one tile position range over a group of blocks, with enough groups to give
+// every CU a workgroup, and only with more than one group does a block sum
+// over the groups' rows follow (config 3: 2^20 blocks, 64 blocks in 8 groups,
+// 32 MiB of rows instead of 256 MiB; 2^23, 8 blocks in one group, no rows).
 // Workgroups of the persistent tile passes: one per CU (a workgroup takes all
 // of a CU's LDS), never more than the tiles.
 // The CU count of the current device, cached per device: each slot is written
@@ -670,20 +718,33 @@ static unsigned tile_grid(int64_t ntiles) {
 
 template <class T>
 static hipError_t run_tiles(const BfhtArgs& a, hipStream_t s, bool fwd) {
-  const unsigned grid = tile_grid(a.nblocks << (a.log_block - kTileLog));
+  const int64_t tiles_per_block = (int64_t)1 << (a.log_block - kTileLog);
+  const unsigned grid = tile_grid(a.nblocks * tiles_per_block);
   const int L = a.layers;
   const int LB = a.log_block;
   const float norm = (LB & 1) ? 0.70710678118654752440f / (float)(1 << (LB >> 1)) : 1.0f / (float)(1 << (LB >> 1));
+  // the backward's summing last pass: groups of group_blocks blocks, one
+  // workgroup per (tile, group), at least as many workgroups as CUs where the
+  // blocks allow, no empty group
+  const int64_t cus = tile_grid(INT64_MAX);
+  int64_t ngroups = std::min<int64_t>(std::max<int64_t>((cus + tiles_per_block - 1) / tiles_per_block, 1), a.nblocks);
+  const int64_t group_blocks = (a.nblocks + ngroups - 1) / ngroups;
+  ngroups = (a.nblocks + group_blocks - 1) / group_blocks;
   for (int k = 0; k <= L; ++k) {
     const int src = k == 0 ? (fwd ? kSrcLatent : kSrcGrad) : kSrcWork;
-    const int dst = k == L ? (fwd ? kDstOut : kDstPartial) : kDstWork;
     const int tl = (k & 1) ? LB - kTileLog : 0;  // odd passes run high tiles
-    const hipError_t e = launch_tile_pass<T>(a, s, src, dst, tl, (int)(k > 0), (int)(k < L), fwd ? k : L - k,
-                                             k > 0 ? norm : 1.0f, grid);
+    const float scale = k > 0 ? norm : 1.0f;
+    hipError_t e;
+    if (k == L && !fwd)
+      e = launch_tile_kind<T, kSrcWork, kDstSum>(a, s, tl, (int)(k > 0), 0, 0, scale,
+                                                  (unsigned)(tiles_per_block * ngroups), group_blocks, (int)ngroups);
+    else
+      e = launch_tile_pass<T>(a, s, src, k == L ? kDstOut : kDstWork, tl, (int)(k > 0), (int)(k < L),
+                              fwd ? k : L - k, scale, grid);
     if (e != hipSuccess) return e;
   }
-  if (fwd) return hipSuccess;
-  return launch_reduce<T>((const float*)a.work, a.nblocks, (int64_t)1 << a.log_block, a.n, (T*)a.dst, s);
+  if (fwd || ngroups == 1) return hipSuccess;
+  return launch_reduce<T>((const float*)a.work, ngroups, group_blocks << a.log_block, a.n, (T*)a.dst, s);
 }
 
 template <class T>

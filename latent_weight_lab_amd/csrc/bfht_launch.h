@@ -16,7 +16,7 @@ constexpr int kWholeBlockMaxLog = 15;
 
 // tile-pass prologues / epilogues
 enum { kSrcLatent = 0, kSrcGrad = 1, kSrcWork = 2 };
-enum { kDstWork = 0, kDstOut = 1, kDstPartial = 2 };
+enum { kDstWork = 0, kDstOut = 1, kDstSum = 2 };
 
 struct BfhtArgs {
   int dtype;

@@ -319,6 +319,28 @@ def test_tile_pass_block_sizes(log_block, layers, dtype):
     assert rel_l2(to_np(gl), gwant) < TOL[dtype]
 
 
+@pytest.mark.parametrize("log_block,nblocks,layers,dtype", [
+    (16, 301, 3, torch.float32),    # 2 tiles per block: 101 groups of 3 blocks, the last of 1, then the group sum
+    (21, 13, 2, torch.bfloat16),    # 64 tiles per block: 4 groups of 4, the last of 1; even L ends on a low pass
+    (22, 3, 1, torch.float32),      # 128 tiles per block: one group, summed straight into grad_latent
+])
+def test_tile_pass_grouped_block_sum(log_block, nblocks, layers, dtype):
+    """The backward's last tile pass sums the blocks: workgroup (tile, group) adds one tile's
+    positions over a group of blocks in ascending order, with more than one group a block sum
+    over the groups' rows follows.  Full-size backward against the C oracle, reruns bit-identical."""
+    B = 1 << log_block
+    n = B - 5
+    size = nblocks * B - 11
+    g = torch.randn(size, generator=torch.Generator().manual_seed(nblocks)).to(dtype)
+    gd = g.cuda()
+    gl = ops.backward(gd, n, dtype, size, layers, 31, 0, size)
+    gl2 = ops.backward(gd, n, dtype, size, layers, 31, 0, size)
+    torch.cuda.synchronize()
+    assert torch.equal(gl, gl2)
+    gwant = c_oracle.backward(g.double().numpy(), n, size, layers, 31, 0, size)
+    assert rel_l2(to_np(gl), gwant) < TOL[dtype]
+
+
 def test_reference_2_23_smoke():
     # reference tests/test_block_fht_cuda.py:34-40
     bfht = BlockFHT((1 << 23) - 17, size=1 << 23, layers=1, seed=9).cuda()
