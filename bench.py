@@ -141,34 +141,11 @@ def time_graph(torch, fn, steps: int, warmup: int) -> float:
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
-    # The GPU spins (a bounded clock loop) while the host submits the graph, so that the start
-    # event is reached with the K launches already queued: the events then time the K steps'
-    # device work, not the host's submission latency (a fixed ~20 us that a 20-step graph would
-    # otherwise add to every step as ~1 us).
-    gpu_spin(torch, 300e-6)
     start.record()
     g.replay()
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / 1e3 / steps
-
-
-_SPIN_CYCLES_PER_S = None
-
-
-def gpu_spin(torch, seconds: float) -> None:
-    """Enqueue a kernel that spins on the device clock for about `seconds` (torch.cuda._sleep,
-    calibrated once against events)."""
-    global _SPIN_CYCLES_PER_S
-    if _SPIN_CYCLES_PER_S is None:
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(1000)
-        a.record()
-        torch.cuda._sleep(1_000_000)
-        b.record()
-        torch.cuda.synchronize()
-        _SPIN_CYCLES_PER_S = 1_000_000 / max(a.elapsed_time(b) / 1e3, 1e-6)
-    torch.cuda._sleep(int(seconds * _SPIN_CYCLES_PER_S))
 
 
 def time_eager(torch, fn, steps: int, warmup: int) -> float:

@@ -182,6 +182,7 @@ lwl::LinearArgs plan_linear(int dtype, int64_t tokens, int64_t in_features, int6
   a.blocks_per_wg = 1;
   if (linear_uses_mfma(a)) {
     a.blocks_per_wg = lwl::linear_blocks_per_wg(a);
+    a.rows_per_tile = lwl::linear_rows_per_tile(a);
     a.token_splits = lwl::linear_token_splits(a);
   } else if (lwl::linear_small_mm_applicable(a)) {
     a.token_splits = lwl::linear_small_mm_token_splits(a);

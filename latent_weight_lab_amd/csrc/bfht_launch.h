@@ -73,6 +73,7 @@ struct LinearArgs {
   int layers;
   float weight_scale;
   int blocks_per_wg;   // generated blocks per workgroup (linear_blocks_per_wg)
+  int rows_per_tile;   // > 0: tiles of this many whole rows instead (linear_rows_per_tile)
   int token_splits;
   LinearEpi epi;       // all null: plain out = weight_scale * x @ W^T
 };
@@ -90,7 +91,8 @@ extern const bool kLinearKernelAvailable;
 // generated block, and their k-major table fits in the LDS).
 bool linear_applicable(int dtype, int log_block, int64_t in_features);
 int linear_blocks_per_wg(const LinearArgs& a);  // needs tokens, in/out features, nblocks_w
-int linear_token_splits(const LinearArgs& a);     // needs blocks_per_wg
+int linear_rows_per_tile(const LinearArgs& a);  // needs blocks_per_wg
+int linear_token_splits(const LinearArgs& a);     // needs blocks_per_wg, rows_per_tile
 // Workspace of one call: float32 partial dot products of the rows that
 // straddle two blocks, then (for large batches) x re-laid out in MFMA order.
 size_t linear_workspace_bytes(const LinearArgs& a);

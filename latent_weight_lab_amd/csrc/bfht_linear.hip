@@ -141,6 +141,7 @@ bool linear_tiled(const LinearArgs& a) {
 }
 
 size_t partial_bytes(const LinearArgs& a) {
+  if (a.rows_per_tile > 0) return 0;  // row tiles: no straddling rows
   const int64_t ntiles = (a.nblocks_w + a.blocks_per_wg - 1) / a.blocks_per_wg;
   return ((size_t)ntiles * 2 * (size_t)a.tokens * sizeof(float) + 255) / 256 * 256;
 }
@@ -187,20 +188,27 @@ __global__ __launch_bounds__(256) void bfht_linear_tile_x(const unsigned char* _
 // (>= the tile's output rows; 16*NT when that fits in the LDS, else exact and
 // the last row tile masked on read).  kEpi: the stores apply `ep` (a separate
 // instantiation, so the plain kernels carry none of its code or registers).
-template <int L, int NT, bool kTiled, int KB, bool kEpi, int KG = kGroup, int KD = kDepth>
+// kRowTiles (KB = 2): the tile is rows tile*rows_per_tile .. + rows_per_tile - 1
+// instead, whole rows that lie in the two generated blocks starting at the
+// block of its first position (linear_rows_per_tile), so no row straddles two
+// tiles: the generated positions outside the tile are dropped, every row is
+// stored directly, and no partial dot products or combine are needed.
+template <int L, int NT, bool kTiled, int KB, bool kEpi, bool kRowTiles = false, int KG = kGroup, int KD = kDepth>
 __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const __bf16* __restrict__ latent,
                                             __bf16* __restrict__ out, float* __restrict__ partial, int tokens,
                                             int in_f, int out_f, int n, uint32_t seed32, float scale,
                                             int token_split, int64_t nblocks, int pitch, int split, int64_t tile,
-                                            const LinearEpi& ep, unsigned char* lds) {
-
+                                            const LinearEpi& ep, unsigned char* lds, int rows_per_tile = 0) {
+  static_assert(!kRowTiles || KB == 2, "row tiles span two generated blocks");
   const int64_t size = (int64_t)in_f * out_f;
-  const int64_t g0 = tile * KB * kB;                          // first flat position
-  const int64_t g1 = (g0 + KB * kB < size) ? g0 + KB * kB : size;  // one past the last
+  const int64_t tile_len = kRowTiles ? (int64_t)rows_per_tile * in_f : (int64_t)KB * kB;
+  const int64_t g0 = tile * tile_len;                             // first flat position
+  const int64_t g1 = (g0 + tile_len < size) ? g0 + tile_len : size;  // one past the last
+  const int64_t b_first = g0 >> kLog;                             // first generated block
   const int o_first = (int)(g0 / in_f);
   const int o_last = (int)((g1 - 1) / in_f);
-  const bool first_partial = (g0 % in_f) != 0;
-  const bool last_partial = (g1 % in_f) != 0;
+  const bool first_partial = !kRowTiles && (g0 % in_f) != 0;
+  const bool last_partial = !kRowTiles && (g1 % in_f) != 0;
   // k steps, padded to whole prefetch rounds: the padding reads zeros (table
   // rows past the row length are zero, x offsets past it are out of range)
   const int nsteps = linear_steps(in_f);
@@ -217,13 +225,18 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     const int row_chunks = in_f >> 3;                   // chunks holding data in a row
     const int c_first = (int)(g0 - (int64_t)o_first * in_f) >> 3;  // first chunk of row 0 in the tile
     const int c_last = (int)(g1 - (int64_t)o_last * in_f) >> 3;    // chunks of the last row in the tile
-    // block position p of block kb -> tile-relative flat offset rel = base_rel + kb * kB + p,
-    // row r = rel / in_f (rel < in_f + KB * kB: float quotient, corrected by one)
+    // block position p of generated block kb -> offset rel = off + kb * kB + p from the
+    // start of row o_first (block tiles: off = the tile's start in that row; row tiles:
+    // the first block's start, at or before g0), row r = rel / in_f (|rel| < in_f +
+    // KB * kB: float quotient, corrected by one); kept where g0 <= flat < g1
     const int base_rel = c_first << 3;
+    const int off = kRowTiles ? (int)((b_first << kLog) - g0) : base_rel;
+    const int rel_lo = base_rel, rel_hi = (int)(g1 - (int64_t)o_first * in_f);
     const float inv_in = 1.0f / (float)in_f;
     u32x4 v[KB][8];
-    if (KB == 2 && tile * KB + 1 < nblocks) {  // both blocks at once (uniform across the workgroup)
-      const Ctx c[2] = {make_ctx(seed32, tile * KB), make_ctx(seed32, tile * KB + 1)};
+    const bool two = kRowTiles ? g1 > ((b_first + 1) << kLog) : (KB == 2 && tile * KB + 1 < nblocks);
+    if (KB == 2 && two) {  // both blocks at once (uniform across the workgroup)
+      const Ctx c[2] = {make_ctx(seed32, b_first), make_ctx(seed32, b_first + 1)};
       u32x4 src[kTiles][2];
       load_latent(c[0], latent, n, src);
       f32x16 acc[2][kTiles];
@@ -231,8 +244,8 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       run_chain2<L>(acc, c, lds, src, [](int i) { return i; }, nw);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) out_chunks<L>(acc[kb], nw[kb], c[kb], v[kb]);
-    } else {  // one block (KB = 1, or the last tile of an odd block count)
-      const Ctx c = make_ctx(seed32, tile * KB);
+    } else {  // one block (KB = 1, the last tile of an odd block count, or a row tile inside one block)
+      const Ctx c = make_ctx(seed32, b_first);
       u32x4 src[kTiles][2];
       load_latent(c, latent, n, src);
       f32x16 acc[kTiles];
@@ -263,17 +276,19 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
         table[table_slot(kc, r, pitch)] = u32x4{0u, 0u, 0u, 0u};
       }
     }
-    const Ctx c = make_ctx(seed32, tile * KB);  // chunk positions do not depend on the block
+    const Ctx c = make_ctx(seed32, b_first);  // chunk positions do not depend on the block
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
+      if (kRowTiles && kb > 0 && !two) break;  // uniform: no second block
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const int rel = base_rel + kb * kB + out_chunk_pos<L>(c, k);
+        const int rel = off + kb * kB + out_chunk_pos<L>(c, k);
         int r = (int)((float)rel * inv_in);
         r -= r * in_f > rel;
         r += (r + 1) * in_f <= rel;
         const int kc = (rel - r * in_f) >> 3;
-        if (g0 + rel - base_rel < g1) table[table_slot(kc, r, pitch)] = v[kb][k];
+        // chunks of 8 positions lie wholly inside or outside [g0, g1) (all multiples of 8)
+        if (rel >= rel_lo && rel < rel_hi) table[table_slot(kc, r, pitch)] = v[kb][k];
       }
     }
   }
@@ -435,7 +450,7 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
           __builtin_amdgcn_raw_buffer_store_b16(b, o_r, out_off(nt, r), 0, 0);
         }
         // partial rows: the first row of the tile (nt 0, l16 0) and its last row
-        if (nt == 0 || 16 * (nt + 1) > o_last - o_first) {
+        if (!kRowTiles && (nt == 0 || 16 * (nt + 1) > o_last - o_first)) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int m = 4 * kq + r;
@@ -467,27 +482,28 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     for (int tg = rest0 + KG * wave; tg < tt1; tg += KG * kWaves) pass(std::integral_constant<int, KG>{}, tg, tt1);
   }
 }
-template <int L, int NT, bool kTiled, int KB, bool kEpi, int KG = kGroup, int KD = kDepth>
+template <int L, int NT, bool kTiled, int KB, bool kEpi, bool kRowTiles = false, int KG = kGroup, int KD = kDepth>
 __global__ __launch_bounds__(kThreads) void bfht_linear_mfma15(const __bf16* __restrict__ x,
                                                                const __bf16* __restrict__ latent,
                                                                __bf16* __restrict__ out,
                                                                float* __restrict__ partial, int tokens,
                                                                int in_f, int out_f, int n, uint32_t seed32,
                                                                float scale, int token_split, int64_t nblocks,
-                                                               int pitch, LinearEpi ep) {
+                                                               int pitch, LinearEpi ep, int rows_per_tile) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLinearLdsBytes];
   // XCD-aware work order: workgroup i runs on XCD i % 8, and work item
   // p = split * ntiles + tile (split-major) goes to XCD p / per_xcd, so each
   // XCD's L2 holds the x rows of one or two token splits instead of all of x.
-  const int64_t ntiles = (nblocks + KB - 1) / KB;
+  const int64_t ntiles = kRowTiles ? (out_f + rows_per_tile - 1) / rows_per_tile : (nblocks + KB - 1) / KB;
   const int64_t nwork = ntiles * token_split;
   const int64_t per_xcd = (nwork + kXcds - 1) / kXcds;
   const int64_t p = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
   if (p >= nwork) return;  // uniform: the grid is rounded up to whole XCD rows
   const int split = (int)(p / ntiles);
   const int64_t tile = p - (int64_t)split * ntiles;
-  linear_item<L, NT, kTiled, KB, kEpi, KG, KD>(x, latent, out, partial, tokens, in_f, out_f, n, seed32, scale,
-                                               token_split, nblocks, pitch, split, tile, ep, lds);
+  linear_item<L, NT, kTiled, KB, kEpi, kRowTiles, KG, KD>(x, latent, out, partial, tokens, in_f, out_f, n, seed32,
+                                                          scale, token_split, nblocks, pitch, split, tile, ep, lds,
+                                                          rows_per_tile);
 }
 
 // Output (t, o) of a straddling row from its two partial dot products, with the epilogue.
@@ -556,20 +572,21 @@ __global__ __launch_bounds__(256) void bfht_linear_combine_grouped(const LinearG
   store_bf16_through(jb.out + (int64_t)t * jb.out_f + o, v);
 }
 
-template <int L, bool kTiled, int KB, bool kEpi>
+template <int L, bool kTiled, int KB, bool kEpi, bool kRowTiles = false>
 hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
-  const int nt = (int)linear_row_tiles(a.in_features, KB);
-  const int64_t ntiles = (a.nblocks_w + KB - 1) / KB;
-  const int pitch = linear_pitch(a.in_features, KB);
+  const int R = a.rows_per_tile;
+  const int nt = kRowTiles ? (R + 15) / 16 : (int)linear_row_tiles(a.in_features, KB);
+  const int64_t ntiles = kRowTiles ? (a.out_features + R - 1) / R : (a.nblocks_w + KB - 1) / KB;
+  const int pitch = kRowTiles ? 16 * nt : linear_pitch(a.in_features, KB);
   const int64_t per_xcd = (ntiles * a.token_splits + kXcds - 1) / kXcds;
   const dim3 grid((unsigned)(per_xcd * kXcds)), block(mfma15::kThreads);
   auto* lat = (const __bf16*)a.latent;
   auto* o = (__bf16*)a.out;
 #define LWL_LIN(NT)                                                                                               \
-  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT, kTiled, KB, kEpi>), \
+  hipLaunchKernelGGL((bfht_linear_mfma15<L, NT, kTiled, KB, kEpi, kRowTiles>), \
                      grid, block, 0, s, x, lat, o, partial,                                                      \
                      (int)a.tokens, (int)a.in_features, (int)a.out_features, (int)a.n, a.seed32, a.weight_scale, \
-                     a.token_splits, a.nblocks_w, pitch, a.epi)
+                     a.token_splits, a.nblocks_w, pitch, a.epi, R)
   switch (nt) {
     case 1: LWL_LIN(1); break;
     case 2: LWL_LIN(2); break;
@@ -581,7 +598,8 @@ hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial
   }
 #undef LWL_LIN
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || ntiles < 2) return e;
+  // no row straddles two tiles: row tiles, or block tiles whose length is a whole number of rows
+  if (e != hipSuccess || ntiles < 2 || kRowTiles || ((int64_t)KB * mfma15::kB) % a.in_features == 0) return e;
   hipLaunchKernelGGL(bfht_linear_combine, dim3((unsigned)((a.tokens + 255) / 256), (unsigned)(ntiles - 1)),
                      dim3(256), 0, s, (const float*)partial, o, (int)a.tokens, (int)a.in_features,
                      (int)a.out_features, ntiles, (int64_t)KB * mfma15::kB, a.weight_scale, a.epi);
@@ -590,8 +608,10 @@ hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial
 
 template <int L, bool kTiled, bool kEpi>
 hipError_t launch_linear_e(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
-  if constexpr (kTiled)
+  if constexpr (kTiled) {
+    if (a.blocks_per_wg == 2 && a.rows_per_tile > 0) return launch_linear_kb<L, true, 2, kEpi, true>(a, x, partial, s);
     if (a.blocks_per_wg == 2) return launch_linear_kb<L, true, 2, kEpi>(a, x, partial, s);
+  }
   return launch_linear_kb<L, kTiled, 1, kEpi>(a, x, partial, s);
 }
 
@@ -781,6 +801,27 @@ int linear_blocks_per_wg(const LinearArgs& a) {
   return linear_pitch_fits(a.in_features, 2) ? 2 : 1;
 }
 
+int linear_rows_per_tile(const LinearArgs& a) {
+  // Tiles of R whole rows in place of two-block tiles whose ends split rows
+  // (the straddling rows' partial sums and their combine launch, ~4.6 us at
+  // 4096 tokens, go away): R a multiple of 16 of at least 48, with R * in at
+  // least 1.5 blocks (about as many rows per loaded x element as two blocks
+  // give), and every tile [j R in, (j + 1) R in) inside the two blocks from the
+  // one holding its start, whose offset in that block is a multiple of
+  // gcd(R in, 2^15) and at most 2^15 - gcd: R in + 2^15 - gcd <= 2^16.
+  // GPT-2's rows of 768: R = 64 (1.5 blocks per tile).
+  if (a.blocks_per_wg != 2 || (2 * mfma15::kB) % a.in_features == 0) return 0;
+  for (int R = 16 * kMaxNT2; R >= 48; R -= 16) {
+    const int64_t len = (int64_t)R * a.in_features;
+    int64_t g = len, b = mfma15::kB;  // gcd(len, 2^15)
+    while (b) { const int64_t t = g % b; g = b; b = t; }
+    if (2 * len >= 3 * mfma15::kB && len + mfma15::kB - g <= 2 * mfma15::kB &&
+        linear_table_bytes(a.in_features, R) <= kLinearLdsBytes)
+      return R;
+  }
+  return 0;
+}
+
 size_t linear_workspace_bytes(const LinearArgs& a) {
   return partial_bytes(a) + (linear_tiled(a) ? x_tiling(a).bytes() : 0);
 }
@@ -789,7 +830,8 @@ int linear_token_splits(const LinearArgs& a) {
   // one workgroup per CU: split tokens so that block tiles x splits fills 256
   // CUs, never below one 16-token tile per split
   const int64_t tiles = (a.tokens + kTokTile - 1) / kTokTile;
-  const int64_t wtiles = (a.nblocks_w + a.blocks_per_wg - 1) / a.blocks_per_wg;
+  const int64_t wtiles = a.rows_per_tile > 0 ? (a.out_features + a.rows_per_tile - 1) / a.rows_per_tile
+                                             : (a.nblocks_w + a.blocks_per_wg - 1) / a.blocks_per_wg;
   int64_t split = wtiles >= 256 ? 1 : 256 / wtiles;
   if (split > tiles) split = tiles;
   return (int)(split < 1 ? 1 : split);

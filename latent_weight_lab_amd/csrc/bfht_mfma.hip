@@ -119,6 +119,13 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
   load_latent<kWhole>(x, latent, n, src);
   f32x16 acc[kTiles];
   uint32_t nw[4];
+  if constexpr (kWhole && L % 2 == 1) {
+    // whole blocks: the chain ends in layout F and each lane stores its chunks directly
+    run_chain<L, true>(acc, x, lds, src, [](int i) { return i; }, nw);
+    store_direct(acc, x, reinterpret_cast<const uint32_t*>(lds + kLdsBytes) + (L - 1) * kWordsPerLayer,
+                 rsrc(out + (block * kB - start), (uint32_t)(kB * 2)));
+    return;
+  }
   run_chain<L>(acc, x, lds, src, [](int i) { return i; }, nw);
   // The signed bf16 block goes through the free exchange buffer in position
   // order, then to memory with consecutive threads on consecutive chunks.

@@ -103,11 +103,12 @@ __device__ __forceinline__ uint32_t swap_idx34(uint32_t x) {
 // 8*(l>>5) + 2v + {0, 1}, o = l & 31, equal scale * (-1)^popcount(remap(k) & o)
 // where remap moves k bit i to bit M[i].  The same registers serve as B operand
 // (o = column) and as A operand (o = row).  make_walsh_table spells them out as
-// bf16 pairs for the five (permutation, scale) combinations the kernels use
+// bf16 pairs for the seven (permutation, scale) combinations the kernels use
 // (walsh_words below builds the same words in registers, checked at compile time):
-//   Q = (0,1,3,2,4) (k bits 2 and 3 exchanged), S = (1,0,2,3,4) (bits 0 and 1);
+//   Q = (0,1,3,2,4) (k bits 2 and 3 exchanged), S = (1,0,2,3,4) (bits 0 and 1),
+//   P = (0,2,1,3,4) (bits 1 and 2: the direct-store last layer, see run_chain);
 //   bf16 0x3e80 = 1/4, 0x3e00 = 1/8, 0x3e35 = bf16(2^-2.5), 0x3db5 = bf16(2^-3.5).
-enum { kWalshQ4, kWalshQ8, kWalshS4, kWalshSL1, kWalshSL3, kWalshSets };
+enum { kWalshQ4, kWalshQ8, kWalshS4, kWalshSL1, kWalshSL3, kWalshPL1, kWalshPL3, kWalshSets };
 
 struct WalshTable {
   uint32_t v[kWalshSets][64][8];
@@ -115,8 +116,9 @@ struct WalshTable {
 
 constexpr WalshTable make_walsh_table() {
   WalshTable tab{};
-  const int perm[kWalshSets][5] = {{0, 1, 3, 2, 4}, {0, 1, 3, 2, 4}, {1, 0, 2, 3, 4}, {1, 0, 2, 3, 4}, {1, 0, 2, 3, 4}};
-  const uint32_t mag[kWalshSets] = {0x3e80u, 0x3e00u, 0x3e80u, 0x3e35u, 0x3db5u};
+  const int perm[kWalshSets][5] = {{0, 1, 3, 2, 4}, {0, 1, 3, 2, 4}, {1, 0, 2, 3, 4}, {1, 0, 2, 3, 4},
+                                   {1, 0, 2, 3, 4}, {0, 2, 1, 3, 4}, {0, 2, 1, 3, 4}};
+  const uint32_t mag[kWalshSets] = {0x3e80u, 0x3e00u, 0x3e80u, 0x3e35u, 0x3db5u, 0x3e35u, 0x3db5u};
   for (int set = 0; set < kWalshSets; ++set)
     for (int lane = 0; lane < 64; ++lane)
       for (int c = 0; c < 2; ++c)
@@ -144,12 +146,14 @@ constexpr WalshTable make_walsh_table() {
 // bits 0-4: word (c, v) = mag * 0x10001 with the high half's sign s-flipped by
 // o'_0 and both signs flipped by h o'_3 ^ c o'_4 ^ v0 o'_1 ^ v1 o'_2.
 __host__ __device__ constexpr uint32_t walsh_perm_bit(int set, int i) {
-  // Q = (0,1,3,2,4) for the Q sets, S = (1,0,2,3,4) for the S sets
-  return (set == kWalshQ4 || set == kWalshQ8) ? (i == 2 ? 3 : i == 3 ? 2 : i) : (i == 0 ? 1 : i == 1 ? 0 : i);
+  // Q = (0,1,3,2,4) for the Q sets, S = (1,0,2,3,4) for the S sets, P = (0,2,1,3,4) for the P sets
+  return (set == kWalshQ4 || set == kWalshQ8)     ? (i == 2 ? 3 : i == 3 ? 2 : i)
+         : (set == kWalshPL1 || set == kWalshPL3) ? (i == 1 ? 2 : i == 2 ? 1 : i)
+                                                  : (i == 0 ? 1 : i == 1 ? 0 : i);
 }
 __host__ __device__ constexpr uint32_t walsh_mag(int set) {
   return set == kWalshQ4 ? 0x3e80u : set == kWalshQ8 ? 0x3e00u : set == kWalshS4 ? 0x3e80u
-       : set == kWalshSL1 ? 0x3e35u : 0x3db5u;
+       : (set == kWalshSL1 || set == kWalshPL1) ? 0x3e35u : 0x3db5u;
 }
 __host__ __device__ constexpr void walsh_words(int set, int lane, uint32_t (&w)[8]) {
   const uint32_t o = (uint32_t)lane & 31u, h = (uint32_t)lane >> 5;
@@ -326,9 +330,9 @@ __device__ __forceinline__ void exchange_write(const f32x16 (&acc)[kTiles], u32x
 }
 
 __device__ __forceinline__ void exchange_read_stage_c(f32x16 (&acc)[kTiles], const u32x4 (&h)[2],
-                                                      const u32x2* xbuf, const Ctx& x) {
+                                                      const u32x2* xbuf, int rid) {
   u32x4 b[kTiles][2];
-  const u32x2* rd = xbuf + x.rid;
+  const u32x2* rd = xbuf + rid;
 #pragma unroll
   for (int t = 0; t < kTiles; ++t)
 #pragma unroll
@@ -371,12 +375,102 @@ constexpr bool exchange_slots_consistent() {
 }
 static_assert(exchange_slots_consistent(), "exchange slot bases disagree with the chunk layout");
 
+// ---- direct-store last layer (odd L, whole blocks)
+// The last exchange's read side is free (it goes through LDS), so the
+// forward's last layer can end in a layout from which every lane stores whole
+// 16-byte output chunks and each store instruction writes 1 KiB contiguous, with
+// no LDS staging and no barrier after the chain:
+//
+//   F (end of the last layer): L0-4 = p4-8, L5 = p3, R = p2 p12 p13 p14, T = p0 p1, W = p9 p10 p11
+//
+// The writer is the regular one (S0, chunk id as exchange_write); the reader
+// of lane (l32, l5) of wave w takes chunk id (l32 >> 1) | (w & 1) << 4 | t << 5 |
+// (l32 & 1) << 7 | (w >> 1) << 8 | l5 << 10 | c << 11 (k bits p2, p3, p12, p13,
+// p14 as before, columns p4-8 instead of p5-9), and stage c uses the Walsh set P,
+// which sends k bits (p2, p3, p12, p13, p14) to row bits (r0, L5, r1, r2, r3).
+// Lane (l32, l5) of wave w then holds output chunk k = (p12, p13, p14) = r >> 1
+// of positions 8 l5 + 16 l32 + 512 w + 4096 k + 0..7, its 32-bit word q = (p1,
+// p2) being the pair of tiles 2 (q & 1), 2 (q & 1) + 1 at register (q >> 1) |
+// k << 1.  In this exchange the 8-byte slot's bit 4 is chunk-id bit 4 XOR bit 7
+// (exchange_slot_final): then the 32 lanes of a write (chunk-id bits 0-4) and
+// the 32 lanes of a read (bits 0-3 and 7) each cover the 32 8-byte bank pairs.
+__host__ __device__ constexpr int exchange_slot_final(int id, int h) {
+  return ((id & 15) | ((((id >> 4) ^ (id >> 7)) & 1) << 4)) + (h << 5) + ((id >> 5) << 6);
+}
+
+// exchange_write in exchange_slot_final: chunk-id bit 7 is register bit 2, so
+// registers 4-7 and 12-15 write through the base with slot bit 4 flipped.
+__device__ __forceinline__ void exchange_write_final(const f32x16 (&acc)[kTiles], u32x2* xbuf, const Ctx& x) {
+  int w1 = x.wid ^ 16;
+  asm("" : "+v"(w1));
+  u32x2* half0 = xbuf + x.wid;
+  u32x2* half1 = xbuf + w1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    u32x2 v;
+    v[0] = pk(acc[0][r], acc[1][r]);
+    v[1] = pk(acc[2][r], acc[3][r]);
+    ((r >> 2) & 1 ? half1 : half0)[((r & 7) << 6) + ((r >> 3) << 10)] = v;
+  }
+}
+
+// Reader base slot of layout F (t << 6 and c << 12 added per operand).
+__device__ __forceinline__ int rid_final(const Ctx& x) {
+  int rid = (x.lane32 >> 1) | (((x.wave & 1) ^ (x.lane32 & 1)) << 4) | ((x.lane32 & 1) << 8) | ((x.wave >> 1) << 9) |
+            (x.l5 << 11);
+  asm("" : "+v"(rid));
+  return rid;
+}
+
+constexpr bool exchange_final_consistent() {
+  for (int lane = 0; lane < 64; ++lane)
+    for (int wave = 0; wave < kWaves; ++wave) {
+      const int l32 = lane & 31, l5 = lane >> 5;
+      const int wid = l32 + ((wave & 1) << 5) + (l5 << 9) + ((wave >> 1) << 11);
+      for (int r = 0; r < 16; ++r) {
+        const int id = l32 + ((r & 7) << 5) + (l5 << 8) + ((r >> 3) << 9) + ((wave >> 1) << 10);
+        if ((((r >> 2) & 1) ? wid ^ 16 : wid) + ((r & 7) << 6) + ((r >> 3) << 10) != exchange_slot_final(id, wave & 1))
+          return false;
+      }
+      const int rid = (l32 >> 1) | (((wave & 1) ^ (l32 & 1)) << 4) | ((l32 & 1) << 8) | ((wave >> 1) << 9) | (l5 << 11);
+      for (int t = 0; t < kTiles; ++t)
+        for (int c = 0; c < 2; ++c) {
+          const int id = (l32 >> 1) | ((wave & 1) << 4) | (t << 5) | ((l32 & 1) << 7) | ((wave >> 1) << 8) |
+                         (l5 << 10) | (c << 11);
+          const int s = rid + (t << 6) + (c << 12);
+          if (s != exchange_slot_final(id, 0) || s + 32 != exchange_slot_final(id, 1)) return false;
+        }
+    }
+  return true;
+}
+static_assert(exchange_final_consistent(), "final exchange slot bases disagree with the chunk layout");
+
+// Even bit-in-word bits of x to the low half, odd ones to the high half, in
+// order: bit j of the result is bit 2j of x, bit 16 + j is bit 2j + 1.
+__host__ __device__ constexpr uint32_t unshuffle_bits(uint32_t x) {
+  uint32_t t = (x ^ (x >> 1)) & 0x22222222u;
+  x ^= t ^ (t << 1);
+  t = (x ^ (x >> 2)) & 0x0c0c0c0cu;
+  x ^= t ^ (t << 2);
+  t = (x ^ (x >> 4)) & 0x00f000f0u;
+  x ^= t ^ (t << 4);
+  t = (x ^ (x >> 8)) & 0x0000ff00u;
+  return x ^ t ^ (t << 8);
+}
+static_assert(unshuffle_bits(0x55555555u) == 0x0000ffffu && unshuffle_bits(0xaaaaaaaau) == 0xffff0000u &&
+                  unshuffle_bits(0x00000006u) == 0x00010002u && unshuffle_bits(0x80000000u) == 0x80000000u,
+              "unshuffle_bits");
+
 // Fills the sign-word table (bytes kLdsBytes.. of the chain's LDS): slot j - 1
 // holds the 1024 inverted words of sign layer sign_layer(j), j = 1..L, two per
 // thread, in the form their reader applies: sign layer j < L is read by kernel
 // layer j, whose stage a runs in S1 (j odd: bit permutation swap_idx34) or S0
 // (j even: swap_idx04); the last one (j = L) is read by the output code, unpermuted.
-template <int L, class SignLayer>
+// kDirect (the direct-store last layer): slot L - 1 holds the last layer's
+// words as store_direct reads them, unshuffled (unshuffle_bits) and at index
+// (w >> 7) + 8 (w & 127), so that the eight words of a lane's chunks k = w >> 7
+// = 0..7 are consecutive.
+template <int L, bool kDirect = false, class SignLayer>
 __device__ __forceinline__ void fill_words(const Ctx& x, uint32_t* wtab, SignLayer sign_layer) {
   static_assert(L <= kMaxChainLayers, "word table holds kMaxChainLayers layers");
 #pragma unroll
@@ -386,8 +480,14 @@ __device__ __forceinline__ void fill_words(const Ctx& x, uint32_t* wtab, SignLay
     for (int h = 0; h < kWordsPerLayer / kThreads; ++h) {
       const uint32_t w = (uint32_t)threadIdx.x + (uint32_t)(h * kThreads);
       uint32_t v = ~lowbias32(key ^ (0xc2b2ae35u * (w + 1u)));
-      if (j < L) v = (j & 1) ? swap_idx34(v) : swap_idx04(v);
-      wtab[(j - 1) * kWordsPerLayer + (int)w] = v;
+      int at = (int)w;
+      if (j < L) {
+        v = (j & 1) ? swap_idx34(v) : swap_idx04(v);
+      } else if (kDirect) {
+        v = unshuffle_bits(v);
+        at = (int)((w >> 7) + 8 * (w & 127));
+      }
+      wtab[(j - 1) * kWordsPerLayer + at] = v;
     }
   }
 }
@@ -420,14 +520,17 @@ __device__ __forceinline__ void read_words(const Ctx& x, const uint32_t* wtab, i
 // `lds` spans kChainLdsBytes; the sign words of layers 1..L are hashed into
 // its table first (their loads' latency covers the hashing) and read after
 // each layer's exchange barrier, which also orders the table's writes.
-template <int L, class SignLayer>
+// kDirect (odd L): the last layer ends in layout F (see exchange_slot_final)
+// instead of S1, and `fin` is not read (store_direct reads the last words).
+template <int L, bool kDirect = false, class SignLayer>
 __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, unsigned char* lds,
                                           const u32x4 (&src)[kTiles][2], SignLayer sign_layer,
                                           uint32_t (&fin)[4]) {
+  static_assert(!kDirect || L % 2 == 1, "layout F follows an even layer's stages a, b");
   uint32_t* wtab = reinterpret_cast<uint32_t*>(lds + kLdsBytes);
   uint32_t nw[L][4];
   layer_words<false>(x, sign_layer(0), nw[0]);
-  fill_words<L>(x, wtab, sign_layer);
+  fill_words<L, kDirect>(x, wtab, sign_layer);
   const int lane = threadIdx.x & 63;
   // Stage a: Q/4 (even layers), S/4 (odd); stage b: Q/8; stage c: S/4 (even),
   // Q/4 (odd); the last stage c carries the residual 2^(-L/2): S/4*2^-0.5
@@ -436,11 +539,13 @@ __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, u
   walsh_operand(kWalshQ4, lane, hq4);
   walsh_operand(kWalshQ8, lane, hq8);
   walsh_operand(kWalshS4, lane, hs4);
-  walsh_operand(L == 1 ? kWalshSL1 : L == 2 ? kWalshQ8 : kWalshSL3, lane, hlast);
+  walsh_operand(kDirect ? (L == 1 ? kWalshPL1 : kWalshPL3) : L == 1 ? kWalshSL1 : L == 2 ? kWalshQ8 : kWalshSL3, lane,
+                hlast);
   const f32x16 zero = {};
 #pragma unroll
   for (int i = 0; i < L; ++i) {
     const bool odd = i & 1;
+    const bool direct = kDirect && i == L - 1;
     if (i == 0) {
       uint64_t pairs[2];
       sign_pairs<false>(nw[0], pairs);
@@ -458,17 +563,20 @@ __device__ __forceinline__ void run_chain(f32x16 (&acc)[kTiles], const Ctx& x, u
     }
     stage_rows<false, false>(acc, hq8, nw[i]);
     u32x2* xbuf = reinterpret_cast<u32x2*>(lds + (i & 1) * kXBufBytes);
-    exchange_write(acc, xbuf, x);
+    if (direct)
+      exchange_write_final(acc, xbuf, x);
+    else
+      exchange_write(acc, xbuf, x);
     __syncthreads();
     if (i + 1 < L) {
       if ((i + 1) & 1)
         read_words<true, true>(x, wtab, i, nw[i + 1]);
       else
         read_words<false, true>(x, wtab, i, nw[i + 1]);
-    } else {
+    } else if (!kDirect) {
       read_words<(L % 2) == 1, false>(x, wtab, L - 1, fin);
     }
-    exchange_read_stage_c(acc, i == L - 1 ? hlast : (odd ? hq4 : hs4), xbuf, x);
+    exchange_read_stage_c(acc, i == L - 1 ? hlast : (odd ? hq4 : hs4), xbuf, direct ? rid_final(x) : x.rid);
   }
 }
 
@@ -541,7 +649,7 @@ __device__ __forceinline__ void run_chain2(f32x16 (&acc)[2][kTiles], const Ctx (
       }
     }
 #pragma unroll
-    for (int b = 0; b < 2; ++b) exchange_read_stage_c(acc[b], i == L - 1 ? hlast : (odd ? hq4 : hs4), xbuf[b], x[b]);
+    for (int b = 0; b < 2; ++b) exchange_read_stage_c(acc[b], i == L - 1 ? hlast : (odd ? hq4 : hs4), xbuf[b], x[b].rid);
   }
 }
 
@@ -667,6 +775,44 @@ __device__ __forceinline__ void stage_output(const f32x16 (&acc)[kTiles], const 
   out_chunks<L>(acc, nw, x, v);
 #pragma unroll
   for (int k = 0; k < 8; ++k) stage[stage_slot(out_chunk_pos<L>(x, k) >> 3)] = v[k];
+}
+
+// The forward's whole block from layout F (run_chain<L, true>): the last sign
+// layer and 16-byte write-through stores of whole chunks, 1 KiB contiguous per
+// instruction, straight from registers.  `words` is the table slot the chain
+// filled for it (fill_words<L, true>): a lane's eight words, those of its chunks
+// k = 0..7, are consecutive; the chunk's bit-in-word bits are p0-p2 (in the
+// chunk) + 8 p3 (l5) + 16 p4 (l32 bit 0), so after the shift by 4 (l5 + 2 p4) of
+// the unshuffled word, bit q (bit 16 + q) holds the sign of the chunk's value 2q
+// (2q + 1), the pair of word q, and (w << (15 - q)) & kPairSign is its mask.
+__device__ __forceinline__ void store_direct(const f32x16 (&acc)[kTiles], const Ctx& x, const uint32_t* words,
+                                             __amdgpu_buffer_rsrc_t out_r) {
+  const u32x4* wt = reinterpret_cast<const u32x4*>(words) + 2 * ((x.lane32 >> 1) + 16 * x.wave);
+  const u32x4 wa = wt[0], wb = wt[1];
+  const int sh = 4 * (x.l5 + 2 * (x.lane32 & 1));
+  const uint32_t w[8] = {wa[0] >> sh, wa[1] >> sh, wa[2] >> sh, wa[3] >> sh,
+                         wb[0] >> sh, wb[1] >> sh, wb[2] >> sh, wb[3] >> sh};
+  u32x4 v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = (q >> 1) | (k << 1);
+      v[k][q] = pk(acc[2 * (q & 1)][r], acc[2 * (q & 1) + 1][r]);
+    }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint64_t pair = (uint64_t)w[k] | ((uint64_t)w[k + 4] << 32);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x2 m = shl_pair(pair, 15 - q);
+      v[k][q] ^= m[0] & kPairSign;
+      v[k + 4][q] ^= m[1] & kPairSign;
+    }
+  }
+  const int base = 16 * x.l5 + 32 * x.lane32 + 1024 * x.wave;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) __builtin_amdgcn_raw_buffer_store_b128(v[k], out_r, base + 8192 * k, 0, kStreamStore);
 }
 
 // Backward tail: applies D_0 (inverted words `nw` of the chain's last sign

@@ -49,6 +49,10 @@ def oracle_linear(x: torch.Tensor, latent: torch.Tensor, out_f: int, layers: int
         (6144, 768, 3072, 32768, 3, 38, 1.0),   # two blocks per workgroup, 55 token tiles: one full round + 3 singles
         (600, 3072, 100, 32768, 2, 34, 0.5),    # two blocks per workgroup, 23-row pitch, 5 tiles
         (300, 5120, 41, 32768, 3, 35, 1.0),     # two blocks per workgroup, one row tile, last tile single
+        # rows of 768: tiles of 64 whole rows (1.5 blocks, inside two generated blocks), no straddling rows
+        (300, 768, 1000, 32768, 2, 39, 1.0),    # 16 row tiles, the last of 40 rows; ragged token tiles
+        (513, 768, 2304, 32768, 3, 40, 0.5),    # GPT-2 qkv at a prefill batch: 36 tiles, one-token last tile
+        (256, 768, 768, 20000, 1, 41, 1.0),     # GPT-2 proj, padded latent (last generated block partial)
     ],
 )
 def test_fused_linear_matches_oracle(tokens, in_f, out_f, n, layers, seed, scale):
