@@ -218,10 +218,11 @@ def test_linear_workspace_size():
     # one pair of float32 partial rows (first / last row of the tile) per workgroup tile of generated
     # blocks and token, then, from 256 tokens, x re-laid out in 16-token x 32-k tiles of 1 KiB
     # (zero-padded).  From 256 tokens a tile is two blocks when one block holds at most 64 rows and
-    # two fit in the LDS (here: 768 in_features, 87 rows per two blocks; 3072, 23 rows; 1000, 67
-    # rows at an exact pitch); otherwise, and below, one block.
+    # two fit in the LDS (here: 3072 in_features, 23 rows; 1000, 67 rows at an exact pitch);
+    # otherwise, and below, one block.  Rows of 768 take tiles of 64 whole rows instead (1.5
+    # blocks): no row straddles two tiles, so no partial rows, only the x copy.
     lib = N.lib()
-    assert lib.lwl_bfht_linear_forward_workspace_size(4096, 768, 3072, 32768) == 36 * 2 * 4096 * 4 + 256 * 24 * 1024
+    assert lib.lwl_bfht_linear_forward_workspace_size(4096, 768, 3072, 32768) == 256 * 24 * 1024
     assert lib.lwl_bfht_linear_forward_workspace_size(4096, 3072, 768, 32768) == 36 * 2 * 4096 * 4 + 256 * 96 * 1024
     partial = (18 * 2 * 255 * 4 + 255) // 256 * 256
     assert lib.lwl_bfht_linear_forward_workspace_size(255, 768, 768, 32768) == partial
