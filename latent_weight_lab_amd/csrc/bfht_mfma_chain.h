@@ -391,17 +391,19 @@ static_assert(exchange_slots_consistent(), "exchange slot bases disagree with th
 // Lane (l32, l5) of wave w then holds output chunk k = (p12, p13, p14) = r >> 1
 // of positions 8 l5 + 16 l32 + 512 w + 4096 k + 0..7, its 32-bit word q = (p1,
 // p2) being the pair of tiles 2 (q & 1), 2 (q & 1) + 1 at register (q >> 1) |
-// k << 1.  In this exchange the 8-byte slot's bit 4 is chunk-id bit 4 XOR bit 7
-// (exchange_slot_final): then the 32 lanes of a write (chunk-id bits 0-4) and
-// the 32 lanes of a read (bits 0-3 and 7) each cover the 32 8-byte bank pairs.
+// k << 1.  The LDS serves 128 bytes (32 banks of 4 bytes) per cycle, so an
+// 8-byte access goes 16 lanes at a time, and each 16 lanes must fall on the 16
+// 8-byte bank pairs (slot bits 0-3).  A write's 16 lanes differ in chunk-id
+// bits 0-3, a read's in bits 0-2 and 7, so in this exchange the slot's bit 3 is
+// chunk-id bit 3 XOR bit 7 (exchange_slot_final).
 __host__ __device__ constexpr int exchange_slot_final(int id, int h) {
-  return ((id & 15) | ((((id >> 4) ^ (id >> 7)) & 1) << 4)) + (h << 5) + ((id >> 5) << 6);
+  return ((id & 23) | ((((id >> 3) ^ (id >> 7)) & 1) << 3)) + (h << 5) + ((id >> 5) << 6);
 }
 
 // exchange_write in exchange_slot_final: chunk-id bit 7 is register bit 2, so
-// registers 4-7 and 12-15 write through the base with slot bit 4 flipped.
+// registers 4-7 and 12-15 write through the base with slot bit 3 flipped.
 __device__ __forceinline__ void exchange_write_final(const f32x16 (&acc)[kTiles], u32x2* xbuf, const Ctx& x) {
-  int w1 = x.wid ^ 16;
+  int w1 = x.wid ^ 8;
   asm("" : "+v"(w1));
   u32x2* half0 = xbuf + x.wid;
   u32x2* half1 = xbuf + w1;
@@ -416,8 +418,8 @@ __device__ __forceinline__ void exchange_write_final(const f32x16 (&acc)[kTiles]
 
 // Reader base slot of layout F (t << 6 and c << 12 added per operand).
 __device__ __forceinline__ int rid_final(const Ctx& x) {
-  int rid = (x.lane32 >> 1) | (((x.wave & 1) ^ (x.lane32 & 1)) << 4) | ((x.lane32 & 1) << 8) | ((x.wave >> 1) << 9) |
-            (x.l5 << 11);
+  int rid = ((x.lane32 >> 1) & 7) | ((((x.lane32 >> 4) ^ x.lane32) & 1) << 3) | ((x.wave & 1) << 4) |
+            ((x.lane32 & 1) << 8) | ((x.wave >> 1) << 9) | (x.l5 << 11);
   asm("" : "+v"(rid));
   return rid;
 }
@@ -429,10 +431,11 @@ constexpr bool exchange_final_consistent() {
       const int wid = l32 + ((wave & 1) << 5) + (l5 << 9) + ((wave >> 1) << 11);
       for (int r = 0; r < 16; ++r) {
         const int id = l32 + ((r & 7) << 5) + (l5 << 8) + ((r >> 3) << 9) + ((wave >> 1) << 10);
-        if ((((r >> 2) & 1) ? wid ^ 16 : wid) + ((r & 7) << 6) + ((r >> 3) << 10) != exchange_slot_final(id, wave & 1))
+        if ((((r >> 2) & 1) ? wid ^ 8 : wid) + ((r & 7) << 6) + ((r >> 3) << 10) != exchange_slot_final(id, wave & 1))
           return false;
       }
-      const int rid = (l32 >> 1) | (((wave & 1) ^ (l32 & 1)) << 4) | ((l32 & 1) << 8) | ((wave >> 1) << 9) | (l5 << 11);
+      const int rid = ((l32 >> 1) & 7) | ((((l32 >> 4) ^ l32) & 1) << 3) | ((wave & 1) << 4) | ((l32 & 1) << 8) |
+                      ((wave >> 1) << 9) | (l5 << 11);
       for (int t = 0; t < kTiles; ++t)
         for (int c = 0; c < 2; ++c) {
           const int id = (l32 >> 1) | ((wave & 1) << 4) | (t << 5) | ((l32 & 1) << 7) | ((wave >> 1) << 8) |
@@ -478,15 +481,16 @@ __device__ __forceinline__ void fill_words(const Ctx& x, uint32_t* wtab, SignLay
     const uint32_t key = x.bkey ^ layer_key(sign_layer(j));
 #pragma unroll
     for (int h = 0; h < kWordsPerLayer / kThreads; ++h) {
-      const uint32_t w = (uint32_t)threadIdx.x + (uint32_t)(h * kThreads);
+      // consecutive threads write consecutive entries (a strided write would
+      // serialize on the LDS banks); the direct slot's entry `at` holds word w
+      const uint32_t at = (uint32_t)threadIdx.x + (uint32_t)(h * kThreads);
+      const bool direct = kDirect && j == L;
+      const uint32_t w = direct ? ((at & 7u) << 7) | (at >> 3) : at;
       uint32_t v = ~lowbias32(key ^ (0xc2b2ae35u * (w + 1u)));
-      int at = (int)w;
-      if (j < L) {
+      if (j < L)
         v = (j & 1) ? swap_idx34(v) : swap_idx04(v);
-      } else if (kDirect) {
+      else if (direct)
         v = unshuffle_bits(v);
-        at = (int)((w >> 7) + 8 * (w & 127));
-      }
       wtab[(j - 1) * kWordsPerLayer + at] = v;
     }
   }
