@@ -12,9 +12,10 @@
 // one generator call (G blocks) at a time, and the generator's final stores
 // land, scaled by weight_scale and rounded to the I/O type, in an LDS table of
 // 16-byte k-chunks: chunk (kc, r) = W[row0 + r][kc*CH .. kc*CH + CH - 1] at slot
-// kc * pitch + r, pitch = rows + 1 (odd, so the generator's stores of
-// consecutive k in one row spread over the LDS banks; the contraction reads 16
-// consecutive rows of one chunk, contiguous).  Each wave then contracts items
+// kc * pitch + mm_row(kc, r), pitch = rows + 1 (odd, so the generator's stores
+// of consecutive k in one row spread over the LDS banks; the contraction reads
+// 16 rows of one chunk, a permutation of 16 consecutive slots, see mm_row).
+// Each wave then contracts items
 // of 4 token tiles x RT row tiles (RT = 1, 2 or 4: the tile's 16-row tiles, at
 // most 4):
 //
@@ -57,6 +58,21 @@ struct MmGeo {
   static_assert(BlockLds<LB>::FLOATS * 4 + TABLE_BYTES <= 160 * 1024, "generator and table fit the LDS");
 };
 
+// Table row of W row r in k chunk kc.  A ds_read_b128 serves 16 lanes per LDS
+// cycle over 64 banks: lanes 0-3, 12-15, 20-23, 24-27 together and 4-7, 8-11,
+// 16-19, 28-31 together (the same for 32-63), i.e. rows l16 in {0-3, 12-15} of
+// chunk kq = 0 with rows {4-11} of chunk 1 and the other way round (2 and 3
+// alike).  Odd chunks sit pitch slots after even ones, so they hold each
+// 16-row group permuted, r -> ((r ^ 1) - pitch) mod 16: every such read then
+// covers the 16 16-byte bank groups once (with rows in place, pitch = 1 mod 16
+// put two lanes on each of 8 groups), and a row keeps its parity, so the
+// generator's stores of 8 consecutive chunks of one row still fall on 8
+// distinct groups modulo 8 (the odd pitch).  The rows per tile are a multiple
+// of 16, so every group is whole.
+__device__ __forceinline__ int mm_row(int kc, int r, int pitch) {
+  return (kc & 1) ? (r & ~15) | ((((r & 15) ^ 1) - pitch) & 15) : r;
+}
+
 // The generator's store functor: tile-relative position p = r * in + k lands in
 // chunk (k / CH, r), element k % CH.
 template <class T>
@@ -73,7 +89,8 @@ struct TableStore {
   __device__ void put(int p, float v) const {
     constexpr int CH = 16 / (int)sizeof(T);
     const int r = p >> log_in, k = p & ((1 << log_in) - 1);
-    tbl[((k / CH) * pitch + r) * CH + (k % CH)] = from_f32<T>(v * scale);
+    const int kc = k / CH;
+    tbl[(kc * pitch + mm_row(kc, r, pitch)) * CH + (k % CH)] = from_f32<T>(v * scale);
   }
   __device__ Range range(int64_t first, int64_t count) const { return Range{(int)(first - base), (int)count}; }
   __device__ void operator()(Range rg, int i, float v) const {
@@ -167,8 +184,9 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small_mm(const T* __r
       else
         xo[g] = (ttb + g < tt1 && t < tokens) ? (uint32_t)(t * in_f + (MG::KSTEP / 4) * kq) * (uint32_t)sizeof(T) : kOff;
     }
-    // table slot of this lane's row in row tile j, chunk 0 of step s: (4 s + kq) * pitch + 16 (rtb + j) + l16
-    const int slot0 = kq * pitch + 16 * rtb + l16;
+    // table slot of this lane's row in row tile j, chunk 0 of step s: (4 s + kq) * pitch + 16 (rtb + j) +
+    // mm_row(kq, l16) (the permutation keeps each 16-row group in place)
+    const int slot0 = kq * pitch + 16 * rtb + mm_row(kq, l16, pitch);
     f32x4m acc[kMmTok][kMmRows];
 #pragma unroll
     for (int g = 0; g < kMmTok; ++g)
