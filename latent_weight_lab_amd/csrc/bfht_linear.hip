@@ -91,14 +91,28 @@ __host__ __device__ constexpr int linear_steps(int64_t in_features) {
 }
 
 // Table chunk (kc, r) — row r of the tile, k chunk kc — lives at
-// kc * pitch + r + (kc >> 2): every k step's 4 chunks are shifted one slot
-// further than the previous step's.  That makes the scatter of a generated
-// block conflict-free: the 16 lanes of one LDS write phase hold chunks 4 apart
-// in one row (kc, kc + 4, ...), whose slots then differ by 4 * pitch + 1, an odd
-// number, so they fall in 16 distinct 16-byte bank groups for any pitch; the
-// contraction reads one step's chunks at a common shift, so its reads stay
-// contiguous.  The table holds 4 * steps * pitch + steps chunks.
-__device__ __forceinline__ int table_slot(int kc, int r, int pitch) { return kc * pitch + r + (kc >> 2); }
+// kc * pitch + table_row(kc, r) + (kc >> 2): every k step's 4 chunks are
+// shifted one slot further than the previous step's.  That makes the scatter
+// of a generated block conflict-free: a ds_write_b128 serves 8 consecutive
+// lanes per LDS cycle over 32 banks, and the lanes of one scatter write hold
+// chunks 4 apart in one row (kc, kc + 4, ... — one parity, so one row
+// position), whose slots then differ by 4 * pitch + 1, an odd number, so they
+// fall in 8 distinct 16-byte bank groups for any pitch.  The contraction reads
+// one step's chunks at a common shift: lane (l16, kq) reads row 16 nt + l16 of
+// chunk 4 step + kq.  A ds_read_b128 serves 16 lanes per cycle over 64 banks,
+// lanes 0-3, 12-15, 20-23, 24-27 together and 4-7, 8-11, 16-19, 28-31 together
+// (the same for 32-63), i.e. rows l16 in {0-3, 12-15} of chunk kq = 0 with
+// rows {4-11} of chunk 1 and the other way round (2 and 3 alike); odd chunks
+// sit pitch slots after even ones, so they hold each whole 16-row group
+// permuted, r -> ((r ^ 1) - pitch) mod 16, and every read covers the 16 bank
+// groups once (with rows in place, an exact pitch of 23 rows put two lanes on
+// each of 8 groups: 1204 conflict cycles per wave at in_features 3072).
+__host__ __device__ constexpr int table_row(int kc, int r, int pitch) {
+  return ((kc & 1) && r < (pitch & ~15)) ? (r & ~15) | ((((r & 15) ^ 1) - pitch) & 15) : r;
+}
+__device__ __forceinline__ int table_slot(int kc, int r, int pitch) {
+  return kc * pitch + table_row(kc, r, pitch) + (kc >> 2);
+}
 
 constexpr int64_t linear_table_bytes(int64_t in_features, int64_t pitch) {
   const int64_t steps = linear_steps(in_features);
@@ -310,12 +324,25 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
                                   : (uint32_t)((int64_t)tokens * in_f * 2));
   float* part_first = partial + (tile * 2 + 0) * (int64_t)tokens;
   float* part_last = partial + (tile * 2 + 1) * (int64_t)tokens;
-  const u32x4* brow = table + kq * pitch + l16;  // + step * (4 * pitch + 1) + 16 * nt
-  // Table rows past the tile's last row (zero padding up to 16 * NT, or with an
-  // exact pitch the next chunk's rows) are read as they are: W row o only
-  // feeds output column o of the MFMA, and the epilogue stores no column past
-  // o_last, so no load waits on a mask before the next step's MFMAs.
-  auto brd = [&](const u32x4* b, int nt) -> u32x4 { return b[16 * nt]; };
+  // This lane's row of row tile nt at step s: brow + s * (4 * pitch + 1) + 16 nt
+  // + dnt[nt].  Rows inside the table go through table_slot; rows past it (an
+  // exact pitch, or a grouped job with fewer row tiles than the launch) read
+  // their tile's first row, or row 0 when the whole tile lies past the table:
+  // the same address as another lane of the LDS cycle, so no bank conflict.
+  // Rows past the tile's last row are read as they are: W row o only feeds
+  // output column o of the MFMA, and the epilogue stores no column past o_last,
+  // so no load waits on a mask before the next step's MFMAs.
+  const int slot_l16 = table_slot(kq, l16, pitch);
+  const u32x4* brow = table + slot_l16;
+  int dnt[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int r = 16 * nt + l16;
+    const int rr = r < pitch ? r : (16 * nt < pitch ? 16 * nt : 0);
+    dnt[nt] = table_slot(kq, rr, pitch) - slot_l16 - 16 * nt;
+  }
+  // row tiles: the table is 16 NT whole rows, so every dnt is 0
+  auto brd = [&](const u32x4* b, int nt) -> u32x4 { return kRowTiles ? b[16 * nt] : b[16 * nt + dnt[nt]]; };
   constexpr uint32_t kOff = 0x80000000u;  // voffset that reads 0
   // epilogue: which terms, the row-sum coefficient (one scalar load), the bias
   const bool has_xs = kEpi && ep.xsum != nullptr, has_base = kEpi && ep.base != nullptr,
