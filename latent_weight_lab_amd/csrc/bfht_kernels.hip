@@ -453,18 +453,36 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
     g.pt = (int)pos((uint32_t)tid, g.tile);
     return g;
   };
+  // A tile wholly inside its buffer (the work buffer always; the latent when
+  // it covers the block, a gradient or output slice when it covers the whole
+  // block) is accessed at the thread's offset plus each register's constant
+  // one in the scalar offset, with no per-element range arithmetic (about a
+  // fifth of a low tile's VALU work otherwise); other tiles check every index.
   auto load_tile = [&](const Geo& g, float (&x)[32]) {
+    if constexpr (SRC == kSrcLatent) {
+      const auto lr = tile_rsrc(src_io, (uint64_t)n * sizeof(T));
+      if (n >= B) {
 #pragma unroll
-    for (int r = 0; r < 32; ++r) {
-      if constexpr (SRC == kSrcLatent) {
-        x[r] = buf_load<T>(tile_rsrc(src_io, (uint64_t)n * sizeof(T)), g.pt + pr(r));
-      } else if constexpr (SRC == kSrcGrad) {
-        // buffer over grad[lo..hi) of this block, indexed by block position - lo
-        const T* g0 = src_io + (g.base + g.lo - start);
-        x[r] = buf_load<T>(tile_rsrc(g0, (uint64_t)(g.hi - g.lo) * sizeof(T)), g.pt + pr(r) - (int)g.lo);
+        for (int r = 0; r < 32; ++r) x[r] = buf_load_at<T>(lr, g.pt, pr(r));
       } else {
-        x[r] = buf_load<float>(tile_rsrc(work + g.slot * B, (uint64_t)B * 4), g.pt + pr(r));
+#pragma unroll
+        for (int r = 0; r < 32; ++r) x[r] = buf_load<T>(lr, g.pt + pr(r));
       }
+    } else if constexpr (SRC == kSrcGrad) {
+      // buffer over grad[lo..hi) of this block, indexed by block position - lo
+      const T* g0 = src_io + (g.base + g.lo - start);
+      const auto gr = tile_rsrc(g0, (uint64_t)(g.hi - g.lo) * sizeof(T));
+      if (g.lo == 0 && g.hi == B) {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) x[r] = buf_load_at<T>(gr, g.pt, pr(r));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) x[r] = buf_load<T>(gr, g.pt + pr(r) - (int)g.lo);
+      }
+    } else {
+      const auto wr = tile_rsrc(work + g.slot * B, (uint64_t)B * 4);
+#pragma unroll
+      for (int r = 0; r < 32; ++r) x[r] = buf_load_at<float>(wr, g.pt, pr(r));
     }
   };
 
@@ -582,17 +600,23 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
       }
     }
 
+    if constexpr (DST == kDstSum) {
 #pragma unroll
-    for (int r = 0; r < 32; ++r) {
-      const float vs = v[r] * scale;
-      if constexpr (DST == kDstSum) {
-        acc[r] += vs;
-      } else if constexpr (DST == kDstWork) {
-        buf_store<float>(vs, tile_rsrc(work + g.slot * B, (uint64_t)B * 4), g.pt + pr(r));
+      for (int r = 0; r < 32; ++r) acc[r] += v[r] * scale;
+    } else if constexpr (DST == kDstWork) {
+      const auto wr = tile_rsrc(work + g.slot * B, (uint64_t)B * 4);
+#pragma unroll
+      for (int r = 0; r < 32; ++r) buf_store_at<float>(v[r] * scale, wr, g.pt, pr(r));
+    } else {
+      static_assert(DST == kDstOut, "tile pass destinations: work buffer, output slice, block sum");
+      T* o0 = dst_io + (g.base + g.lo - start);
+      const auto orr = tile_rsrc(o0, (uint64_t)(g.hi - g.lo) * sizeof(T));
+      if (g.lo == 0 && g.hi == B) {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) buf_store_at<T>(v[r] * scale, orr, g.pt, pr(r));
       } else {
-        static_assert(DST == kDstOut, "tile pass destinations: work buffer, output slice, block sum");
-        T* o0 = dst_io + (g.base + g.lo - start);
-        buf_store<T>(vs, tile_rsrc(o0, (uint64_t)(g.hi - g.lo) * sizeof(T)), g.pt + pr(r) - (int)g.lo);
+#pragma unroll
+        for (int r = 0; r < 32; ++r) buf_store<T>(v[r] * scale, orr, g.pt + pr(r) - (int)g.lo);
       }
     }
   }
