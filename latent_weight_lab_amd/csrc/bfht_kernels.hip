@@ -368,6 +368,39 @@ __device__ __forceinline__ void tile_signs(const uint32_t* words, float (&v)[32]
   }
 }
 
+// The same for a group below bit 10 (L >= 5): the thread's and the register's
+// bit fields of e are disjoint and the register's lie at bit 5 and above, so
+// every register takes the same bit of the words at the thread's base plus a
+// constant per register (immediate LDS offsets, no per-register index work).
+template <int L, int NB>
+__device__ __forceinline__ void tile_signs_split(const uint32_t* words, float (&v)[32], int tid) {
+  static_assert(L >= 5, "the bit within a sign word comes from the thread index alone");
+  const int e0 = group_pos<kTileLog, 5>(tid, 0, L, NB);
+  const uint32_t* w = words + (e0 >> 5);
+  const int bit = e0 & 31;
+#pragma unroll
+  for (int r0 = 0; r0 < 32; r0 += 8) {
+#pragma unroll
+    for (int r = r0; r < r0 + 8; ++r) v[r] = signed_by(v[r], w[group_pos<kTileLog, 5>(0, r, L, NB) >> 5], bit);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+// group_pos(t, r, L, NB) = group_pos(t, 0, L, NB) | group_pos(0, r, L, NB) for L >= 5, as tile_signs_split uses it
+constexpr bool tile_signs_split_ok() {
+  for (int L = 5; L <= 10; ++L)
+    for (int NB = 1; NB <= 5 && L + NB <= 15; ++NB)
+      for (int i = 0; i < 14; ++i)
+        for (int r = 0; r < 32; ++r) {
+          // every single thread-index bit, none, all, and two mixed patterns
+          const int t = i < 10 ? 1 << i : i == 10 ? 0 : i == 11 ? kTileThreads - 1 : i == 12 ? 0x155 : 0x2aa;
+          const int e = group_pos<kTileLog, 5>(t, r, L, NB), a = group_pos<kTileLog, 5>(t, 0, L, NB),
+                    b = group_pos<kTileLog, 5>(0, r, L, NB);
+          if (e != (a | b) || (a & b) != 0 || (b & 31) != 0) return false;
+        }
+  return true;
+}
+static_assert(tile_signs_split_ok(), "tile_signs_split's split of the element index");
+
 // Butterflies over register bits [LO, 5).
 template <int LO>
 __device__ __forceinline__ void reg_butterflies(float (&v)[32]) {
@@ -570,16 +603,26 @@ __global__ __launch_bounds__(kTileThreads) void bfht_tile_pass(
 #pragma unroll
         for (int r = 0; r < 32; ++r) v[r] = signed_by(v[r], my_word, r);
       } else {
-        // a high tile's small group below bit 10: the signs go on in the load
-        // layout (as in a register-only tile), then back to the group
-        group_rw(v, G::kLastLo, G::kLastNb, false);
-        __syncthreads();
-        group_rw(v, 10, 5, true);
-        tile_signs<10, 5>(words, v, tid);  // the table is complete: barriers since its writes
-        if (post) {
-          group_rw(v, 10, 5, false);
+        // a high tile's small group below bit 10.  A middle pass (work buffer to
+        // work buffer, transformed again after the signs) puts the signs on in
+        // the group's layout (each element's word looked up by its tile index;
+        // the table is complete: barriers since its writes).  The other passes
+        // keep their register budget: the signs go on in the load layout (as in
+        // a register-only tile), then back to the group if transformed again.
+        bool in_group = false;
+        if constexpr (DST == kDstWork) in_group = post != 0;
+        if (in_group) {
+          tile_signs_split<G::kLastLo, G::kLastNb>(words, v, tid);
+        } else {
+          group_rw(v, G::kLastLo, G::kLastNb, false);
           __syncthreads();
-          group_rw(v, G::kLastLo, G::kLastNb, true);
+          group_rw(v, 10, 5, true);
+          tile_signs<10, 5>(words, v, tid);
+          if (post) {
+            group_rw(v, 10, 5, false);
+            __syncthreads();
+            group_rw(v, G::kLastLo, G::kLastNb, true);
+          }
         }
       }
       // upwards: the groups of the second transform (or only the way back); a
