@@ -272,9 +272,18 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
   }
   f32x16 acc[kTiles];
   uint32_t nw[4];
+  __bf16* row = partial + slot * mfma15_part_stride(n);
+  if constexpr (kWhole && L % 2 == 1) {
+    // whole blocks, odd L: the chain ends in layout F and the row (its first n
+    // positions, n % 8 == 0: whole 16-byte chunks) goes out from registers, as
+    // the forward's whole blocks do
+    run_chain<L, true>(acc, x, lds, src, [](int i) { return L - i; }, nw);
+    store_direct(acc, x, reinterpret_cast<const uint32_t*>(lds + kLdsBytes) + (L - 1) * kWordsPerLayer,
+                 rsrc(row, (uint32_t)n * 2u));
+    return;
+  }
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
-
-  write_partial_row<L, kWhole, __bf16>(acc, nw, x, lds, partial + slot * mfma15_part_stride(n), n, 1.0f);
+  write_partial_row<L, kWhole, __bf16>(acc, nw, x, lds, row, n, 1.0f);
 }
 
 // ---------------------------------------------------------------- grouped
