@@ -63,50 +63,6 @@ __device__ __forceinline__ void store_range_shifted(const u32x4* stage, __bf16* 
   }
 }
 
-// Output ranges staged and stored one after another by the forward kernel
-// when the chain ends in S1 (odd L): 1, 2 or 4.
-constexpr int kOutPhases = 2;
-
-// The 8 bf16 of a chunk times `scale`, rounded to bf16 (torch's bf16 * scalar).
-__device__ __forceinline__ u32x4 scale_chunk(u32x4 v, float scale) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    v[k] = pk(__uint_as_float(v[k] << 16) * scale, __uint_as_float(v[k] & 0xffff0000u) * scale);
-  return v;
-}
-
-// Whole block (all kB positions, out_r over its 64 KiB) from the chain's S1
-// result: in S1 a lane's chunk k lies in position range (k >> 1) of four
-// (bits 13-14), so the block is staged and stored range by range, a range's
-// stores going out while the next range's chunks are written to LDS.  Each
-// value is multiplied by `scale` (exact when 1) after its rounding to bf16.
-template <int L>
-__device__ __forceinline__ void store_whole_phased(const f32x16 (&acc)[kTiles], const uint32_t (&nw)[4],
-                                                   const Ctx& x, u32x4* stage, __amdgpu_buffer_rsrc_t out_r,
-                                                   float scale) {
-  static_assert(L % 2 == 1, "S1 chunk ranges");
-  u32x4 v[8];
-  out_chunks<L>(acc, nw, x, v);
-  constexpr int kPerPhase = kChunks / kOutPhases;
-#pragma unroll
-  for (int ph = 0; ph < kOutPhases; ++ph) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (k * kOutPhases / 8 == ph) stage[stage_slot(out_chunk_pos<L>(x, k) >> 3)] = v[k];
-    __syncthreads();
-    u32x4 w[kPerPhase / kThreads];
-#pragma unroll
-    for (int i = 0; i < kPerPhase / kThreads; ++i) {
-      w[i] = stage[stage_slot(ph * kPerPhase + i * kThreads + (int)threadIdx.x)];
-      if (scale != 1.0f) w[i] = scale_chunk(w[i], scale);
-    }
-#pragma unroll
-    for (int i = 0; i < kPerPhase / kThreads; ++i)
-      __builtin_amdgcn_raw_buffer_store_b128(w[i], out_r, (ph * kPerPhase + i * kThreads + (int)threadIdx.x) * 16, 0,
-                                             kStreamStore);
-  }
-}
-
 template <int L, bool kWhole>
 __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __restrict__ latent,
                                                             __bf16* __restrict__ out, int n,
@@ -119,29 +75,26 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd(const __bf16* __rest
   load_latent<kWhole>(x, latent, n, src);
   f32x16 acc[kTiles];
   uint32_t nw[4];
-  if constexpr (kWhole && L % 2 == 1) {
-    // whole blocks: the chain ends in layout F and each lane stores its chunks directly
-    run_chain<L, true>(acc, x, lds, src, [](int i) { return i; }, nw);
-    store_direct(acc, x, reinterpret_cast<const uint32_t*>(lds + kLdsBytes) + (L - 1) * kWordsPerLayer,
-                 rsrc(out + (block * kB - start), (uint32_t)(kB * 2)));
-    return;
-  }
-  run_chain<L>(acc, x, lds, src, [](int i) { return i; }, nw);
-  // The signed bf16 block goes through the free exchange buffer in position
-  // order, then to memory with consecutive threads on consecutive chunks.
-  u32x4* stage = reinterpret_cast<u32x4*>(lds + (L & 1) * kXBufBytes);
   // block-local output range [lo, hi); out element of block position p is (base - start) + p
   const int64_t base = block * kB;
   const int lo = kWhole ? 0 : (int)(start - base > 0 ? start - base : 0);
   const int hi = kWhole ? kB : (int)(stop - base < kB ? stop - base : kB);
   __bf16* oblk = out + (base - start);
   const bool full = kWhole || (lo == 0 && hi == kB && (((uintptr_t)oblk & 15) == 0));
-  if constexpr (L % 2 == 1 && kOutPhases > 1) {
+  if constexpr (L % 2 == 1) {
+    // a whole block (uniform): the chain ends in layout F and each lane stores
+    // its chunks directly
     if (full) {
-      store_whole_phased<L>(acc, nw, x, stage, rsrc(oblk, (uint32_t)(kB * 2)), 1.0f);
+      run_chain<L, true>(acc, x, lds, src, [](int i) { return i; }, nw);
+      store_direct(acc, x, reinterpret_cast<const uint32_t*>(lds + kLdsBytes) + (L - 1) * kWordsPerLayer,
+                   rsrc(oblk, (uint32_t)(kB * 2)));
       return;
     }
   }
+  run_chain<L>(acc, x, lds, src, [](int i) { return i; }, nw);
+  // The signed bf16 block goes through the free exchange buffer in position
+  // order, then to memory with consecutive threads on consecutive chunks.
+  u32x4* stage = reinterpret_cast<u32x4*>(lds + (L & 1) * kXBufBytes);
   stage_output<L>(acc, nw, x, stage);
   __syncthreads();
   if (!kWhole && !full && (((uintptr_t)oblk & 1) == 0)) {
@@ -302,18 +255,21 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_fwd_grouped(const GroupT
   load_latent(x, static_cast<const __bf16*>(jb.src), jb.n, src);
   f32x16 acc[kTiles];
   uint32_t nw[4];
-  run_chain<L>(acc, x, lds, src, [](int i) { return i; }, nw);
-  u32x4* stage = reinterpret_cast<u32x4*>(lds + (L & 1) * kXBufBytes);
   const int64_t base = block * kB;
   const int hi = jb.size - base < kB ? (int)(jb.size - base) : kB;
   __bf16* oblk = static_cast<__bf16*>(jb.dst) + base;
   const bool full = hi == kB && (((uintptr_t)oblk & 15) == 0);
-  if constexpr (L % 2 == 1 && kOutPhases > 1) {
+  if constexpr (L % 2 == 1) {
+    // a whole block (uniform): layout F, direct stores, as bfht_mfma15_fwd
     if (full) {
-      store_whole_phased<L>(acc, nw, x, stage, rsrc(oblk, (uint32_t)(kB * 2)), jb.scale);
+      run_chain<L, true>(acc, x, lds, src, [](int i) { return i; }, nw);
+      store_direct(acc, x, reinterpret_cast<const uint32_t*>(lds + kLdsBytes) + (L - 1) * kWordsPerLayer,
+                   rsrc(oblk, (uint32_t)(kB * 2)), jb.scale);
       return;
     }
   }
+  run_chain<L>(acc, x, lds, src, [](int i) { return i; }, nw);
+  u32x4* stage = reinterpret_cast<u32x4*>(lds + (L & 1) * kXBufBytes);
   stage_output<L>(acc, nw, x, stage);
   __syncthreads();
   const auto out_r = rsrc(full ? (const void*)oblk : jb.dst, full ? (uint32_t)(kB * 2) : 0u);

@@ -781,6 +781,14 @@ __device__ __forceinline__ void stage_output(const f32x16 (&acc)[kTiles], const 
   for (int k = 0; k < 8; ++k) stage[stage_slot(out_chunk_pos<L>(x, k) >> 3)] = v[k];
 }
 
+// The 8 bf16 of a chunk times `scale`, rounded to bf16 (torch's bf16 * scalar).
+__device__ __forceinline__ u32x4 scale_chunk(u32x4 v, float scale) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    v[k] = pk(__uint_as_float(v[k] << 16) * scale, __uint_as_float(v[k] & 0xffff0000u) * scale);
+  return v;
+}
+
 // The forward's whole block from layout F (run_chain<L, true>): the last sign
 // layer and 16-byte write-through stores of whole chunks, 1 KiB contiguous per
 // instruction, straight from registers.  `words` is the table slot the chain
@@ -789,8 +797,9 @@ __device__ __forceinline__ void stage_output(const f32x16 (&acc)[kTiles], const 
 // chunk) + 8 p3 (l5) + 16 p4 (l32 bit 0), so after the shift by 4 (l5 + 2 p4) of
 // the unshuffled word, bit q (bit 16 + q) holds the sign of the chunk's value 2q
 // (2q + 1), the pair of word q, and (w << (15 - q)) & kPairSign is its mask.
+// Each value is multiplied by `scale` (exact when 1) after its rounding to bf16.
 __device__ __forceinline__ void store_direct(const f32x16 (&acc)[kTiles], const Ctx& x, const uint32_t* words,
-                                             __amdgpu_buffer_rsrc_t out_r) {
+                                             __amdgpu_buffer_rsrc_t out_r, float scale = 1.0f) {
   const u32x4* wt = reinterpret_cast<const u32x4*>(words) + 2 * ((x.lane32 >> 1) + 16 * x.wave);
   const u32x4 wa = wt[0], wb = wt[1];
   const int sh = 4 * (x.l5 + 2 * (x.lane32 & 1));
@@ -813,6 +822,10 @@ __device__ __forceinline__ void store_direct(const f32x16 (&acc)[kTiles], const 
       v[k][q] ^= m[0] & kPairSign;
       v[k + 4][q] ^= m[1] & kPairSign;
     }
+  }
+  if (scale != 1.0f) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = scale_chunk(v[k], scale);
   }
   const int base = 16 * x.l5 + 32 * x.lane32 + 1024 * x.wave;
 #pragma unroll
