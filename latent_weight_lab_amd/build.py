@@ -3,6 +3,14 @@
 Usage: ``python -m latent_weight_lab_amd.build`` (also called by
 ``__graft_entry__.build()``).  Objects compile in parallel; the library is
 written to a temporary name and renamed, so a reader never sees half a file.
+
+``python -m latent_weight_lab_amd.build --sanitize`` builds a second library,
+``lib/sanitize/liblwl_bfht.so``, whose host code (validators, planners, the
+C ABI) carries AddressSanitizer and UndefinedBehaviorSanitizer; device code is
+compiled as usual.  It is for the CPU test suite only, never for kernels:
+
+    LD_PRELOAD=<clang>/lib/linux/libclang_rt.asan-x86_64.so ASAN_OPTIONS=detect_leaks=0 \
+    LWL_BFHT_LIBRARY=latent_weight_lab_amd/lib/sanitize/liblwl_bfht.so python -m pytest tests -m "not gpu"
 """
 from __future__ import annotations
 
@@ -43,9 +51,17 @@ def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
-def _compile(src: Path) -> Path:
-    obj = OBJ_DIR / (src.name + ".o")
+# Host-only sanitizers (each flag behind -Xarch_host, so no device code is built with them).
+SANITIZE_FLAGS = ["-O1", "-g", "-Xarch_host", "-fno-omit-frame-pointer",
+                  "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                  "-Xarch_host", "-fno-sanitize-recover=undefined"]
+
+
+def _compile(src: Path, obj_dir: Path = OBJ_DIR, sanitize: bool = False) -> Path:
+    obj = obj_dir / (src.name + ".o")
     flags = COMMON_FLAGS + (DEVICE_FLAGS if src.suffix == ".hip" else [])
+    if sanitize:
+        flags = [f for f in flags if f != "-O3"] + SANITIZE_FLAGS
     cmd = [hipcc(), *flags, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -53,23 +69,27 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+def build(verbose: bool = False, sanitize: bool = False) -> Path:
+    out_dir = OUT_DIR / "sanitize" if sanitize else OUT_DIR
+    obj_dir = out_dir / "obj"
+    lib = out_dir / LIB.name
+    obj_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-        objs = list(pool.map(_compile, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+        objs = list(pool.map(lambda s: _compile(s, obj_dir, sanitize), srcs))
+    tmp = lib.with_suffix(".so.tmp")
+    link = ["-shared-libasan", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined"] if sanitize else []
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *link, "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, sanitize="--sanitize" in sys.argv[1:])
     sys.exit(0)
