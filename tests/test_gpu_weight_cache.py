@@ -37,6 +37,9 @@ JOBS = [
     (10, 7 * 33, 3, -4, 1.0, F32, F16),               # block 2^4 (256 blocks per workgroup), partial
     (1, 5, 2, 3, 1.5, F32, F32),                      # one-element latent, block 2^0
     (4096, 4096, 3, 11, 1.0, BF16, F32),              # bf16 latent, block 2^12, fp32 cache
+    (32768, 300 * 1000, 3, 12, 0.75, BF16, BF16),     # matrix cores, odd L: whole blocks stored from
+                                                      # registers, the partial last one staged; scaled
+    (30000, 512 * 700, 1, 13, 1.0, BF16, BF16),       # matrix cores, one layer, partial last block
 ]
 
 
