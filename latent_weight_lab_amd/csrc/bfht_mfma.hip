@@ -226,13 +226,13 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd(const __bf16* __rest
   f32x16 acc[kTiles];
   uint32_t nw[4];
   __bf16* row = partial + slot * mfma15_part_stride(n);
-  if constexpr (kWhole && L % 2 == 1) {
-    // whole blocks, odd L: the chain ends in layout F and the row (its first n
-    // positions, n % 8 == 0: whole 16-byte chunks) goes out from registers, as
-    // the forward's whole blocks do
+  if constexpr (L % 2 == 1) {
+    // odd L: the chain ends in layout F and the row goes out from registers,
+    // as the forward's whole blocks do, in whole 16-byte chunks up to the row
+    // stride (n rounded up to 8; the block sum reads only the first n)
     run_chain<L, true>(acc, x, lds, src, [](int i) { return L - i; }, nw);
     store_direct(acc, x, reinterpret_cast<const uint32_t*>(lds + kLdsBytes) + (L - 1) * kWordsPerLayer,
-                 rsrc(row, (uint32_t)n * 2u));
+                 rsrc(row, (uint32_t)mfma15_part_stride(n) * 2u));
     return;
   }
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
@@ -342,9 +342,17 @@ __global__ __launch_bounds__(kThreads) void bfht_mfma15_bwd_grouped(const GroupT
   }
   f32x16 acc[kTiles];
   uint32_t nw[4];
+  __bf16* row = static_cast<__bf16*>(jb.part) + slot * (int64_t)jb.stride;
+  if constexpr (L % 2 == 1) {
+    // odd L: the row from layout F in whole 16-byte chunks up to the row stride
+    // (a multiple of 64; the block sum reads only the first n), as bfht_mfma15_bwd
+    run_chain<L, true>(acc, x, lds, src, [](int i) { return L - i; }, nw);
+    store_direct(acc, x, reinterpret_cast<const uint32_t*>(lds + kLdsBytes) + (L - 1) * kWordsPerLayer,
+                 rsrc(row, (uint32_t)jb.stride * 2u));
+    return;
+  }
   run_chain<L>(acc, x, lds, src, [](int i) { return L - i; }, nw);
-  write_partial_row<L, false, __bf16>(acc, nw, x, lds, static_cast<__bf16*>(jb.part) + slot * (int64_t)jb.stride,
-                                      jb.n, 1.0f);
+  write_partial_row<L, false, __bf16>(acc, nw, x, lds, row, jb.n, 1.0f);
 }
 
 }  // namespace
