@@ -118,6 +118,16 @@ constexpr int64_t linear_table_bytes(int64_t in_features, int64_t pitch) {
   const int64_t steps = linear_steps(in_features);
   return (4 * steps * pitch + steps) * 16;
 }
+// Three-block row tiles: the first k steps whose table (4 pitch + 1 slots per
+// step) fits in the LDS, in whole prefetch rounds; the W tiles of the steps
+// after them go to the workgroup's overflow in global memory.
+__host__ __device__ constexpr int linear_lds_steps(int nsteps, int pitch) {
+  const int fit = (kLinearLdsBytes / 16) / (4 * pitch + 1) / kDepth * kDepth;
+  return fit < nsteps ? fit : nsteps;
+}
+// Three-block row tiles: the staging area of the first two blocks' generated
+// chunks (8 per thread and block) while the third block's chain runs.
+constexpr int kStageBytes = 2 * 8 * mfma15::kThreads * 16;
 // Table rows: whole 16-row tiles when they fit in the LDS, else the exact row
 // count (the reads of the last row tile then run up to 15 rows past the table,
 // into entries whose output columns are never stored, so an exact table leaves
@@ -138,7 +148,10 @@ constexpr int64_t kTiledMinTokens = 256;
 
 // Tiled x: for token tile T (16 tokens) and k step s, 64 16-byte chunks in
 // lane order, chunk (l16 + 16*kq) = x[16*T + l16][32*s + 8*kq .. +7]; tokens
-// past the end and k past the row are zero.
+// past the end and k past the row are zero.  Step-major: the 1 KiB group of
+// (s, T) is the (s * tiles + T)-th, so the token tiles a workgroup reads at one
+// k step are one contiguous run (token-tile-major, they lay a whole row's
+// steps apart and the contraction's x stream ran slower).
 struct XTiling {
   int64_t tiles;  // token tiles
   int steps;      // k steps holding data: ceil(in / 32)
@@ -154,7 +167,31 @@ bool linear_tiled(const LinearArgs& a) {
   return a.tokens >= kTiledMinTokens && x_tiling(a).bytes() < ((size_t)1 << 31);
 }
 
+// Rows of a three-block row tile at this row length, or 0: three blocks hold a
+// whole number of rows that two do not, in one or two 16-row tiles, with no k
+// padding (in_features 3072: 32 rows).
+int linear_three_block_rows(int64_t in_features) {
+  const int64_t len = 3 * (int64_t)mfma15::kB;
+  if (in_features % (kKStep * kDepth) != 0 || len % in_features != 0 || (2 * mfma15::kB) % in_features == 0)
+    return 0;
+  const int64_t rows = len / in_features;
+  return rows % 16 == 0 && rows / 16 <= 2 ? (int)rows : 0;
+}
+
+// Batches from this many tokens use three-block tiles where they apply: a
+// workgroup's three chains, the staging round trip and the scatter take ~29 us
+// against the pair chain's ~13, and the contraction streams a third less x
+// (3072 -> 768: 57.7 / 52.5 us at 2048 tokens, 71.5 / 77.0 at 4096, 190 / 237
+// at 16384, three / two blocks).
+constexpr int64_t kThreeBlockMinTokens = 3072;
+
 size_t partial_bytes(const LinearArgs& a) {
+  if (a.blocks_per_wg == 3) {  // every work item's overflow W tiles and staging area
+    const int nt = a.rows_per_tile / 16, nsteps = linear_steps(a.in_features);
+    const int64_t per_item = (int64_t)(nsteps - linear_lds_steps(nsteps, 16 * nt)) * nt * 1024 + kStageBytes;
+    const int64_t items = (a.out_features + a.rows_per_tile - 1) / a.rows_per_tile * a.token_splits;
+    return ((size_t)(items * per_item) + 255) / 256 * 256;
+  }
   if (a.rows_per_tile > 0) return 0;  // row tiles: no straddling rows
   const int64_t ntiles = (a.nblocks_w + a.blocks_per_wg - 1) / a.blocks_per_wg;
   return ((size_t)ntiles * 2 * (size_t)a.tokens * sizeof(float) + 255) / 256 * 256;
@@ -177,7 +214,8 @@ __global__ __launch_bounds__(256) void bfht_linear_tile_x(const unsigned char* _
   const int tt = wv / runs;
   const int s0 = (wv - tt * runs) * kTileSteps;
   const auto x_r = rsrc(x, (uint32_t)((int64_t)tokens * row_bytes));
-  const auto xt_r = rsrc(xt, (uint32_t)((int64_t)(tt + 1) * steps * 1024));
+  const int tiles = waves / runs;
+  const auto xt_r = rsrc(xt, (uint32_t)((int64_t)tiles * steps * 1024));
   const int lane = threadIdx.x & 63;
   const int t = tt * kTokTile + (lane & 15);
   const int k0 = 64 * s0 + 16 * (lane >> 4);
@@ -191,7 +229,7 @@ __global__ __launch_bounds__(256) void bfht_linear_tile_x(const unsigned char* _
 #pragma unroll
   for (int j = 0; j < kTileSteps; ++j) {
     const int s = s0 + j;  // steps past the row are not stored (the copy holds `steps` steps per tile)
-    const int off = s < steps ? ((tt * steps + s) * 64 + lane) * 16 : (int)0x80000000;
+    const int off = s < steps ? ((s * tiles + tt) * 64 + lane) * 16 : (int)0x80000000;
     __builtin_amdgcn_raw_buffer_store_b128(v[j], xt_r, off, 0, kStreamStore);
   }
 }
@@ -207,13 +245,20 @@ __global__ __launch_bounds__(256) void bfht_linear_tile_x(const unsigned char* _
 // block of its first position (linear_rows_per_tile), so no row straddles two
 // tiles: the generated positions outside the tile are dropped, every row is
 // stored directly, and no partial dot products or combine are needed.
+// KB = 3 (row tiles, linear_three_block_rows): three whole blocks hold a whole
+// number of rows (in_features 3072: 32 rows, 1.5 times the rows per loaded x
+// element of a two-block tile) but their table does not fit in the LDS: the
+// first linear_lds_steps k steps are read from the LDS table, the rest from
+// this workgroup's overflow in `partial`, written in MFMA B-operand order
+// (per k step and row tile, 64 lanes x 16 bytes) and read with the x stream.
 template <int L, int NT, bool kTiled, int KB, bool kEpi, bool kRowTiles = false, int KG = kGroup, int KD = kDepth>
 __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const __bf16* __restrict__ latent,
                                             __bf16* __restrict__ out, float* __restrict__ partial, int tokens,
                                             int in_f, int out_f, int n, uint32_t seed32, float scale,
                                             int token_split, int64_t nblocks, int pitch, int split, int64_t tile,
                                             const LinearEpi& ep, unsigned char* lds, int rows_per_tile = 0) {
-  static_assert(!kRowTiles || KB == 2, "row tiles span two generated blocks");
+  static_assert(!kRowTiles || KB == 2 || KB == 3, "row tiles span two or three generated blocks");
+  static_assert(KB != 3 || (kRowTiles && kTiled), "three-block tiles are row tiles over the tiled x");
   const int64_t size = (int64_t)in_f * out_f;
   const int64_t tile_len = kRowTiles ? (int64_t)rows_per_tile * in_f : (int64_t)KB * kB;
   const int64_t g0 = tile * tile_len;                             // first flat position
@@ -227,6 +272,14 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
   // rows past the row length are zero, x offsets past it are out of range)
   const int nsteps = linear_steps(in_f);
   const int kchunks = 4 * nsteps;  // 8-element k chunks per table row
+  // three-block tiles: the k steps read from the LDS table, and this work
+  // item's overflow (its own region of `partial`: work item split * tiles + tile)
+  const int lds_steps = KB == 3 ? linear_lds_steps(nsteps, pitch) : nsteps;
+  const uint32_t ovf_bytes = KB == 3 ? (uint32_t)(nsteps - lds_steps) * NT * 1024u : 0u;
+  const int64_t item = KB == 3 ? split * (int64_t)((out_f + rows_per_tile - 1) / rows_per_tile) + tile : 0;
+  unsigned char* item_ws = reinterpret_cast<unsigned char*>(partial) + item * (ovf_bytes + (KB == 3 ? kStageBytes : 0));
+  const auto ovf_r = rsrc(item_ws, ovf_bytes);
+  const auto stage_r = rsrc(item_ws + ovf_bytes, KB == 3 ? (uint32_t)kStageBytes : 0u);
 
   // 1. generate the tile's blocks (signed bf16; the first kept in registers
   //    while the next one's chain uses the LDS) and scatter them into LDS as a
@@ -249,7 +302,39 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     const float inv_in = 1.0f / (float)in_f;
     u32x4 v[KB][8];
     const bool two = kRowTiles ? g1 > ((b_first + 1) << kLog) : (KB == 2 && tile * KB + 1 < nblocks);
-    if (KB == 2 && two) {  // both blocks at once (uniform across the workgroup)
+    if constexpr (KB == 3) {
+      // one block at a time (each chain reuses the LDS once every wave has
+      // read the previous one's last exchange; the pair chain, whose peak
+      // register use leaves no room for a third block's chunks, is slower
+      // here than two single chains); the last tile of a matrix may generate
+      // blocks past its end, whose positions are dropped
+      // The first two blocks' chunks wait in this work item's staging area
+      // (8 coalesced 16-byte stores per thread and block) while the later
+      // chains run, and come back with all 16 loads in flight at once: kept in
+      // registers through a chain they would be spilled, and the compiler
+      // reloads spilled registers one memory round trip at a time.
+#pragma unroll
+      for (int kb = 0; kb < 3; ++kb) {
+        if (kb > 0) __syncthreads();
+        const Ctx cb = make_ctx(seed32, b_first + kb);
+        u32x4 src[kTiles][2];
+        load_latent(cb, latent, n, src);
+        f32x16 acc[kTiles];
+        uint32_t nw[4];
+        run_chain<L>(acc, cb, lds, src, [](int i) { return i; }, nw);
+        out_chunks<L>(acc, nw, cb, v[kb]);
+        if (kb < 2) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            __builtin_amdgcn_raw_buffer_store_b128(v[kb][k], stage_r, ((kb * 8 + k) * kThreads + threadIdx.x) * 16, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          v[kb][k] = __builtin_amdgcn_raw_buffer_load_b128(stage_r, ((kb * 8 + k) * kThreads + threadIdx.x) * 16, 0, 0);
+    } else if (KB == 2 && two) {  // both blocks at once (uniform across the workgroup)
       const Ctx c[2] = {make_ctx(seed32, b_first), make_ctx(seed32, b_first + 1)};
       u32x4 src[kTiles][2];
       load_latent(c[0], latent, n, src);
@@ -272,7 +357,8 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     // (disjoint from it, so no barrier in between): chunks before the tile's
     // start in row 0 and from its end in the last row, and k padding.  Rows
     // past the last one stay as they are (their output columns are not stored).
-    {
+    // Three-block tiles are whole rows with no k padding (in_features % 128 == 0).
+    if constexpr (KB != 3) {
       const int n_edge = 2 * kchunks;  // rows 0 and nrows - 1, every kc
       for (int i = threadIdx.x; i < n_edge; i += kThreads) {
         const int e = i >= kchunks;
@@ -293,7 +379,7 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     const Ctx c = make_ctx(seed32, b_first);  // chunk positions do not depend on the block
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      if (kRowTiles && kb > 0 && !two) break;  // uniform: no second block
+      if (KB == 2 && kRowTiles && kb > 0 && !two) break;  // uniform: no second block
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int rel = off + kb * kB + out_chunk_pos<L>(c, k);
@@ -302,7 +388,14 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
         r += (r + 1) * in_f <= rel;
         const int kc = (rel - r * in_f) >> 3;
         // chunks of 8 positions lie wholly inside or outside [g0, g1) (all multiples of 8)
-        if (rel >= rel_lo && rel < rel_hi) table[table_slot(kc, r, pitch)] = v[kb][k];
+        if (rel >= rel_lo && rel < rel_hi) {
+          if (KB != 3 || kc < 4 * lds_steps) {
+            table[table_slot(kc, r, pitch)] = v[kb][k];
+          } else {  // overflow: k step kc / 4, row tile r / 16, lane (r % 16) + 16 (kc % 4)
+            const int e = (((kc >> 2) - lds_steps) * NT + (r >> 4)) * 64 + (r & 15) + 16 * (kc & 3);
+            __builtin_amdgcn_raw_buffer_store_b128(v[kb][k], ovf_r, e * 16, 0, 0);
+          }
+        }
       }
     }
   }
@@ -361,13 +454,13 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
   // Tiles from `tend` on are masked.
   auto pass = [&](auto g_const, int tg, int tend) {
     constexpr int G = decltype(g_const)::value;
-    constexpr int D = G == 1 ? kDepthSingle : KD;
+    constexpr int D = (G == 1 && KB != 3) ? kDepthSingle : KD;
     uint32_t xo[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int tt = tg + g, t = tt * kTokTile + l16;
       if constexpr (kTiled)
-        xo[g] = tt < tend ? (uint32_t)((tt * xsteps * 64 + lane) * 16) : kOff;
+        xo[g] = tt < tend ? (uint32_t)((tt * 64 + lane) * 16) : kOff;
       else
         xo[g] = (tt < tend && t < tokens) ? (uint32_t)((t * in_f + 8 * kq) * 2) : kOff;
     }
@@ -376,7 +469,7 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     auto xload = [&](int g, int step) -> u32x4 {
       if constexpr (kTiled) {
         const uint32_t off = step < xsteps ? xo[g] : kOff;
-        return __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)off, step * 1024, 0);
+        return __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)off, step * ntiles_all * 1024, 0);
       } else {
         const uint32_t off = (step * kKStep + 8 * kq < in_f) ? xo[g] : kOff;
         return __builtin_amdgcn_raw_buffer_load_b128(x_r, (int)off, step * kKStep * 2, 0);
@@ -387,6 +480,20 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) acc[g][nt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    // three-block tiles: the W tiles of the overflow steps (lds_steps on), D
+    // steps ahead like x; the first D are loaded first, so they have arrived
+    // by the time the loop waits for its x
+    auto wload = [&](int nt, int step) -> u32x4 {
+      const uint32_t off = step < nsteps ? (uint32_t)(lane * 16) : kOff;
+      return __builtin_amdgcn_raw_buffer_load_b128(ovf_r, (int)off, ((step - lds_steps) * NT + nt) * 1024, 0);
+    };
+    u32x4 wring[KB == 3 ? D : 1][NT];
+    if constexpr (KB == 3) {
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) wring[d][nt] = wload(nt, lds_steps + d);
+    }
     // Issue the first KD steps' loads in slot order, the order the loop
     // refills them in: the wait counts the compiler derives at the loop
     // head then let slot d's data arrive behind the later slots' requests.
@@ -403,10 +510,10 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     u32x4 bt[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) bt[nt] = brd(bs, nt);
-    for (int s0 = 0; s0 < nsteps; s0 += D) {
+    for (int s0 = 0; s0 < lds_steps; s0 += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        const int sn = (s0 + d + 1 < nsteps) ? s0 + d + 1 : nsteps - 1;
+        const int sn = (s0 + d + 1 < lds_steps) ? s0 + d + 1 : lds_steps - 1;
         const u32x4* bsn = brow + sn * (4 * pitch + 1);
         u32x4 bn[NT];
 #pragma unroll
@@ -425,6 +532,24 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < G; ++g) ring[d][g] = xload(g, s0 + d + D);
+      }
+    }
+    if constexpr (KB == 3) {
+      // the overflow steps: W from the ring, refilled with x (lds_steps and
+      // nsteps are whole prefetch rounds; loads past nsteps read 0)
+      for (int s0 = lds_steps; s0 < nsteps; s0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[g][nt] = mfma16(ring[d][g], wring[d][nt], acc[g][nt]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int g = 0; g < G; ++g) ring[d][g] = xload(g, s0 + d + D);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) wring[d][nt] = wload(nt, s0 + d + D);
+        }
       }
     }
     // D[m = 4*kq + r][n = l16]: token 16 tt + 4 kq + r, row o_first + 16 nt + l16.
@@ -617,8 +742,8 @@ hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial
   switch (nt) {
     case 1: LWL_LIN(1); break;
     case 2: LWL_LIN(2); break;
-    case 3: LWL_LIN(3); break;
-    case 4: LWL_LIN(4); break;
+    case 3: if constexpr (KB != 3) LWL_LIN(3); else return hipErrorInvalidValue; break;
+    case 4: if constexpr (KB != 3) LWL_LIN(4); else return hipErrorInvalidValue; break;
     case 5: if constexpr (KB == 2) LWL_LIN(5); else return hipErrorInvalidValue; break;
     case 6: if constexpr (KB == 2) LWL_LIN(6); else return hipErrorInvalidValue; break;
     default: return hipErrorInvalidValue;
@@ -636,6 +761,7 @@ hipError_t launch_linear_kb(const LinearArgs& a, const __bf16* x, float* partial
 template <int L, bool kTiled, bool kEpi>
 hipError_t launch_linear_e(const LinearArgs& a, const __bf16* x, float* partial, hipStream_t s) {
   if constexpr (kTiled) {
+    if (a.blocks_per_wg == 3) return launch_linear_kb<L, true, 3, kEpi, true>(a, x, partial, s);
     if (a.blocks_per_wg == 2 && a.rows_per_tile > 0) return launch_linear_kb<L, true, 2, kEpi, true>(a, x, partial, s);
     if (a.blocks_per_wg == 2) return launch_linear_kb<L, true, 2, kEpi>(a, x, partial, s);
   }
@@ -822,8 +948,10 @@ int linear_blocks_per_wg(const LinearArgs& a) {
   // holds at most 64 rows (the contraction is bound by streaming x, and two
   // blocks feed each x element twice the rows: at 768 -> 3072 the second chain
   // costs ~7 us and the contraction saves ~13), their rows fit the register
-  // budget and their table the LDS.
+  // budget and their table the LDS.  Three when three blocks hold whole rows
+  // (linear_three_block_rows) and the batch is large enough to pay the third chain.
   if (!linear_tiled(a) || a.nblocks_w < 2 || linear_rows(a.in_features, 1) > 64) return 1;
+  if (a.nblocks_w >= 3 && a.tokens >= kThreeBlockMinTokens && linear_three_block_rows(a.in_features) > 0) return 3;
   if (linear_row_tiles(a.in_features, 2) > kMaxNT2) return 1;
   return linear_pitch_fits(a.in_features, 2) ? 2 : 1;
 }
@@ -837,6 +965,7 @@ int linear_rows_per_tile(const LinearArgs& a) {
   // one holding its start, whose offset in that block is a multiple of
   // gcd(R in, 2^15) and at most 2^15 - gcd: R in + 2^15 - gcd <= 2^16.
   // GPT-2's rows of 768: R = 64 (1.5 blocks per tile).
+  if (a.blocks_per_wg == 3) return linear_three_block_rows(a.in_features);
   if (a.blocks_per_wg != 2 || (2 * mfma15::kB) % a.in_features == 0) return 0;
   for (int R = 16 * kMaxNT2; R >= 48; R -= 16) {
     const int64_t len = (int64_t)R * a.in_features;

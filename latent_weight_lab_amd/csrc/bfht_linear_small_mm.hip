@@ -160,10 +160,10 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small_mm(const T* __r
   const int l16 = lane & 15, kq = lane >> 4;
   constexpr int kWaves = Gm::WG / 64;
   const int nsteps = in_f / MG::KSTEP;  // 64 bytes of k per step
-  // x: the tiled copy (1 KiB per token tile and step) or the row-major input
+  // x: the tiled copy (1 KiB per token tile and step, step-major) or the row-major input
   const bool tiled = xt != nullptr;
   const auto x_r = tiled ? tile_rsrc(xt, (uint64_t)ntt * nsteps * 1024) : tile_rsrc(x, (uint64_t)tokens * in_f * sizeof(T));
-  const uint32_t xstride = tiled ? 1024u : 64u;
+  const uint32_t xstride = tiled ? (uint32_t)ntt * 1024u : 64u;  // per step
   const auto o_r = tile_rsrc(out, (uint64_t)tokens * out_f * sizeof(T));
   const bool has_xs = ep.xsum != nullptr, has_base = ep.base != nullptr, has_bias = ep.bias != nullptr;
   const float cx = has_xs ? ep.cscale * *ep.coef : 0.f;
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small_mm(const T* __r
     for (int g = 0; g < kMmTok; ++g) {
       const int t = (ttb + g) * 16 + l16;
       if (tiled)
-        xo[g] = ttb + g < tt1 ? (uint32_t)(((ttb + g) * nsteps * 64 + lane) * 16) : kOff;
+        xo[g] = ttb + g < tt1 ? (uint32_t)(((ttb + g) * 64 + lane) * 16) : kOff;
       else
         xo[g] = (ttb + g < tt1 && t < tokens) ? (uint32_t)(t * in_f + (MG::KSTEP / 4) * kq) * (uint32_t)sizeof(T) : kOff;
     }
