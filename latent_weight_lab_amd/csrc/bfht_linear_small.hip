@@ -44,6 +44,7 @@ struct LdsWeightStore {
 };
 
 constexpr int kQuad = 4;  // tokens per team pass
+constexpr int kSpan = 8;  // k iterations of a lane whose x loads are in flight together
 
 template <int LB>
 struct SmallLinearGeo {
@@ -67,6 +68,29 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small(const T* __rest
   const int64_t size = (int64_t)in_f * out_f;
   const int64_t base = tile * SG::kTileElems;
 
+  // this split's token quads, and the x of a quad staged in LDS (step 2)
+  const int quads = (tokens + kQuad - 1) / kQuad;
+  const int per_split = (quads + token_split - 1) / token_split;
+  const int q0 = split * per_split;
+  const int q1 = q0 + per_split < quads ? q0 + per_split : quads;
+  const auto x_r = tile_rsrc(x, (uint64_t)tokens * in_f * sizeof(T));
+  const int nstage = kQuad * in_f;
+  const bool staged = nstage <= BlockLds<LB>::FLOATS;
+  // thread's share i0 + e * WG (e < kSpan) of quad q's staged x (tokens past the batch read 0)
+  auto stage_load = [&](int q, int i0, float (&v)[kSpan]) {
+#pragma unroll
+    for (int e = 0; e < kSpan; ++e) {
+      const int i = i0 + e * Gm::WG;
+      const int t = q * kQuad + (i >> log_in);
+      v[e] = buf_load<T>(x_r, i < nstage && t < tokens ? t * in_f + (i & (in_f - 1)) : -1);
+    }
+  };
+  // When one round of loads stages a quad, the first quad's are issued before
+  // the generator runs, which hides their latency.
+  const bool prefetch = staged && nstage <= kSpan * Gm::WG && q0 < q1;
+  float xpre[kSpan];
+  if (prefetch) stage_load(q0, (int)threadIdx.x, xpre);
+
   // 1. the tile's G blocks (inactive slots past the last block store nothing;
   //    their rows lie past out_features and are never read)
   const int64_t slot = tile * Gm::G + (threadIdx.x >> Gm::LT);
@@ -78,10 +102,6 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small(const T* __rest
   const int row0 = (int)(base >> log_in);
   const int tile_rows = SG::kTileElems >> log_in;
   const int rows = out_f - row0 < tile_rows ? out_f - row0 : tile_rows;
-  const int quads = (tokens + kQuad - 1) / kQuad;
-  const int per_split = (quads + token_split - 1) / token_split;
-  const int q0 = split * per_split;
-  const int q1 = q0 + per_split < quads ? q0 + per_split : quads;
   if (rows <= 0 || q0 >= q1) return;  // uniform across the workgroup
   const int log_ks = log_in < 6 ? log_in : 6;  // lanes per team: min(in, 64)
   const int ks = 1 << log_ks;
@@ -90,7 +110,6 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small(const T* __rest
   const int team = (int)(threadIdx.x >> log_ks);
   const int nteams = Gm::WG >> log_ks;
   const int npairs = (q1 - q0) * rows;
-  const auto x_r = tile_rsrc(x, (uint64_t)tokens * in_f * sizeof(T));
   const auto o_r = tile_rsrc(out, (uint64_t)tokens * out_f * sizeof(T));
   // epilogue terms (uniform); absent inputs get empty resources
   const bool has_xs = ep.xsum != nullptr, has_base = ep.base != nullptr, has_bias = ep.bias != nullptr;
@@ -98,36 +117,132 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small(const T* __rest
   const auto xs_r = tile_rsrc(has_xs ? (const void*)ep.xsum : (const void*)out, has_xs ? (uint64_t)tokens * 4 : 0);
   const auto b_r = tile_rsrc(has_base ? ep.base : (const void*)out, has_base ? (uint64_t)tokens * out_f * sizeof(T) : 0);
   const auto bias_r = tile_rsrc(has_bias ? ep.bias : (const void*)out, has_bias ? (uint64_t)out_f * sizeof(T) : 0);
-  // A team's lanes share `pr`, so the shuffles below only read lanes that run
-  // the same iteration.
-  for (int pr = team; pr < npairs; pr += nteams) {
-    const int q = q0 + pr / rows;
-    const int r = pr - (pr / rows) * rows;
+  // One team pass: rows r, r + rstride, ... (NR of them; those from `rows` on
+  // compute on row r and store nothing) against the first NU tokens of quad q
+  // (NU = 1 for a quad holding one token, else kQuad).  Lane j adds
+  // x[t][k] w[row][k] for k = j, j + ks, ... in that order (x from `xat`),
+  // then the team's lanes are summed with butterfly shuffles.  A team's lanes
+  // share the pass, so the shuffles only read lanes that run the same
+  // iteration.  Every (row, token) sum takes the same additions in the same
+  // order whatever NR and NU are.
+  auto pass = [&](auto nr_c, auto nu_c, int q, int r, int rstride, auto xat) {
+    constexpr int NR = decltype(nr_c)::value, NU = decltype(nu_c)::value;
     const int t0 = q * kQuad;
-    const float* wrow = wt + (r << log_in);
-    int xi[kQuad];
+    const float* wrow[NR];
 #pragma unroll
-    for (int u = 0; u < kQuad; ++u) xi[u] = t0 + u < tokens ? (t0 + u) * in_f : -1;  // -1: reads 0
-    float acc[kQuad] = {0.f, 0.f, 0.f, 0.f};
-    for (int k = j; k < in_f; k += ks) {
-      const float w = wrow[k];
-#pragma unroll
-      for (int u = 0; u < kQuad; ++u) acc[u] += buf_load<T>(x_r, xi[u] < 0 ? -1 : xi[u] + k) * w;
+    for (int h = 0; h < NR; ++h) {
+      const int rh = r + h * rstride;
+      wrow[h] = wt + ((rh < rows ? rh : r) << log_in);
     }
+    float acc[NR][NU];
 #pragma unroll
-    for (int u = 0; u < kQuad; ++u)
-      for (int s = ks >> 1; s >= 1; s >>= 1) acc[u] += __shfl_xor(acc[u], s, 64);
-    if (j == 0) {
-      const int o = row0 + r;
-      const float bias_o = has_bias ? buf_load<T>(bias_r, o) : 0.f;
+    for (int h = 0; h < NR; ++h)
 #pragma unroll
-      for (int u = 0; u < kQuad; ++u) {
-        const int t = t0 + u;
-        const int i = t < tokens ? t * out_f + o : -1;  // -1: loads read 0, the store is dropped
-        const float xs = has_xs ? cx * buf_load<float>(xs_r, t < tokens ? t : -1) : 0.f;
-        const float base_v = has_base ? buf_load<T>(b_r, i) : 0.f;
-        buf_store<T>(linear_epilogue(acc[u], has_xs, xs, has_base, base_v, has_bias, bias_o), o_r, i);
+      for (int u = 0; u < NU; ++u) acc[h][u] = 0.f;
+    // kSpan iterations' loads are issued before their products (the loop's
+    // trip count is not known at compile time, so without this each iteration
+    // waited out one load's latency); the k order is the same either way
+    int k = j;
+    for (; k + (kSpan - 1) * ks < in_f; k += kSpan * ks) {
+      float xv[kSpan][NU], wv[kSpan][NR];
+#pragma unroll
+      for (int i = 0; i < kSpan; ++i) {
+#pragma unroll
+        for (int h = 0; h < NR; ++h) wv[i][h] = wrow[h][k + i * ks];
+#pragma unroll
+        for (int u = 0; u < NU; ++u) xv[i][u] = xat(t0, u, k + i * ks);
       }
+#pragma unroll
+      for (int i = 0; i < kSpan; ++i)
+#pragma unroll
+        for (int h = 0; h < NR; ++h)
+#pragma unroll
+          for (int u = 0; u < NU; ++u) acc[h][u] += xv[i][u] * wv[i][h];
+    }
+    for (; k < in_f; k += ks) {
+#pragma unroll
+      for (int h = 0; h < NR; ++h) {
+        const float w = wrow[h][k];
+#pragma unroll
+        for (int u = 0; u < NU; ++u) acc[h][u] += xat(t0, u, k) * w;
+      }
+    }
+    // the lane sums: each distance's shuffles of every sum in flight together
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+      if (s >= ks) continue;  // uniform
+      float sh[NR][NU];
+#pragma unroll
+      for (int h = 0; h < NR; ++h)
+#pragma unroll
+        for (int u = 0; u < NU; ++u) sh[h][u] = __shfl_xor(acc[h][u], s, 64);
+#pragma unroll
+      for (int h = 0; h < NR; ++h)
+#pragma unroll
+        for (int u = 0; u < NU; ++u) acc[h][u] += sh[h][u];
+    }
+    if (j == 0) {
+#pragma unroll
+      for (int h = 0; h < NR; ++h) {
+        const int rh = r + h * rstride;
+        if (rh >= rows) continue;  // uniform across the team
+        const int o = row0 + rh;
+        const float bias_o = has_bias ? buf_load<T>(bias_r, o) : 0.f;
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+          const int t = t0 + u;
+          const int i = t < tokens ? t * out_f + o : -1;  // -1: loads read 0, the store is dropped
+          const float xs = has_xs ? cx * buf_load<float>(xs_r, t < tokens ? t : -1) : 0.f;
+          const float base_v = has_base ? buf_load<T>(b_r, i) : 0.f;
+          buf_store<T>(linear_epilogue(acc[h][u], has_xs, xs, has_base, base_v, has_bias, bias_o), o_r, i);
+        }
+      }
+    }
+  };
+  using One = std::integral_constant<int, 1>;
+  using Two = std::integral_constant<int, 2>;
+  using Quad = std::integral_constant<int, kQuad>;
+  if (staged) {
+    // Each quad's x rows are staged once in the generator's LDS (its exchange
+    // buffers and sign tables, free after the barrier above) and every team
+    // reads them there: read from memory, all the workgroup's passes (and all
+    // the workgroups of an XCD, at decode batches) ask its L2 for the same
+    // few lines.  Tokens past the batch stage as 0.
+    float* xs = smem;
+    for (int q = q0; q < q1; ++q) {
+      if (q > q0) __syncthreads();  // every team has read the previous quad
+      for (int i0 = (int)threadIdx.x; i0 < nstage; i0 += kSpan * Gm::WG) {
+        float v[kSpan];
+        if (prefetch && q == q0) {
+#pragma unroll
+          for (int e = 0; e < kSpan; ++e) v[e] = xpre[e];
+        } else {
+          stage_load(q, i0, v);
+        }
+#pragma unroll
+        for (int e = 0; e < kSpan; ++e)
+          if (i0 + e * Gm::WG < nstage) xs[i0 + e * Gm::WG] = v[e];
+      }
+      __syncthreads();
+      // two rows per pass (x read once for both); a quad of one token (decode)
+      // computes that token alone
+      auto xat = [&](int, int u, int kk) { return xs[(u << log_in) + kk]; };
+      const bool single = tokens - q * kQuad == 1;
+      for (int r = team; r < rows; r += 2 * nteams) {
+        if (single)
+          pass(Two{}, One{}, q, r, nteams, xat);
+        else
+          pass(Two{}, Quad{}, q, r, nteams, xat);
+      }
+    }
+  } else {
+    for (int pr = team; pr < npairs; pr += nteams) {
+      const int q = q0 + pr / rows;
+      int xi[kQuad];
+#pragma unroll
+      for (int u = 0; u < kQuad; ++u) xi[u] = q * kQuad + u < tokens ? (q * kQuad + u) * in_f : -1;  // -1: reads 0
+      pass(One{}, Quad{}, q, pr - (pr / rows) * rows, 0,
+           [&](int, int u, int kk) { return buf_load<T>(x_r, xi[u] < 0 ? -1 : xi[u] + kk); });
     }
   }
 }
