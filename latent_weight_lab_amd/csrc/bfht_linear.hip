@@ -125,9 +125,9 @@ __host__ __device__ constexpr int linear_lds_steps(int nsteps, int pitch) {
   const int fit = (kLinearLdsBytes / 16) / (4 * pitch + 1) / kDepth * kDepth;
   return fit < nsteps ? fit : nsteps;
 }
-// Three-block row tiles: the staging area of the first two blocks' generated
-// chunks (8 per thread and block) while the third block's chain runs.
-constexpr int kStageBytes = 2 * 8 * mfma15::kThreads * 16;
+// Three-block row tiles: the staging area of the first block's generated
+// chunks (8 per thread) while the other two blocks' chains run.
+constexpr int kStageBytes = 8 * mfma15::kThreads * 16;
 // Table rows: whole 16-row tiles when they fit in the LDS, else the exact row
 // count (the reads of the last row tile then run up to 15 rows past the table,
 // into entries whose output columns are never stored, so an exact table leaves
@@ -308,11 +308,12 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       // register use leaves no room for a third block's chunks, is slower
       // here than two single chains); the last tile of a matrix may generate
       // blocks past its end, whose positions are dropped
-      // The first two blocks' chunks wait in this work item's staging area
-      // (8 coalesced 16-byte stores per thread and block) while the later
-      // chains run, and come back with all 16 loads in flight at once: kept in
-      // registers through a chain they would be spilled, and the compiler
-      // reloads spilled registers one memory round trip at a time.
+      // The first block's chunks wait in this work item's staging area (8
+      // coalesced 16-byte stores per thread) while the later chains run, and
+      // come back with all 8 loads in flight at once; the second block's stay
+      // in registers.  Two blocks' chunks kept in registers through a chain
+      // are spilled, and the compiler reloads spilled registers one memory
+      // round trip at a time.
 #pragma unroll
       for (int kb = 0; kb < 3; ++kb) {
         if (kb > 0) __syncthreads();
@@ -323,17 +324,15 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
         uint32_t nw[4];
         run_chain<L>(acc, cb, lds, src, [](int i) { return i; }, nw);
         out_chunks<L>(acc, nw, cb, v[kb]);
-        if (kb < 2) {
+        if (kb == 0) {
 #pragma unroll
           for (int k = 0; k < 8; ++k)
-            __builtin_amdgcn_raw_buffer_store_b128(v[kb][k], stage_r, ((kb * 8 + k) * kThreads + threadIdx.x) * 16, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(v[0][k], stage_r, (k * kThreads + threadIdx.x) * 16, 0, 0);
         }
       }
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          v[kb][k] = __builtin_amdgcn_raw_buffer_load_b128(stage_r, ((kb * 8 + k) * kThreads + threadIdx.x) * 16, 0, 0);
+      for (int k = 0; k < 8; ++k)
+        v[0][k] = __builtin_amdgcn_raw_buffer_load_b128(stage_r, (k * kThreads + threadIdx.x) * 16, 0, 0);
     } else if (KB == 2 && two) {  // both blocks at once (uniform across the workgroup)
       const Ctx c[2] = {make_ctx(seed32, b_first), make_ctx(seed32, b_first + 1)};
       u32x4 src[kTiles][2];

@@ -438,10 +438,10 @@ def test_linear_workspace_three_block_tiles():
     # k-major table (96 k steps x (4 x 32 + 1) 16-byte slots) exceeds the 160 KiB LDS; the LDS
     # holds the first 76 steps (79 fit, in whole rounds of 4) and every work item (24 row tiles x
     # 256 // 24 = 10 token splits) keeps the other 20 steps' W tiles, 2 row tiles x 1 KiB each,
-    # and a staging area for two blocks' generated chunks (8 x 16 bytes per thread of 512)
+    # and a staging area for one block's generated chunks (8 x 16 bytes per thread of 512)
     lib = N.lib()
     assert (160 * 1024 // 16) // (4 * 32 + 1) // 4 * 4 == 76
-    overflow = 24 * 10 * ((96 - 76) * 2 * 1024 + 2 * 8 * 512 * 16)
+    overflow = 24 * 10 * ((96 - 76) * 2 * 1024 + 8 * 512 * 16)
     tiled_x = (4096 // 16) * 96 * 1024
     assert lib.lwl_bfht_linear_forward_workspace_size(4096, 3072, 768, 32768) == overflow + tiled_x
     # below 3072 tokens: two-block tiles (36 for 72 blocks), whose straddling rows keep two
