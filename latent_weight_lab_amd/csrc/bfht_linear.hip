@@ -303,32 +303,37 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     u32x4 v[KB][8];
     const bool two = kRowTiles ? g1 > ((b_first + 1) << kLog) : (KB == 2 && tile * KB + 1 < nblocks);
     if constexpr (KB == 3) {
-      // one block at a time (each chain reuses the LDS once every wave has
-      // read the previous one's last exchange; the pair chain, whose peak
-      // register use leaves no room for a third block's chunks, is slower
-      // here than two single chains); the last tile of a matrix may generate
-      // blocks past its end, whose positions are dropped
-      // The first block's chunks wait in this work item's staging area (8
-      // coalesced 16-byte stores per thread) while the later chains run, and
-      // come back with all 8 loads in flight at once; the second block's stay
-      // in registers.  Two blocks' chunks kept in registers through a chain
-      // are spilled, and the compiler reloads spilled registers one memory
-      // round trip at a time.
-#pragma unroll
-      for (int kb = 0; kb < 3; ++kb) {
-        if (kb > 0) __syncthreads();
-        const Ctx cb = make_ctx(seed32, b_first + kb);
+      // The first block alone, then the other two together (`run_chain2`;
+      // each chain reuses the LDS once every wave has read the previous one's
+      // last exchange).  The first block's chunks wait in this work item's
+      // staging area (8 coalesced 16-byte stores per thread) while the pair
+      // runs, and come back with all 8 loads in flight at once: kept in
+      // registers through the pair chain they would be spilled, and the
+      // compiler reloads spilled registers one memory round trip at a time.
+      // The last tile of a matrix may generate blocks past its end, whose
+      // positions are dropped.
+      {
+        const Ctx c0 = make_ctx(seed32, b_first);
         u32x4 src[kTiles][2];
-        load_latent(cb, latent, n, src);
+        load_latent(c0, latent, n, src);
         f32x16 acc[kTiles];
         uint32_t nw[4];
-        run_chain<L>(acc, cb, lds, src, [](int i) { return i; }, nw);
-        out_chunks<L>(acc, nw, cb, v[kb]);
-        if (kb == 0) {
+        run_chain<L>(acc, c0, lds, src, [](int i) { return i; }, nw);
+        out_chunks<L>(acc, nw, c0, v[0]);
 #pragma unroll
-          for (int k = 0; k < 8; ++k)
-            __builtin_amdgcn_raw_buffer_store_b128(v[0][k], stage_r, (k * kThreads + threadIdx.x) * 16, 0, 0);
-        }
+        for (int k = 0; k < 8; ++k)
+          __builtin_amdgcn_raw_buffer_store_b128(v[0][k], stage_r, (k * kThreads + threadIdx.x) * 16, 0, 0);
+      }
+      __syncthreads();
+      {
+        const Ctx c[2] = {make_ctx(seed32, b_first + 1), make_ctx(seed32, b_first + 2)};
+        u32x4 src[kTiles][2];
+        load_latent(c[0], latent, n, src);
+        f32x16 acc[2][kTiles];
+        uint32_t nw[2][4];
+        run_chain2<L>(acc, c, lds, src, [](int i) { return i; }, nw);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) out_chunks<L>(acc[kb], nw[kb], c[kb], v[kb + 1]);
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k)
