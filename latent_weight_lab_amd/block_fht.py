@@ -95,22 +95,25 @@ def block_fht_grad_latent(latent: torch.Tensor, grad_out: torch.Tensor, size: in
 
 
 def block_fht_linear_forward(input: torch.Tensor, latent: torch.Tensor, out_features: int, layers: int, seed: int,
-                             weight_scale: float = 1.0, fused: bool = True) -> torch.Tensor:
+                             weight_scale: float = 1.0, fused: bool | None = None) -> torch.Tensor:
     """``input @ (weight_scale * W)^T`` with ``W = BlockFHT(latent)[: in*out].view(out, in)``
     (reference ``block_fht.py:251-288``).
 
-    With ``fused=True`` (default) shapes a fused kernel takes — the reference's own domain
-    (float32 / float16 / bfloat16 latents of block <= 2^14 with ``block % in_features ==
-    0``), and bf16 latents of block 2^15 with ``in_features % 8 == 0`` in 528..5120 — generate
-    W on chip for every token range and contract it there, so only the latent and the
-    activations live in HBM.  Other shapes, or ``fused=False``, generate W once into a
-    transient buffer (one launch, ``weight_scale`` folded in) and call ``F.linear`` — the
-    reference's fallback (``:282-288``).  For one GPT-2 matrix at a time that second route
-    is the faster one on MI355X (it costs the transient W, ~1 µs of HBM traffic per
-    matrix); at decode batch sizes ``forward_fused_grouped`` runs many matrices' fused
-    kernels together and beats both.  Both routes are differentiable in the input and
-    the latent, as the reference's fallback is: the fused one through ``_FusedLinearFn``
-    (W regenerated in the backward), the other through ``block_fht_slice``.
+    Two routes.  The fused one, for shapes a fused kernel takes — the reference's own
+    domain (float32 / float16 / bfloat16 latents of block <= 2^14 with ``block %
+    in_features == 0``), and bf16 latents of block 2^15 with ``in_features % 8 == 0`` in
+    528..5120 — generates W on chip for every token range and contracts it there, so only
+    the latent and the activations live in HBM.  The other generates W once into a
+    transient buffer (one launch, ``weight_scale`` folded in) and calls ``F.linear`` — the
+    reference's fallback (``:282-288``), which the reference also takes at every block-2^15
+    shape.  ``fused=True`` takes the fused route wherever a kernel takes the shape,
+    ``fused=False`` never; the default (None) takes it where it is also the faster one:
+    small batches (``ops.linear_fused_preferred``: below 128 tokens on the block-2^15
+    kernel, below 8 in the reference's domain).  At decode batch sizes
+    ``forward_fused_grouped`` runs many matrices' fused kernels together.  Both routes are
+    differentiable in the input and the latent, as the reference's fallback is: the fused
+    one through ``_FusedLinearFn`` (W regenerated in the backward), the other through
+    ``block_fht_slice``.
     """
     return _generated_linear(input, latent, out_features, layers, seed, weight_scale, None, fused)
 
@@ -124,7 +127,9 @@ def _generated_linear(input, latent, out_features, layers, seed, weight_scale, b
     flat = input.reshape(-1, in_features)
     _native.require_cuda(flat, latent)
     size = in_features * out_features
-    if fused and ops.linear_supported(in_features, out_features, latent, flat):
+    use_fused = (ops.linear_fused_preferred(in_features, out_features, latent, flat) if fused is None
+                 else bool(fused) and ops.linear_supported(in_features, out_features, latent, flat))
+    if use_fused:
         if torch.is_grad_enabled() and (latent.requires_grad or flat.requires_grad):
             out = _FusedLinearFn.apply(flat, latent, out_features, int(layers), int(seed), float(weight_scale))
         else:
@@ -363,12 +368,14 @@ class BlockFHTLinear(nn.Module):
                                        self.fused_latent_grad)
 
     def forward_fused(self, input: torch.Tensor, weight_scale: float = 1.0) -> torch.Tensor:
-        """Inference forward (reference ``block_fht.py:482-501``).  Where a fused kernel takes
-        the shape and no gradient is recorded: one fused launch whose stores also add the
-        modulation term, the residual base and the bias (``lwl_bfht_linear_forward_ex``; W
-        never stored, one rounding to the output dtype instead of one per term).  Recording
-        gradients: the fused (or generated) linear with the reference's sequence of terms
-        after it, the bias in the GEMM's epilogue when nothing comes between."""
+        """Inference forward (reference ``block_fht.py:482-501``).  Where the default route
+        of ``block_fht_linear_forward`` is the fused kernel (it takes the shape and the
+        batch is small, ``ops.linear_fused_preferred``) and no gradient is recorded: one
+        fused launch whose stores also add the modulation term, the residual base and the
+        bias (``lwl_bfht_linear_forward_ex``; W never stored, one rounding to the output
+        dtype instead of one per term).  Otherwise: that route's linear (fused or W
+        generated once) with the reference's sequence of terms after it, the bias in the
+        GEMM's epilogue when nothing comes between."""
         if self.output_gain is not None or self.input_gain is not None or self.spectral_core is not None:
             return F.linear(input, self.weight.to(dtype=input.dtype), self.bias)
         g = self.generator
@@ -379,7 +386,7 @@ class BlockFHTLinear(nn.Module):
             return ops.linear_forward(flat, *args, **kwargs).reshape(*input.shape[:-1], self.out_features)
         if self.modulation_alpha == 0.0 and self.residual_base_weight is None:
             # the bias rides in the GEMM's epilogue
-            return _generated_linear(input, g.latent, self.out_features, g.layers, g.seed, scale, self.bias, True)
+            return _generated_linear(input, g.latent, self.out_features, g.layers, g.seed, scale, self.bias, None)
         out = block_fht_linear_forward(input, g.latent, self.out_features, g.layers, g.seed, weight_scale=scale)
         if self.modulation_alpha != 0.0:
             modulation = self.modulation_alpha * self._modulation_offset()
@@ -406,7 +413,7 @@ class BlockFHTLinear(nn.Module):
         if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (g.latent, input, bias)):
             return None
         flat = input.reshape(-1, self.in_features)
-        if not ops.linear_supported(self.in_features, self.out_features, g.latent, flat):
+        if not ops.linear_fused_preferred(self.in_features, self.out_features, g.latent, flat):
             return None
         if bias is not None and bias.dtype != flat.dtype:
             return None

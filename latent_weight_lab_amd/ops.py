@@ -73,6 +73,27 @@ def linear_supported(in_features: int, out_features: int, latent: torch.Tensor, 
                                                  in_features, latent.numel(), out_features, 1) == N.LWL_OK
 
 
+# Batches from these sizes on run faster as W generated once plus a GEMM than through the
+# fused kernels (MI355X, graph-replayed calls): the bf16 block-2^15 kernel at GPT-2 shapes
+# 12.5-20.8 against 14.8-18.5 us at 128 tokens and 1.1-1.8x slower from 256; the reference
+# domain (1024 -> 4096, latent 16384) 12.5-12.9 against 17.7-23.5 us at one token, about even
+# at 8, slower from 32.
+FUSED_MAX_TOKENS_MFMA15 = 128
+FUSED_MAX_TOKENS_SMALL = 8
+
+
+def linear_fused_preferred(in_features: int, out_features: int, latent: torch.Tensor, x: torch.Tensor) -> bool:
+    """Whether the default route of the linear forward takes the fused kernel: it takes
+    the shape and the batch is below the size from which generating W once and calling a
+    GEMM is faster (the fused kernels then pay for regenerating W per token range and,
+    from 256 tokens, for a re-laid-out copy of x that outweighs the transient W)."""
+    if not linear_supported(in_features, out_features, latent, x):
+        return False
+    tokens = x.numel() // max(1, in_features)
+    mfma15 = latent.dtype == torch.bfloat16 and next_power_of_two(latent.numel()) == 32768
+    return tokens < (FUSED_MAX_TOKENS_MFMA15 if mfma15 else FUSED_MAX_TOKENS_SMALL)
+
+
 def _epilogue(tokens: int, out_features: int, dtype: torch.dtype, dev, bias=None, base=None,
               row_sum_coef=None, row_sum_scale: float = 1.0):
     """The ``lwl_bfht_linear_epilogue`` of the given terms (None: no epilogue) and the

@@ -92,6 +92,36 @@ def test_fused_linear_3d_input_and_module():
     assert O.rel_l2(fused.double().cpu().numpy(), dense.double().cpu().numpy()) < 1e-2
 
 
+@pytest.mark.parametrize("dtype,n,in_f,out_f,layers,small,large", [
+    (torch.bfloat16, 32768, 768, 3072, 3, 127, 128),   # block-2^15 kernel: fused below 128 tokens
+    (torch.float16, 16384, 1024, 4096, 2, 7, 8),        # the reference's domain: fused below 8
+])
+def test_default_route_by_batch(dtype, n, in_f, out_f, layers, small, large):
+    # the default route is the fused kernel for small batches and W generated once + GEMM from
+    # the crossover on, bit for bit the same as asking for that route; forward_fused follows it
+    g = torch.Generator().manual_seed(12)
+    latent = torch.randn(n, generator=g).to(dtype).cuda()
+    lin = BlockFHTLinear(in_f, out_f, bias=True, latent_dim=n, layers=layers, seed=6).cuda().to(dtype)
+    with torch.no_grad():
+        lin.generator.latent.copy_(latent)
+        lin.bias.normal_()
+    for tokens, fused in ((small, True), (large, False)):
+        x = torch.randn(tokens, in_f, generator=g).to(dtype).cuda()
+        assert ops.linear_supported(in_f, out_f, latent, x)
+        assert ops.linear_fused_preferred(in_f, out_f, latent, x) == fused
+        with torch.no_grad():
+            auto = block_fht_linear_forward(x, latent, out_f, layers, 6)
+            want = block_fht_linear_forward(x, latent, out_f, layers, 6, fused=fused)
+            assert torch.equal(auto, want), (tokens, fused)
+            mod = lin.forward_fused(x)
+            if fused:
+                ref = ops.linear_forward(x, latent, out_f, layers, 6, 1.0, bias=lin.bias)
+            else:
+                w = block_fht_slice(latent, in_f * out_f, layers, 6, 0, in_f * out_f).view(out_f, in_f)
+                ref = torch.nn.functional.linear(x, w, lin.bias)
+            assert torch.equal(mod, ref), (tokens, fused)
+
+
 def test_generate_route_bitwise():
     # generate + GEMM: W equals the slice forward times weight_scale, rounded as the
     # reference's fallback (bf16 * scale in bf16), and the product is F.linear's

@@ -94,8 +94,8 @@ def test_reference_domain_through_shim(ext, dtype, tokens, in_f, out_f, n, layer
     assert got.shape == (tokens, out_f) and got.dtype == dtype
     want = oracle_out(x, latent, out_f, layers, seed, scale)
     assert O.rel_l2(got.double().cpu().numpy(), want) < TOL[dtype]
-    # the package's route is the same kernel
-    pkg = block_fht_linear_forward(xd, ld, out_f, layers, seed, weight_scale=scale)
+    # the package's fused route is the same kernel
+    pkg = block_fht_linear_forward(xd, ld, out_f, layers, seed, weight_scale=scale, fused=True)
     assert torch.equal(pkg, got)
 
 
