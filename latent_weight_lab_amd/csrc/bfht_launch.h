@@ -144,9 +144,12 @@ hipError_t launch_linear_small(const LinearArgs& a, hipStream_t s);
 // The same domain at batches of kLinearMmMinTokens and more, contracted on the
 // matrix cores (bfht_linear_small_mm.hip): blocks of 2^5 .. 2^14, in_features a
 // multiple of 32 (16-bit I/O) or 16 (float32) with at least 16 rows per
-// 32768-weight (16384 for float32) workgroup tile.
+// 32768-weight (16384 for float32) workgroup tile.  From 16 tokens: the VALU
+// kernel's contraction costs ~1.1 us per token (1024 -> 4096, latent 16384:
+// 18.4-22.1 us at 8 tokens, 27.2-34.2 at 16), the matrix-core one's call is
+// flat (24.7-31.7 us from 8 to 64 tokens).
 constexpr int kLinearMmMinLog = 5;
-constexpr int64_t kLinearMmMinTokens = 64;
+constexpr int64_t kLinearMmMinTokens = 16;
 bool linear_small_mm_applicable(const LinearArgs& a);  // needs dtype, log_block, in/out features, tokens
 int linear_small_mm_token_splits(const LinearArgs& a);
 // From 256 tokens its workspace holds x re-laid out (launch_tile_x); else none.

@@ -1,7 +1,7 @@
 // Fused BlockFHTLinear forward for the reference extension's own domain
 // (float32 / float16 / bfloat16, block B <= 2^14, B % in_features == 0;
 // reference gate latent_weight_lab/block_fht.py:263-273, kernel
-// csrc/block_fht_ext_cuda.cu:225-329) at batches of 64 tokens and more, with
+// csrc/block_fht_ext_cuda.cu:225-329) at batches of 16 tokens and more, with
 // the contraction on the matrix cores.  From 256 tokens x is first re-laid out
 // in MFMA operand order (launch_tile_x: one 1 KiB load per 16 tokens and step
 // instead of 16 rows x 64 bytes).

@@ -62,13 +62,15 @@ CASES = [
     (12, 8, 6, 32, 1, 7, 1.0),         # batched 3 x 4 tokens
     (1, 1024, 4096, 16384, 2, 123, 0.5),  # reference profiling case (scripts/profile_fused_once.py)
     (300, 1024, 4096, 16384, 2, 123, 0.5),  # the same with a batch: token splits
-    (37, 64, 200, 4096, 3, -3, 1.0),   # 64 rows per block, partial last block (200 rows)
+    (37, 64, 200, 4096, 3, -3, 1.0),   # 64 rows per block, partial last block (200 rows); matrix cores
+    (13, 64, 200, 4096, 3, -3, 1.0),   # the same on VALU: a single-token last quad, teams' second rows past the tile
+    (12, 2048, 40, 16384, 3, 7, 1.0),  # x of a quad staged in two rounds of loads, three quads
     (130, 16384, 5, 16384, 1, 11, 2.0),  # one row per block
     (9, 1, 7, 1, 3, 4, 1.0),           # block 2^0
     (70, 2, 300, 3, 2, 5, 1.0),        # block 2^2: 256 blocks per workgroup
     (1000, 32, 2000, 500, 3, 6, 0.75),  # block 2^9 (16 rows of 32), 16 blocks per workgroup
     (3, 4096, 3, 8000, 2, 12, 1.0),    # block 2^13, out smaller than one block
-    # from 64 tokens the contraction runs on the matrix cores (bfht_linear_small_mm) where
+    # from 16 tokens the contraction runs on the matrix cores (bfht_linear_small_mm) where
     # in_features is a multiple of 32 (16 for float32) with >= 16 rows per workgroup tile
     (256, 64, 200, 4096, 3, -3, 1.0),   # block 2^12: 200 of 512 table rows, 13 row tiles
     (100, 256, 1000, 2000, 2, 5, 1.0),  # block 2^11, ragged token tiles
