@@ -85,12 +85,16 @@ def test_graph_fused_linear():
     lat_ref = torch.randn(16384, device="cuda", generator=g).to(torch.float16)
     xr = torch.randn(300, 1024, device="cuda", generator=g).to(torch.float16)
     xr5 = torch.randn(5, 1024, device="cuda", generator=g).to(torch.float16)
+    x3k = torch.randn(3100, 3072, device="cuda", generator=g).to(torch.bfloat16)
+    bias768 = torch.randn(768, device="cuda", generator=g).to(torch.bfloat16)
 
     def fn():
         return [ops.linear_forward(x64, lat, 3072, 3, 3, 1.0),
                 ops.linear_forward(x300, lat, 3072, 3, 3, 1.0, bias=bias, row_sum_coef=coef),  # tiled x, epilogue
                 ops.linear_forward(xr, lat_ref, 4096, 2, 123, 0.5),   # reference domain, matrix cores
-                ops.linear_forward(xr5, lat_ref, 4096, 2, 123, 0.5)]  # reference domain, VALU
+                ops.linear_forward(xr5, lat_ref, 4096, 2, 123, 0.5),  # reference domain, VALU
+                # three-block tiles: overflow W tiles and a staged block round-trip through the workspace
+                ops.linear_forward(x3k, lat, 700, 3, 3, 0.5, bias=bias768[:700])]
 
     check_graph(fn)
 

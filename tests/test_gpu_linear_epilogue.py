@@ -35,6 +35,7 @@ CASES = [
     (torch.bfloat16, 64, 768, 3072, 32768, 3, 3, 1.0),     # matrix cores, untiled, straddling rows
     (torch.bfloat16, 4096, 768, 3072, 32768, 3, 3, 1.0),   # tiled x, two blocks per workgroup (NT 6)
     (torch.bfloat16, 300, 3072, 768, 32768, 3, 4, 0.5),    # tiled, 3072 -> 768
+    (torch.bfloat16, 3100, 3072, 700, 32768, 3, 4, 0.5),   # three-block tiles, last tile 28 rows
     (torch.bfloat16, 17, 528, 200, 30000, 2, 5, 2.0),      # ragged tokens, one partial block
     (torch.float32, 300, 1024, 4096, 16384, 2, 123, 0.5),  # reference domain
     (torch.float16, 37, 64, 200, 4096, 3, -3, 1.0),
