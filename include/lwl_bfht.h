@@ -153,7 +153,7 @@ int lwl_bfht_backward_noalloc(const void* grad_out, int dtype, int64_t latent_si
  * The workspace query has no dtype (as ext.linear_forward has none) and
  * returns the most any dtype needs for the shape: the block-2^15 kernel's
  * partial rows of the rows that straddle its tiles (none where tiles hold whole
- * rows: from 256 tokens, rows of 768 are tiled 64 at a time; from 3072 tokens,
+ * rows: from 256 tokens, rows of 768 are tiled 64 at a time; from 2048 tokens,
  * rows of 3072 are tiled 32 at a time, three blocks, and each work item keeps
  * the W tiles its LDS cannot hold and one staged block instead, 104 KiB) and,
  * from 256 tokens, a copy of x in MFMA order (in the reference's domain only

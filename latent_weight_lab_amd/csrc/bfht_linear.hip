@@ -179,11 +179,12 @@ int linear_three_block_rows(int64_t in_features) {
 }
 
 // Batches from this many tokens use three-block tiles where they apply: a
-// workgroup's three chains, the staging round trip and the scatter take ~29 us
-// against the pair chain's ~13, and the contraction streams a third less x
-// (3072 -> 768: 57.7 / 52.5 us at 2048 tokens, 71.5 / 77.0 at 4096, 190 / 237
-// at 16384, three / two blocks).
-constexpr int64_t kThreeBlockMinTokens = 3072;
+// workgroup's generation (one chain, the staging round trip, the pair chain,
+// the scatter) takes ~22 us against the pair chain's ~13, and the contraction
+// streams a third less x (3072 -> 768, three / two blocks: 48.8 / 43.1 us at
+// 1536 tokens, 51.5 / 52.8 at 2048, 51.7 / 57.8 at 2560, 66.0 / 77.0 at 4096,
+// 189 / 237 at 16384).
+constexpr int64_t kThreeBlockMinTokens = 2048;
 
 size_t partial_bytes(const LinearArgs& a) {
   if (a.blocks_per_wg == 3) {  // every work item's overflow W tiles and staging area

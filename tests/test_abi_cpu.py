@@ -218,7 +218,7 @@ def test_linear_workspace_size():
     # one pair of float32 partial rows (first / last row of the tile) per workgroup tile of generated
     # blocks and token, then, from 256 tokens, x re-laid out in 16-token x 32-k tiles of 1 KiB
     # (zero-padded).  From 256 tokens a tile is two blocks when one block holds at most 64 rows and
-    # two fit in the LDS (here: 1000 in_features, 67 rows at an exact pitch; 3072 below 3072
+    # two fit in the LDS (here: 1000 in_features, 67 rows at an exact pitch; 3072 below 2048
     # tokens, test_linear_workspace_three_block_tiles); otherwise, and below, one block.  Rows of
     # 768 take tiles of 64 whole rows instead (1.5 blocks): no row straddles two tiles, so no
     # partial rows, only the x copy.
@@ -434,7 +434,7 @@ def test_linear_jobs_validation():
 
 
 def test_linear_workspace_three_block_tiles():
-    # rows of 3072 from 3072 tokens on (tiled x): tiles of three blocks = 32 whole rows, whose
+    # rows of 3072 from 2048 tokens on (tiled x): tiles of three blocks = 32 whole rows, whose
     # k-major table (96 k steps x (4 x 32 + 1) 16-byte slots) exceeds the 160 KiB LDS; the LDS
     # holds the first 76 steps (79 fit, in whole rounds of 4) and every work item (24 row tiles x
     # 256 // 24 = 10 token splits) keeps the other 20 steps' W tiles, 2 row tiles x 1 KiB each,
@@ -444,10 +444,10 @@ def test_linear_workspace_three_block_tiles():
     overflow = 24 * 10 * ((96 - 76) * 2 * 1024 + 8 * 512 * 16)
     tiled_x = (4096 // 16) * 96 * 1024
     assert lib.lwl_bfht_linear_forward_workspace_size(4096, 3072, 768, 32768) == overflow + tiled_x
-    # below 3072 tokens: two-block tiles (36 for 72 blocks), whose straddling rows keep two
+    # below 2048 tokens: two-block tiles (36 for 72 blocks), whose straddling rows keep two
     # float32 partial sums per token, 256-byte aligned
-    partial = (36 * 2 * 3071 * 4 + 255) // 256 * 256
-    assert lib.lwl_bfht_linear_forward_workspace_size(3071, 3072, 768, 32768) == partial + 192 * 96 * 1024
+    partial = (36 * 2 * 2047 * 4 + 255) // 256 * 256
+    assert lib.lwl_bfht_linear_forward_workspace_size(2047, 3072, 768, 32768) == partial + 128 * 96 * 1024
 
 
 def test_linear_job_and_epilogue_structs_match_header():

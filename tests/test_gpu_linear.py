@@ -53,12 +53,12 @@ def oracle_linear(x: torch.Tensor, latent: torch.Tensor, out_f: int, layers: int
         (300, 768, 1000, 32768, 2, 39, 1.0),    # 16 row tiles, the last of 40 rows; ragged token tiles
         (513, 768, 2304, 32768, 3, 40, 0.5),    # GPT-2 qkv at a prefill batch: 36 tiles, one-token last tile
         (256, 768, 768, 20000, 1, 41, 1.0),     # GPT-2 proj, padded latent (last generated block partial)
-        # rows of 3072 from 3072 tokens: tiles of three whole blocks (32 rows), the last 20 k steps'
+        # rows of 3072 from 2048 tokens: tiles of three whole blocks (32 rows), the last 20 k steps'
         # W tiles read from the workgroup's overflow in global memory
-        (3072, 3072, 700, 32768, 2, 42, 0.5),   # the smallest such batch; last tile 28 rows, its third block partial
+        (2048, 3072, 700, 32768, 2, 42, 0.5),   # the smallest such batch; last tile 28 rows, its third block partial
         (3100, 3072, 40, 20000, 1, 43, 1.0),    # one layer, padded latent, ragged token tiles, last tile 8 rows
         (5000, 3072, 96, 32768, 3, 44, 1.0),    # three whole tiles, two rounds of token tiles
-        (3071, 3072, 96, 32768, 3, 44, 1.0),    # just below it: two-block tiles with straddling rows
+        (2047, 3072, 96, 32768, 3, 44, 1.0),    # just below it: two-block tiles with straddling rows
     ],
 )
 def test_fused_linear_matches_oracle(tokens, in_f, out_f, n, layers, seed, scale):
