@@ -92,8 +92,10 @@ lwl::BfhtArgs plan(int dtype, int64_t latent_size, int64_t layers, int64_t seed,
 }
 
 size_t forward_ws(const lwl::BfhtArgs& a) {
+  // the tile passes' float32 work buffer, for one group of blocks at a time
   if (a.log_block <= lwl::kWholeBlockMaxLog || a.nblocks == 0) return 0;
-  return align_up((size_t)a.nblocks * ((size_t)1 << a.log_block) * sizeof(float));
+  const int64_t blocks = std::min<int64_t>(a.nblocks, lwl::tile_group_blocks(a.log_block));
+  return align_up((size_t)blocks * ((size_t)1 << a.log_block) * sizeof(float));
 }
 
 size_t backward_ws(const lwl::BfhtArgs& a) {

@@ -784,6 +784,29 @@ static unsigned tile_grid(int64_t ntiles) {
 }
 
 template <class T>
+static hipError_t run_tiles(const BfhtArgs& a, hipStream_t s, bool fwd);
+
+// Forward: the passes over one group of blocks after another (tile_group_blocks),
+// each group a slice of the call's range, in the same work buffer.
+template <class T>
+static hipError_t run_tiles_grouped(const BfhtArgs& a, hipStream_t s) {
+  const int64_t per = tile_group_blocks(a.log_block);
+  if (a.nblocks <= per) return run_tiles<T>(a, s, true);
+  const int64_t B = (int64_t)1 << a.log_block;
+  for (int64_t b0 = 0; b0 < a.nblocks; b0 += per) {
+    BfhtArgs g = a;
+    g.first_block = a.first_block + b0;
+    g.nblocks = std::min<int64_t>(per, a.nblocks - b0);
+    g.start = std::max<int64_t>(a.start, g.first_block * B);
+    g.stop = std::min<int64_t>(a.stop, (g.first_block + g.nblocks) * B);
+    g.dst = static_cast<T*>(a.dst) + (g.start - a.start);
+    const hipError_t e = run_tiles<T>(g, s, true);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+template <class T>
 static hipError_t run_tiles(const BfhtArgs& a, hipStream_t s, bool fwd) {
   const int64_t tiles_per_block = (int64_t)1 << (a.log_block - kTileLog);
   const unsigned grid = tile_grid(a.nblocks * tiles_per_block);
@@ -829,7 +852,7 @@ static hipError_t run_typed(const BfhtArgs& a, hipStream_t s, bool fwd) {
   }
   if (a.log_block <= kTileLog)
     return dispatch_block<T>(a.log_block, fwd, a, s, std::make_integer_sequence<int, kTileLog + 1>{});
-  return run_tiles<T>(a, s, fwd);
+  return fwd ? run_tiles_grouped<T>(a, s) : run_tiles<T>(a, s, false);
 }
 
 hipError_t launch_reduce_grouped(const GroupTable& g, int dtype, bool part_bf16, hipStream_t s) {

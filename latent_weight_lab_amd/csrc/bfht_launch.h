@@ -14,6 +14,19 @@ enum { kF32 = 0, kF16 = 1, kBF16 = 2 };
 // through the float32 work buffer in tile passes.
 constexpr int kWholeBlockMaxLog = 15;
 
+// The tile-pass forward runs its passes over groups of blocks whose work
+// buffer is at most 128 MiB (at least one block): a group's passes then find
+// more of the buffer in the 256 MB last-level cache (config 3, 2^26
+// coordinates in two groups, same box: 0.421 -> 0.397-0.403 ms at 2^23
+// blocks, 2^20 unchanged within the spread), the workspace halves, and
+// quarter-size groups leave too few tiles per CU (0.42 / 0.44 ms).  The
+// backward, whose last pass sums across blocks, does not gain and is not split.
+constexpr int64_t kTileGroupBytes = (int64_t)128 << 20;
+inline int64_t tile_group_blocks(int log_block) {
+  const int64_t b = kTileGroupBytes >> (log_block + 2);
+  return b > 0 ? b : 1;
+}
+
 // tile-pass prologues / epilogues
 enum { kSrcLatent = 0, kSrcGrad = 1, kSrcWork = 2 };
 enum { kDstWork = 0, kDstOut = 1, kDstSum = 2 };

@@ -85,7 +85,10 @@ def test_forward_rejects_missing_workspace_without_launching():
 def test_workspace_sizes():
     lib = N.lib()
     assert lib.lwl_bfht_forward_workspace_size(32768, 8 << 20, 0, 8 << 20) == 0
-    assert lib.lwl_bfht_forward_workspace_size(1 << 20, 1 << 26, 0, 1 << 26) == 64 * (1 << 20) * 4
+    # the tile-pass forward works through groups of blocks of at most 128 MiB of float32
+    assert lib.lwl_bfht_forward_workspace_size(1 << 20, 1 << 26, 0, 1 << 26) == 32 * (1 << 20) * 4
+    assert lib.lwl_bfht_forward_workspace_size(1 << 23, 1 << 26, 0, 1 << 26) == 4 * (1 << 23) * 4
+    assert lib.lwl_bfht_forward_workspace_size(1 << 16, 1 << 20, 0, 1 << 20) == 16 * (1 << 16) * 4
     # slice [12345, 1012345) of B=2^20 touches blocks 0..0
     assert lib.lwl_bfht_forward_workspace_size(1 << 20, 1 << 26, 12345, 1_012_345) == (1 << 20) * 4
     # backward whole-block sizes: one float32 partial row of latent_size per overlapped block,

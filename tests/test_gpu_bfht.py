@@ -281,6 +281,16 @@ def test_config3_multipass(log_block):
     for s0, s1 in [(2 * B - 777, 2 * B + 4321), (size - B, size)]:
         want = c_oracle.forward(lat.double().numpy(), size, 3, 99, s0, s1)
         assert rel_l2(to_np(y[s0:s1]), want) < 1e-5
+    # the forward runs its passes over groups of blocks of at most 128 MiB of float32 work
+    # (32 blocks of 2^20, 4 of 2^23): a slice over more than one group, partial at both ends,
+    # equals the full call bit for bit, and the oracle around its ends and the group boundary
+    per = (128 << 20) // (4 * B)
+    s0, s1 = 12345, (per + 2) * B + 999
+    ys = ops.forward(latent, size, 3, 99, s0, s1)
+    assert torch.equal(ys, y[s0:s1])
+    for w0, w1 in [(s0, s0 + 3000), (per * B - 1500, per * B + 1500), (s1 - 3000, s1)]:
+        want = c_oracle.forward(lat.double().numpy(), size, 3, 99, w0, w1)
+        assert rel_l2(to_np(ys[w0 - s0:w1 - s0]), want) < 1e-5
     # adjointness <T x, g> = <x, T^T g> over the full size (fp64 dot products)
     g = torch.randn(size, generator=torch.Generator().manual_seed(3)).cuda()
     gl = ops.backward(g, B, torch.float32, size, 3, 99, 0, size)
