@@ -134,7 +134,9 @@ int lwl_bfht_backward_noalloc(const void* grad_out, int dtype, int64_t latent_si
  * with y generated from `latent` over size = in_features * out_features.
  * input is row-major [tokens, in_features], out row-major [tokens, out_features],
  * both `dtype`, as the latent.  W is generated on chip, block by block, and
- * never written to memory.  Unlike the reference (.cu:639-642) any in_features
+ * contracted there; only the three-block tiles of in_features 3072 from 2048
+ * tokens park part of each workgroup's tile in the workspace (the k steps its
+ * LDS cannot hold, one staged block).  Unlike the reference (.cu:639-642) any in_features
  * <= B works (rows may straddle blocks; partial rows are summed in a fixed
  * order through the workspace).  B <= 2^15.
  *

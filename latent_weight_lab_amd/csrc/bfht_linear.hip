@@ -1,5 +1,6 @@
 // Fused BlockFHTLinear forward: out = weight_scale * x @ W^T with W generated
-// on chip, block by block, never written to memory.
+// on chip, block by block, and contracted there (three-block tiles, below, are
+// the exception: each workgroup parks part of its tiles in its own workspace).
 //
 // W[o, i] = y[o * in + i] where y is the BlockFHT output of the latent over
 // size = in * out (reference latent_weight_lab/block_fht.py:251-288).  One
