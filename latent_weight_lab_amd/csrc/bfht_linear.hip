@@ -384,7 +384,10 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
     }
     const Ctx c = make_ctx(seed32, b_first);  // chunk positions do not depend on the block
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
+    for (int kbi = 0; kbi < KB; ++kbi) {
+      // three-block tiles scatter the staged first block last, so its reloads
+      // arrive while the other two blocks' chunks go out
+      const int kb = KB == 3 ? (kbi + 1) % 3 : kbi;
       if (KB == 2 && kRowTiles && kb > 0 && !two) break;  // uniform: no second block
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
