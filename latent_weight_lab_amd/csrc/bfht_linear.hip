@@ -383,27 +383,67 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       }
     }
     const Ctx c = make_ctx(seed32, b_first);  // chunk positions do not depend on the block
+    if constexpr (KB == 3) {
+      // A lane's chunk k = i + G g sits at block position out_chunk_pos(0) + 8 i
+      // + GS g: G consecutive chunks per group.  Three-block tiles are whole rows
+      // (off = 0) of in_features % 128 == 0 positions and a group starts at a
+      // multiple of 8 G, so a group lies in one row and one k step (kc of its
+      // first chunk a multiple of G, and of 4 when G = 4): one row and one
+      // LDS-or-overflow choice per group, rows and columns advanced by adding
+      // GS's and the block length's quotient and remainder by in_features.
+      constexpr int G = L % 2 == 1 ? 2 : 4, GS = L % 2 == 1 ? 8192 : 2048, NG = 8 / G;
+      const int q_g = GS / in_f, m_g = GS - q_g * in_f;
+      const int q_b = kB / in_f, m_b = kB - q_b * in_f;
+      const int rel0 = off + out_chunk_pos<L>(c, 0);
+      int r0 = (int)((float)rel0 * inv_in);
+      r0 -= r0 * in_f > rel0;
+      r0 += (r0 + 1) * in_f <= rel0;
+      const int col0 = rel0 - r0 * in_f;
 #pragma unroll
-    for (int kbi = 0; kbi < KB; ++kbi) {
-      // three-block tiles scatter the staged first block last, so its reloads
-      // arrive while the other two blocks' chunks go out
-      const int kb = KB == 3 ? (kbi + 1) % 3 : kbi;
-      if (KB == 2 && kRowTiles && kb > 0 && !two) break;  // uniform: no second block
+      for (int kbi = 0; kbi < 3; ++kbi) {
+        // the staged first block last, so its reloads arrive while the other two
+        // blocks' chunks go out
+        const int kb = (kbi + 1) % 3;
+        int r = r0 + kb * q_b, col = col0 + kb * m_b;
+        if (kb == 2 && col >= 2 * in_f) { col -= in_f; ++r; }
+        if (col >= in_f) { col -= in_f; ++r; }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int rel = off + kb * kB + out_chunk_pos<L>(c, k);
-        int r = (int)((float)rel * inv_in);
-        r -= r * in_f > rel;
-        r += (r + 1) * in_f <= rel;
-        const int kc = (rel - r * in_f) >> 3;
-        // chunks of 8 positions lie wholly inside or outside [g0, g1) (all multiples of 8)
-        if (rel >= rel_lo && rel < rel_hi) {
-          if (KB != 3 || kc < 4 * lds_steps) {
-            table[table_slot(kc, r, pitch)] = v[kb][k];
-          } else {  // overflow: k step kc / 4, row tile r / 16, lane (r % 16) + 16 (kc % 4)
-            const int e = (((kc >> 2) - lds_steps) * NT + (r >> 4)) * 64 + (r & 15) + 16 * (kc & 3);
-            __builtin_amdgcn_raw_buffer_store_b128(v[kb][k], ovf_r, e * 16, 0, 0);
+        for (int g = 0; g < NG; ++g) {
+          if (g > 0) {
+            r += q_g;
+            col += m_g;
+            if (col >= in_f) { col -= in_f; ++r; }
           }
+          const int rel = rel0 + kb * kB + g * GS;
+          if (rel >= rel_lo && rel < rel_hi) {
+            const int kc = col >> 3;
+            if (kc < 4 * lds_steps) {
+              // odd chunks of a group: table_row's permuted row, one k chunk on
+              const int s0 = kc * pitch + r + (kc >> 2), s1 = s0 + pitch + table_row(1, r, pitch) - r;
+#pragma unroll
+              for (int i = 0; i < G; ++i) table[(i & 1 ? s1 : s0) + (i >> 1) * 2 * pitch] = v[kb][i + G * g];
+            } else {  // overflow: k step kc / 4, row tile r / 16, lane (r % 16) + 16 (kc % 4)
+              const int e = (((kc >> 2) - lds_steps) * NT + (r >> 4)) * 64 + (r & 15) + 16 * (kc & 3);
+#pragma unroll
+              for (int i = 0; i < G; ++i)
+                __builtin_amdgcn_raw_buffer_store_b128(v[kb][i + G * g], ovf_r, (e + 16 * i) * 16, 0, 0);
+            }
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        if (KB == 2 && kRowTiles && kb > 0 && !two) break;  // uniform: no second block
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int rel = off + kb * kB + out_chunk_pos<L>(c, k);
+          int r = (int)((float)rel * inv_in);
+          r -= r * in_f > rel;
+          r += (r + 1) * in_f <= rel;
+          const int kc = (rel - r * in_f) >> 3;
+          // chunks of 8 positions lie wholly inside or outside [g0, g1) (all multiples of 8)
+          if (rel >= rel_lo && rel < rel_hi) table[table_slot(kc, r, pitch)] = v[kb][k];
         }
       }
     }
