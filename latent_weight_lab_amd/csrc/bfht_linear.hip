@@ -383,14 +383,16 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       }
     }
     const Ctx c = make_ctx(seed32, b_first);  // chunk positions do not depend on the block
-    if constexpr (KB == 3) {
+    if (KB == 3 || in_f % 32 == 0) {
       // A lane's chunk k = i + G g sits at block position out_chunk_pos(0) + 8 i
-      // + GS g: G consecutive chunks per group.  Three-block tiles are whole rows
-      // (off = 0) of in_features % 128 == 0 positions and a group starts at a
-      // multiple of 8 G, so a group lies in one row and one k step (kc of its
-      // first chunk a multiple of G, and of 4 when G = 4): one row and one
-      // LDS-or-overflow choice per group, rows and columns advanced by adding
-      // GS's and the block length's quotient and remainder by in_features.
+      // + GS g: G consecutive chunks per group.  With in_features % 32 == 0 the
+      // tile's start in its first row, its end, the block starts and so every
+      // group start are multiples of 8 G positions from a row start (three-block
+      // tiles: in_features % 128 == 0), so a group lies in one row, one k step
+      // and one side of the tile's edges (kc of its first chunk a multiple of G,
+      // and of 4 when G = 4): one row and one LDS-or-overflow choice per group,
+      // rows and columns advanced by adding GS's and the block length's quotient
+      // and remainder by in_features.
       constexpr int G = L % 2 == 1 ? 2 : 4, GS = L % 2 == 1 ? 8192 : 2048, NG = 8 / G;
       const int q_g = GS / in_f, m_g = GS - q_g * in_f;
       const int q_b = kB / in_f, m_b = kB - q_b * in_f;
@@ -400,10 +402,11 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       r0 += (r0 + 1) * in_f <= rel0;
       const int col0 = rel0 - r0 * in_f;
 #pragma unroll
-      for (int kbi = 0; kbi < 3; ++kbi) {
-        // the staged first block last, so its reloads arrive while the other two
-        // blocks' chunks go out
-        const int kb = (kbi + 1) % 3;
+      for (int kbi = 0; kbi < KB; ++kbi) {
+        // three-block tiles scatter the staged first block last, so its reloads
+        // arrive while the other two blocks' chunks go out
+        const int kb = KB == 3 ? (kbi + 1) % 3 : kbi;
+        if (KB == 2 && kRowTiles && kb > 0 && !two) break;  // uniform: no second block
         int r = r0 + kb * q_b, col = col0 + kb * m_b;
         if (kb == 2 && col >= 2 * in_f) { col -= in_f; ++r; }
         if (col >= in_f) { col -= in_f; ++r; }
@@ -417,7 +420,7 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
           const int rel = rel0 + kb * kB + g * GS;
           if (rel >= rel_lo && rel < rel_hi) {
             const int kc = col >> 3;
-            if (kc < 4 * lds_steps) {
+            if (KB != 3 || kc < 4 * lds_steps) {
               // odd chunks of a group: table_row's permuted row, one k chunk on
               const int s0 = kc * pitch + r + (kc >> 2), s1 = s0 + pitch + table_row(1, r, pitch) - r;
 #pragma unroll
@@ -431,7 +434,7 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
           }
         }
       }
-    } else {
+    } else if constexpr (KB != 3) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         if (KB == 2 && kRowTiles && kb > 0 && !two) break;  // uniform: no second block
