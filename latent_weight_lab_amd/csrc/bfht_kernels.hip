@@ -82,7 +82,7 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_block_bwd(const T* __restric
 // loads in flight and leaves most of the chip idle for latent lengths of a
 // few 10^4.)
 constexpr int kRedWaves = 8;
-constexpr int kRedDepth = 16;
+constexpr int kRedDepth = 16;  // row loads in flight per wave (32 when a wave has more than 16 rows)
 
 template <int kVec>
 struct RedVec;
@@ -96,9 +96,9 @@ struct RedVec<4> { typedef float4 type; };
 // Columns c0 .. c0 + kVec - 1 of the sum (kVec-wide loads when the row stride
 // allows); every thread of the workgroup calls it, and wave 0 returns true with
 // the totals.  Wave w adds rows w, w + 8, w + 16, ... in ascending order with
-// kRedDepth row loads in flight (rows past the end are loaded from row 0 and
+// kDepth row loads in flight (rows past the end are loaded from row 0 and
 // not added, so the loads need no branch), and wave 0 adds the 8 wave sums in
-// wave order: the result does not depend on kVec or on timing.
+// wave order: the result does not depend on kVec, kDepth or timing.
 // kVec partial-row elements of type P, loaded together and widened to float
 template <class P, int kVec>
 struct PartVec;
@@ -131,7 +131,7 @@ __device__ __forceinline__ V load_once(const V* p) {
   else return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const w4*>(p)));
 }
 
-template <int kVec, class P = float>
+template <int kVec, class P = float, int kDepth = kRedDepth>
 __device__ __forceinline__ bool reduce_columns(const P* __restrict__ part, int64_t nblocks, int64_t stride,
                                                int n, int c0, float (&sums)[kRedWaves][kVec][64],
                                                float (&t)[kVec]) {
@@ -143,15 +143,18 @@ __device__ __forceinline__ bool reduce_columns(const P* __restrict__ part, int64
   auto lanes = [](const V& v, int e) -> float { return PartVec<P, kVec>::at(v, e); };
   if (c0 + kVec <= n) {
     // every column of the lane is in range: vector loads
-    for (int64_t b0 = wave; b0 < nblocks; b0 += (int64_t)kRedWaves * kRedDepth) {
-      V v[kRedDepth];
+    for (int64_t b0 = wave; b0 < nblocks; b0 += (int64_t)kRedWaves * kDepth) {
+      V v[kDepth];
 #pragma unroll
-      for (int j = 0; j < kRedDepth; ++j) {
+      for (int j = 0; j < kDepth; ++j) {
         const int64_t b = b0 + (int64_t)kRedWaves * j;
         v[j] = load_once(reinterpret_cast<const V*>(part + (b < nblocks ? b : 0) * stride + c0));
       }
+      // every load issued before the first add: left to itself the compiler
+      // issues them in batches of eight and waits out each batch
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < kRedDepth; ++j) {
+      for (int j = 0; j < kDepth; ++j) {
         const bool ok = b0 + (int64_t)kRedWaves * j < nblocks;
 #pragma unroll
         for (int e = 0; e < kVec; ++e) a[e] = ok ? a[e] + lanes(v[j], e) : a[e];
@@ -189,14 +192,14 @@ __device__ __forceinline__ bool reduce_columns(const P* __restrict__ part, int64
   return true;
 }
 
-template <class T, int kVec, class P = float>
+template <class T, int kVec, class P = float, int kDepth = kRedDepth>
 __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_blocks(const P* __restrict__ part,
                                                                      int64_t nblocks, int64_t stride, int n,
                                                                      T* __restrict__ grad_latent) {
   __shared__ float sums[kRedWaves][kVec][64];
   const int c0 = (blockIdx.x * 64 + (threadIdx.x & 63)) * kVec;
   float t[kVec];
-  if (!reduce_columns<kVec, P>(part, nblocks, stride, n, c0, sums, t)) return;
+  if (!reduce_columns<kVec, P, kDepth>(part, nblocks, stride, n, c0, sums, t)) return;
 #pragma unroll
   for (int e = 0; e < kVec; ++e)
     if (c0 + e < n) grad_latent[c0 + e] = from_f32<T>(t[e]);
@@ -277,7 +280,13 @@ static void launch_reduce_vec(const P* part, int64_t nblocks, int64_t stride, in
     return;
   }
   const dim3 grid((unsigned)((n + 64 * kVec - 1) / (64 * kVec))), block(64 * kRedWaves);
-  hipLaunchKernelGGL((bfht_reduce_blocks<T, kVec, P>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
+  // More than 16 rows per wave (config 2: 256 rows, 32 per wave): all of a
+  // wave's row loads in one round instead of two memory round trips.
+  if (nblocks > (int64_t)kRedWaves * kRedDepth)
+    hipLaunchKernelGGL((bfht_reduce_blocks<T, kVec, P, 2 * kRedDepth>), grid, block, 0, s, part, nblocks, stride,
+                       (int)n, dst);
+  else
+    hipLaunchKernelGGL((bfht_reduce_blocks<T, kVec, P>), grid, block, 0, s, part, nblocks, stride, (int)n, dst);
 }
 
 template <class T, class P = float>
