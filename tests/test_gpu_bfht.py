@@ -113,6 +113,10 @@ CASES = [
     (16384, 50000, 3, 2, 0, 50000),          # B = 2^14
     (20000, 65536, 1, 123, 111, 4096),       # reference global-backend test shape (B = 2^15)
     (32768, 200_000, 3, 7, 12345, 198_765),  # B = 2^15, config-2 block size
+    # more than 128 blocks: the block sum keeps 32 row loads per wave in flight, rows split
+    # unevenly over its 8 waves
+    (7, 1500, 2, 21, 0, 1500),               # B = 8, 188 blocks
+    (32768, 150 * 32768 + 1000, 3, 13, 0, 150 * 32768 + 1000),  # B = 2^15, 151 blocks (last partial)
     (40000, 200_000, 2, 3, 1000, 150_000),   # B = 2^16: tile passes
     ((1 << 17) - 5, 300_000, 3, -9, 70_000, 299_999),
 ]
