@@ -250,9 +250,9 @@ __global__ __launch_bounds__(256) void bfht_reduce_few(const P* __restrict__ par
 // the destination in T when the job accumulates.  Rows are 128-byte aligned
 // (the planner rounds the stride up to 32 floats), so loads are 16 bytes wide.
 template <class T>
-__device__ __forceinline__ void grad_store(T* dst, int i, float sum, float scale, int accumulate) {
+__device__ __forceinline__ void grad_store(T* dst, int i, float sum, float scale, int accumulate, float prev) {
   float r = round_to<T>(round_to<T>(sum) * scale);
-  if (accumulate) r = to_f32(dst[i]) + r;
+  if (accumulate) r = prev + r;  // prev: dst[i] as float
   dst[i] = from_f32<T>(r);
 }
 
@@ -267,9 +267,16 @@ __global__ __launch_bounds__(64 * kRedWaves) void bfht_reduce_grouped(const Grou
   float t[4];
   if (!reduce_columns<4, P>(static_cast<const P*>(jb.part), jb.nblocks, jb.stride, n, c0, sums, t)) return;
   T* dst = static_cast<T*>(jb.dst);
+  // an accumulating job reads its four destination values together first
+  // (each read behind its own column check was waited out on its own)
+  float prev[4] = {0.f, 0.f, 0.f, 0.f};
+  if (jb.accumulate) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) prev[e] = c0 + e < n ? to_f32(dst[c0 + e]) : 0.f;
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e)
-    if (c0 + e < n) grad_store<T>(dst, c0 + e, t[e], jb.scale, jb.accumulate);
+    if (c0 + e < n) grad_store<T>(dst, c0 + e, t[e], jb.scale, jb.accumulate, prev[e]);
 }
 
 template <class T, int kVec, class P>

@@ -629,16 +629,21 @@ __device__ __forceinline__ void linear_item(const __bf16* __restrict__ x, const 
       // The epilogue's inputs of the whole token tile are loaded before its
       // first store: a load issued after a store that may alias it waits for
       // that store, which would serialize one memory round trip per element.
+      // No load sits behind a branch on its term (a branched load is waited
+      // for on its own): an absent term's buffer is empty and reads 0.  With
+      // five or six row tiles the base values all in flight would spill, so
+      // there base and bias keep their branches.
       float xs[4] = {0.f, 0.f, 0.f, 0.f}, base_v[NT][4], bias_v[NT];
       if constexpr (kEpi) {
+        constexpr bool kFlat = NT <= 4;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (has_xs) xs[r] = cx * __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xs_r, (4 * kq + r) * 4, 0, 0));
+          xs[r] = cx * __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xs_r, (4 * kq + r) * 4, 0, 0));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          bias_v[nt] = has_bias ? bf16_at(bias_r, (o_first + 16 * nt + l16) * 2) : 0.f;
+          bias_v[nt] = (kFlat || has_bias) ? bf16_at(bias_r, (o_first + 16 * nt + l16) * 2) : 0.f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) base_v[nt][r] = has_base ? bf16_at(b_r, out_off(nt, r)) : 0.f;
+          for (int r = 0; r < 4; ++r) base_v[nt][r] = (kFlat || has_base) ? bf16_at(b_r, out_off(nt, r)) : 0.f;
         }
       }
 #pragma unroll
