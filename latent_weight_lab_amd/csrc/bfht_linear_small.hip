@@ -182,19 +182,31 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small(const T* __rest
         for (int u = 0; u < NU; ++u) acc[h][u] += sh[h][u];
     }
     if (j == 0) {
+      // The epilogue's inputs first, none behind a branch on its term or
+      // behind a store that may alias it (either would be waited out on its
+      // own): an absent term's buffer is empty and reads 0, and so does index
+      // -1 (rows from `rows` on, tokens past the batch), whose store is dropped.
+      float xs[NU], bias_o[NR], base_v[NR][NU];
+#pragma unroll
+      for (int u = 0; u < NU; ++u) xs[u] = cx * buf_load<float>(xs_r, t0 + u < tokens ? t0 + u : -1);
+#pragma unroll
+      for (int h = 0; h < NR; ++h) {
+        const int rh = r + h * rstride, o = row0 + rh;
+        bias_o[h] = buf_load<T>(bias_r, rh < rows ? o : -1);
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          base_v[h][u] = buf_load<T>(b_r, rh < rows && t0 + u < tokens ? (t0 + u) * out_f + o : -1);
+      }
 #pragma unroll
       for (int h = 0; h < NR; ++h) {
         const int rh = r + h * rstride;
         if (rh >= rows) continue;  // uniform across the team
         const int o = row0 + rh;
-        const float bias_o = has_bias ? buf_load<T>(bias_r, o) : 0.f;
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
           const int t = t0 + u;
-          const int i = t < tokens ? t * out_f + o : -1;  // -1: loads read 0, the store is dropped
-          const float xs = has_xs ? cx * buf_load<float>(xs_r, t < tokens ? t : -1) : 0.f;
-          const float base_v = has_base ? buf_load<T>(b_r, i) : 0.f;
-          buf_store<T>(linear_epilogue(acc[h][u], has_xs, xs, has_base, base_v, has_bias, bias_o), o_r, i);
+          const int i = t < tokens ? t * out_f + o : -1;  // -1: the store is dropped
+          buf_store<T>(linear_epilogue(acc[h][u], has_xs, xs[u], has_base, base_v[h][u], has_bias, bias_o[h]), o_r, i);
         }
       }
     }

@@ -249,15 +249,17 @@ __global__ __launch_bounds__(Geo<LB>::WG) void bfht_linear_small_mm(const T* __r
       return (ttb + g < tt1 && t < tokens && rr < rows) ? t * out_f + row0 + rr : -1;
     };
 #pragma unroll
-    for (int j = 0; j < kMmRows; ++j) bias_v[j] = has_bias ? buf_load<T>(bias_r, row0 + 16 * (rtb + j) + l16) : 0.f;
+    // (no load behind a branch on its term, which would be waited out on its
+    // own: an absent term's buffer is empty and reads 0)
+    for (int j = 0; j < kMmRows; ++j) bias_v[j] = buf_load<T>(bias_r, row0 + 16 * (rtb + j) + l16);
 #pragma unroll
     for (int g = 0; g < kMmTok; ++g)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = (ttb + g) * 16 + 4 * kq + r;
-        xs[g][r] = has_xs ? cx * buf_load<float>(xs_r, t < tokens ? t : -1) : 0.f;
+        xs[g][r] = cx * buf_load<float>(xs_r, t < tokens ? t : -1);
 #pragma unroll
-        for (int j = 0; j < kMmRows; ++j) base_v[g][j][r] = has_base ? buf_load<T>(b_r, elem(g, j, r)) : 0.f;
+        for (int j = 0; j < kMmRows; ++j) base_v[g][j][r] = buf_load<T>(b_r, elem(g, j, r));
       }
 #pragma unroll
     for (int g = 0; g < kMmTok; ++g)
