@@ -33,7 +33,9 @@ TOL = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1e-2}
 CASES = [
     # (dtype, tokens, in, out, latent, layers, seed, scale)
     (torch.bfloat16, 64, 768, 3072, 32768, 3, 3, 1.0),     # matrix cores, untiled, straddling rows
-    (torch.bfloat16, 4096, 768, 3072, 32768, 3, 3, 1.0),   # tiled x, two blocks per workgroup (NT 6)
+    (torch.bfloat16, 4096, 768, 3072, 32768, 3, 3, 1.0),   # tiled x, 64-row tiles (NT 4)
+    (torch.bfloat16, 320, 704, 64, 32768, 3, 37, 1.0),     # two blocks, 6 row tiles: base and bias loads branched
+    (torch.bfloat16, 300, 1000, 77, 30000, 2, 8, 1.0),     # two blocks, 5 row tiles, rows straddle blocks
     (torch.bfloat16, 300, 3072, 768, 32768, 3, 4, 0.5),    # tiled, 3072 -> 768
     (torch.bfloat16, 3100, 3072, 700, 32768, 3, 4, 0.5),   # three-block tiles, last tile 28 rows
     (torch.bfloat16, 17, 528, 200, 30000, 2, 5, 2.0),      # ragged tokens, one partial block
